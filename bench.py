@@ -1,0 +1,209 @@
+"""Benchmark of split-K paged decode attention on one MI355X.
+
+Workload (default): BASELINE config 2, the Qwen2.5-7B decode shape — batch 64,
+28 query / 4 KV heads, head_dim 128, fp16 K/V in a paged arena (page 16),
+context lengths U[512, 8192], randomly permuted pages. One step = one call of
+the hot path (one layer's decode attention for the whole batch) with inputs
+resident in HBM.
+
+Timing: W warmup calls, then K timed calls, each bracketed by HIP events on
+the stream the kernel runs on. Between timed calls a 1 GiB buffer is written
+so the 256 MB Infinity Cache and the L2s hold none of the arena (flushed =
+HBM numbers); a second pass without the flush is reported as "warm".
+value = algorithmic K/V bytes / median call time (GB/s). The CPU baseline is
+the oracle's threaded C++ restatement of the reference's split-K algorithm,
+timed on a bounded sample of the same workload on this host's cores.
+
+Prints ONE JSON line. Only --gpus 1 is supported (a one-GPU build).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "llm-inference_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
+METRIC = "decode-attention effective K/V GB/s (% of HBM peak) + µs/layer-step"
+TRAFFIC_FILE = ROOT / "profiles" / "traffic_config2.json"
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
+    ap.add_argument("--split-pages", type=int, default=0)
+    ap.add_argument("--no-flush", action="store_true", help="skip the flushed pass")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="approximate CPU time budget of the CPU-baseline sample")
+    ap.add_argument("--no-cpu", action="store_true")
+    return ap.parse_args()
+
+
+def time_calls(call, steps, flush=None):
+    import torch
+
+    stream = torch.cuda.current_stream()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        if flush is not None:
+            flush()
+        starts[i].record(stream)
+        call()
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    return ms, wall
+
+
+def cpu_baseline(w, budget_s):
+    """Oracle's C++ split-K restatement on a sample of sequences of the same
+    workload, all host cores; returns the dict for the JSON line."""
+    import numpy as np
+
+    from oracle import cpu_oracle
+
+    cores = cpu_oracle.host_cores()
+    q, k, v, t, n = w.numpy()
+    spans = w.spans()
+    per_seq = spans * w.kv_heads * w.head_dim * 4  # K+V bytes per sequence
+    # Calibrate on one sequence, then size the sample to the budget.
+    def run(idx):
+        t0 = time.perf_counter()
+        cpu_oracle.decode_splitk(q[idx], k, v, t[idx], n[idx], page_size=w.page_size,
+                                 scale=w.scale, window=w.window, softcap=w.softcap,
+                                 threads=cores)
+        return time.perf_counter() - t0
+
+    first = np.arange(min(4, w.batch))
+    dt = run(first)
+    rate = per_seq[first].sum() / max(dt, 1e-9)
+    target_bytes = rate * max(budget_s, 0.5) / 2
+    count = int(np.searchsorted(np.cumsum(per_seq), target_bytes)) + 1
+    count = max(1, min(w.batch, count))
+    idx = np.arange(count)
+    reps, total_t, total_b = 0, 0.0, 0
+    while total_t < budget_s / 2 or reps < 1:
+        total_t += run(idx)
+        total_b += int(per_seq[idx].sum())
+        reps += 1
+    return {
+        "value": round(total_b / total_t / 1e9, 3),
+        "unit": "GB/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": (f"first {count} of {w.batch} sequences of {w.name} "
+                   f"({int(per_seq[idx].sum())} K/V bytes) x {reps} calls; C++ float32 "
+                   "restatement of the reference split-K kernel (metal_kernels.py:18-124), "
+                   "std::thread over (sequence, kv head, split)"),
+        "seconds": round(total_t, 2),
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build runs on one GPU only (--gpus 1); "
+              "multi-GPU sharding is a design note, not a measured path.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from instinct_amd import _lib, workloads
+    from instinct_amd.hip_kernels import paged_decode_attention
+
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    w = workloads.CONFIGS[args.config](device=device)
+    kv_bytes = w.kv_bytes()
+    out = torch.empty_like(w.q)
+
+    def call():
+        paged_decode_attention(w.q, w.keys, w.values, w.tables, w.lengths,
+                               page_size=w.page_size, longest=w.longest, scale=w.scale,
+                               window=w.window, softcap=w.softcap,
+                               split_pages=args.split_pages, out=out)
+
+    for _ in range(args.warmup):
+        call()
+    torch.cuda.synchronize()
+    flush_buf = torch.empty(1 << 30, dtype=torch.uint8, device=device)
+
+    def flush():
+        flush_buf.fill_(1)
+
+    ms_flush, wall = (None, None) if args.no_flush else time_calls(call, args.steps, flush)
+    ms_warm, _ = time_calls(call, args.steps)
+    ms = ms_flush if ms_flush is not None else ms_warm
+    med = statistics.median(ms)
+    mean = statistics.fmean(ms)
+    value = kv_bytes / (med * 1e-3) / 1e9
+    achieved = kv_bytes / (mean * 1e-3) / 1e9
+    pages, splits = _lib.plan(w.batch, w.q_heads, w.kv_heads, w.head_dim, w.page_size,
+                              int(w.tables.shape[1]), w.longest, w.window, args.split_pages)
+    traffic = None
+    if TRAFFIC_FILE.exists() and args.config == 2:
+        traffic = json.loads(TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(med, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seeded N(0,1) K/V/Q, random page permutation)",
+        "config": {
+            "workload": w.name,
+            "batch": w.batch, "q_heads": w.q_heads, "kv_heads": w.kv_heads,
+            "head_dim": w.head_dim, "page_size": w.page_size, "window": w.window,
+            "longest": w.longest, "kv_bytes": kv_bytes,
+            "split_pages": pages, "max_splits": splits,
+            "cache": "flushed (1 GiB write between calls)" if ms_flush else "warm",
+        },
+        "us_per_layer_step": round(med * 1e3, 2),
+        "steps_per_s": round(1e3 / med, 1),
+        "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "warm": {"us_median": round(statistics.median(ms_warm) * 1e3, 2),
+                 "GB_per_s": round(kv_bytes / (statistics.median(ms_warm) * 1e-3) / 1e9, 2)},
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "kernel": "paged_decode_kernel<128,7> (split + fused merge, one launch)",
+            "us_mean": round(mean * 1e3, 2),
+        },
+    }
+    if w.meta.get("sharers") is not None:
+        line["config"]["unique_kv_bytes"] = w.unique_kv_bytes()
+    if wall is not None:
+        line["wall_s_timed_loop"] = round(wall, 3)
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

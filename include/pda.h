@@ -1,0 +1,118 @@
+/*
+ * pda.h — split-K paged decode attention for AMD Instinct MI355X (gfx950).
+ *
+ * C-ABI of libpda.so. Plain pointers and sizes only; every device pointer is
+ * a HIP device address, `stream` is a hipStream_t (NULL = the null stream).
+ * The library allocates no device memory on the call path: the caller owns
+ * the queries, the K/V arenas, the page tables, the output and the workspace.
+ *
+ * Reference interface replaced (KavinP21/LLM-Inference, "Instinct"):
+ *   paged_decode_attention(mx, queries, keys, values, tables, lengths, *,
+ *                          page_size, longest, scale, window=0, softcap=0.0)
+ *   python/instinct/backends/metal_kernels.py:164-248, called once per
+ *   attention layer per decode step from DecodeBatch.attend
+ *   (python/instinct/batches.py:203-226).
+ *
+ * Layouts (identical to the reference's KVCache, paged_kv.py:156-292):
+ *   queries  [batch, q_heads, head_dim]            fp16
+ *   keys     [arena_rows, kv_heads, head_dim]      fp16, one layer's arena
+ *   values   [arena_rows, kv_heads, head_dim]      fp16
+ *   tables   [batch, table_stride]                 int32, physical page ids;
+ *            row of logical position t = tables[b][t / page_size] * page_size
+ *            + t % page_size (paged_kv.py:259-265, metal_kernels.py:47)
+ *   lengths  [batch]                               int32, keys per sequence,
+ *            the new token included (batches.py:162-164)
+ *   out      [batch, q_heads, head_dim]            fp16
+ *
+ * Visible keys of sequence b are positions [first, lengths[b]) with
+ * first = max(0, lengths[b] - window) when window > 0, else 0
+ * (metal_kernels.py:32-36, portable.py:194-205). A page id that is negative
+ * (a page released by the sliding-window trim, mlx_engine.py:349-372) or not
+ * below arena_rows / page_size masks the keys it would hold, as the portable
+ * path masks released pages (portable.py:202-204). Table entries beyond the
+ * visible range are never read. A length above table_stride * page_size is
+ * clamped to it; a length of zero or less yields a zero output row.
+ */
+#ifndef PDA_H
+#define PDA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Return codes. Every entry point validates its arguments on the host before
+ * any HIP call and returns one of these; pda_last_error() then names the
+ * problem. Mirrors the reference's ValueError for a bad head ratio
+ * (metal_kernels.py:189-190). */
+#define PDA_OK 0
+#define PDA_ERR_INVALID_ARGUMENT (-1) /* null pointer, non-positive size, ... */
+#define PDA_ERR_HEAD_RATIO (-2)       /* q_heads is not a multiple of kv_heads */
+#define PDA_ERR_HEAD_DIM (-3)         /* head_dim has no compiled kernel      */
+#define PDA_ERR_PAGE_SIZE (-4)        /* page_size not a multiple of the step */
+#define PDA_ERR_WORKSPACE (-5)        /* workspace missing or too small       */
+#define PDA_ERR_ALIGNMENT (-6)        /* fp16 buffers must be 16-byte aligned */
+#define PDA_ERR_TOO_LONG (-7)         /* context beyond the split planner     */
+#define PDA_ERR_HIP (-8)              /* a HIP runtime call failed            */
+
+/* Library version, (major << 16) | minor. No reference counterpart. */
+int pda_version(void);
+
+/* Thread-local description of the last error returned on this thread
+ * ("" after success). Replaces the reference's exception text
+ * (metal_kernels.py:189-190). */
+const char* pda_last_error(void);
+
+/* Bytes of device workspace pda_paged_decode_attention needs for this shape.
+ * Replaces the per-call allocation of the split partials
+ * (metal_kernels.py:228-239 output_shapes: partial_o [B,HQ,S,D],
+ * partial_m / partial_l [B,HQ,S] in float32). The first
+ * pda_workspace_zero_bytes() bytes of a workspace hold split counters: they
+ * must be zero before the workspace is first used (the kernel leaves them at
+ * zero when it finishes). `longest` and `split_pages` as for the decode call. */
+int pda_workspace_bytes(int32_t batch, int32_t q_heads, int32_t kv_heads,
+                        int32_t head_dim, int32_t page_size,
+                        int32_t table_stride, int32_t longest, int32_t window,
+                        int32_t split_pages, size_t* bytes);
+
+/* Leading bytes of a workspace of this shape that must start at zero. */
+int pda_workspace_zero_bytes(int32_t batch, int32_t q_heads, int32_t kv_heads,
+                             size_t* bytes);
+
+/* The split plan the decode call would use: pages per split and the largest
+ * split count of any sequence. Replaces KEYS_PER_SPLIT / MAX_SPLITS and the
+ * batch-wide split rule (metal_kernels.py:126-127,193-194), which the MI355X
+ * kernel replaces by a per-sequence split of fixed-size page chunks. */
+int pda_plan(int32_t batch, int32_t q_heads, int32_t kv_heads,
+             int32_t head_dim, int32_t page_size, int32_t table_stride,
+             int32_t longest, int32_t window, int32_t split_pages,
+             int32_t* pages_per_split, int32_t* max_splits);
+
+/* Paged decode attention for one new token per sequence.
+ * Replaces paged_decode_attention (metal_kernels.py:164-248): same inputs and
+ * meaning. `scale` multiplies q.k; `softcap` > 0 applies
+ * softcap * tanh(score / softcap) (metal_kernels.py:53); `window` 0 = full
+ * attention. `longest` is the host-side largest length, as in the reference
+ * (a planning hint only: results never depend on it, and lengths above it
+ * stay correct). `split_pages` = 0 lets the planner choose the pages per
+ * split; a positive value forces it (tuning and tests). `arena_rows` is the
+ * row count of the keys/values arenas. Stream-ordered; calls that share a
+ * workspace must not overlap. */
+int pda_paged_decode_attention(const void* queries, const void* keys,
+                               const void* values, const int32_t* tables,
+                               const int32_t* lengths, void* out,
+                               int32_t batch, int32_t q_heads,
+                               int32_t kv_heads, int32_t head_dim,
+                               int32_t page_size, int32_t table_stride,
+                               int64_t arena_rows, int32_t longest,
+                               float scale, int32_t window, float softcap,
+                               int32_t split_pages, void* workspace,
+                               size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PDA_H */

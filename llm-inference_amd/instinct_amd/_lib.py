@@ -1,0 +1,115 @@
+"""ctypes binding of libpda.so (the C-ABI declared in include/pda.h).
+
+The library is built in-tree by ``make -C llm-inference_amd`` (or
+``__graft_entry__.build()``). There is no fallback: if the library is missing
+or does not load, :func:`library` raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import c_float, c_int32, c_int64, c_size_t, c_void_p
+from pathlib import Path
+
+PACKAGE_ROOT = Path(__file__).resolve().parent.parent
+LIBRARY_PATH = PACKAGE_ROOT / "lib" / "libpda.so"
+
+# Return codes (pda.h).
+PDA_OK = 0
+PDA_ERR_INVALID_ARGUMENT = -1
+PDA_ERR_HEAD_RATIO = -2
+PDA_ERR_HEAD_DIM = -3
+PDA_ERR_PAGE_SIZE = -4
+PDA_ERR_WORKSPACE = -5
+PDA_ERR_ALIGNMENT = -6
+PDA_ERR_TOO_LONG = -7
+PDA_ERR_HIP = -8
+
+# Every symbol include/pda.h declares, with its ctypes signature.
+SIGNATURES = {
+    "pda_version": (ctypes.c_int, []),
+    "pda_last_error": (ctypes.c_char_p, []),
+    "pda_workspace_bytes": (
+        ctypes.c_int,
+        [c_int32] * 9 + [ctypes.POINTER(c_size_t)],
+    ),
+    "pda_workspace_zero_bytes": (
+        ctypes.c_int,
+        [c_int32] * 3 + [ctypes.POINTER(c_size_t)],
+    ),
+    "pda_plan": (
+        ctypes.c_int,
+        [c_int32] * 9 + [ctypes.POINTER(c_int32), ctypes.POINTER(c_int32)],
+    ),
+    "pda_paged_decode_attention": (
+        ctypes.c_int,
+        [c_void_p] * 6
+        + [c_int32] * 6
+        + [c_int64, c_int32, c_float, c_int32, c_float, c_int32, c_void_p, c_size_t, c_void_p],
+    ),
+}
+
+_lib: ctypes.CDLL | None = None
+
+
+class PdaError(RuntimeError):
+    """A non-zero return code from libpda, with the library's message."""
+
+    def __init__(self, code: int, message: str) -> None:
+        super().__init__(f"libpda error {code}: {message}")
+        self.code = code
+        self.message = message
+
+
+def library() -> ctypes.CDLL:
+    """Load libpda.so once; raise if it is missing."""
+    global _lib
+    if _lib is None:
+        path = Path(os.environ.get("PDA_LIBRARY", LIBRARY_PATH))
+        if not path.exists():
+            raise FileNotFoundError(
+                f"{path} is not built; run `make -C {PACKAGE_ROOT}` "
+                "or __graft_entry__.build()"
+            )
+        lib = ctypes.CDLL(str(path))
+        for name, (restype, argtypes) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        _lib = lib
+    return _lib
+
+
+def check(code: int) -> None:
+    if code != PDA_OK:
+        message = library().pda_last_error().decode()
+        if code == PDA_ERR_HEAD_RATIO:
+            # The reference raises ValueError here (metal_kernels.py:189-190).
+            raise ValueError(message)
+        raise PdaError(code, message)
+
+
+def workspace_bytes(batch, q_heads, kv_heads, head_dim, page_size, table_stride,
+                    longest, window, split_pages=0) -> int:
+    out = c_size_t(0)
+    check(library().pda_workspace_bytes(batch, q_heads, kv_heads, head_dim, page_size,
+                                        table_stride, longest, window, split_pages,
+                                        ctypes.byref(out)))
+    return out.value
+
+
+def workspace_zero_bytes(batch, q_heads, kv_heads) -> int:
+    out = c_size_t(0)
+    check(library().pda_workspace_zero_bytes(batch, q_heads, kv_heads, ctypes.byref(out)))
+    return out.value
+
+
+def plan(batch, q_heads, kv_heads, head_dim, page_size, table_stride, longest, window,
+         split_pages=0) -> tuple[int, int]:
+    pages = c_int32(0)
+    splits = c_int32(0)
+    check(library().pda_plan(batch, q_heads, kv_heads, head_dim, page_size, table_stride,
+                             longest, window, split_pages, ctypes.byref(pages),
+                             ctypes.byref(splits)))
+    return pages.value, splits.value

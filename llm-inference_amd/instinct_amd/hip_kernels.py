@@ -1,0 +1,105 @@
+"""Paged decode attention on MI355X, behind the reference's operator API.
+
+:func:`paged_decode_attention` keeps the signature and meaning of the
+reference's ``paged_decode_attention`` (python/instinct/backends/
+metal_kernels.py:164-248) with torch tensors on the GPU in place of MLX
+arrays: queries ``[batch, q_heads, head_dim]``, a layer's whole K/V arena
+``[rows, kv_heads, head_dim]``, page tables ``[batch, width]`` int32 and
+lengths ``[batch]`` int32 (the new key included). It returns
+``[batch, q_heads, head_dim]`` in the queries' dtype (fp16).
+
+The work happens in hand-written HIP kernels (libpda.so, see
+``csrc/pda_kernels.hip``) called through the C-ABI of ``include/pda.h``; this
+module only validates, allocates the output and the split workspace, and
+passes device pointers and the current stream.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Any
+
+import torch
+
+from . import _lib
+
+_workspaces: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def workspace(device: torch.device, nbytes: int, zero_bytes: int) -> torch.Tensor:
+    """A cached, 256-byte aligned device workspace of at least ``nbytes``.
+
+    The leading ``zero_bytes`` hold split counters that start at zero and that
+    the kernel returns to zero, so the buffer is zeroed once when created."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    key = (index, 0)
+    buf = _workspaces.get(key)
+    if buf is None or buf.numel() < nbytes:
+        size = max(nbytes, 1 << 20)
+        if buf is not None:
+            size = max(size, 2 * buf.numel())
+        buf = torch.zeros(size, dtype=torch.uint8, device=device)
+        _workspaces[key] = buf
+    del zero_bytes  # the kernel keeps the counters at zero between calls
+    return buf
+
+
+def paged_decode_attention(
+    queries: torch.Tensor,
+    keys: torch.Tensor,
+    values: torch.Tensor,
+    tables: torch.Tensor,
+    lengths: torch.Tensor,
+    *,
+    page_size: int,
+    longest: int,
+    scale: float,
+    window: int = 0,
+    softcap: float = 0.0,
+    scales: tuple[Any, Any] | None = None,
+    split_pages: int = 0,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Attention for one new token per sequence over its paged keys
+    (metal_kernels.py:164-186). ``split_pages`` (0 = planner's choice) forces
+    the pages per split; the result does not depend on it."""
+    if scales is not None:
+        raise NotImplementedError("8-bit K/V (scales) has no MI355X kernel yet")
+    batch, q_heads, head_dim = (int(n) for n in queries.shape)
+    kv_heads = int(keys.shape[1])
+    if q_heads % kv_heads:
+        raise ValueError("query heads must be a multiple of kv heads")
+    for name, t in (("queries", queries), ("keys", keys), ("values", values)):
+        if t.dtype != torch.float16:
+            raise TypeError(f"{name} must be float16, got {t.dtype}")
+        if not t.is_cuda:
+            raise ValueError(f"{name} must be on a GPU")
+        if not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous")
+    if tuple(keys.shape) != tuple(values.shape) or int(keys.shape[2]) != head_dim:
+        raise ValueError("keys and values must both be [rows, kv_heads, head_dim]")
+    if tables.dtype != torch.int32 or lengths.dtype != torch.int32:
+        raise TypeError("tables and lengths must be int32")
+    if tables.dim() != 2 or tables.shape[0] != batch or lengths.shape != (batch,):
+        raise ValueError("tables must be [batch, width] and lengths [batch]")
+    tables = tables.contiguous()
+    lengths = lengths.contiguous()
+    device = queries.device
+    if out is None:
+        out = torch.empty_like(queries)
+    if batch == 0:
+        return out
+    stride = int(tables.shape[1])
+    need = _lib.workspace_bytes(batch, q_heads, kv_heads, head_dim, page_size, stride,
+                                int(longest), int(window), int(split_pages))
+    zero = _lib.workspace_zero_bytes(batch, q_heads, kv_heads)
+    ws = workspace(device, need, zero)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    rc = _lib.library().pda_paged_decode_attention(
+        queries.data_ptr(), keys.data_ptr(), values.data_ptr(), tables.data_ptr(),
+        lengths.data_ptr(), out.data_ptr(), batch, q_heads, kv_heads, head_dim,
+        int(page_size), stride, int(keys.shape[0]), int(longest), float(scale),
+        int(window), float(softcap), int(split_pages), ws.data_ptr(),
+        ws.numel(), ctypes.c_void_p(stream))
+    _lib.check(rc)
+    return out

@@ -1,0 +1,171 @@
+"""Paged K/V storage in MI355X HBM: the arena and page-pool conventions the
+decode kernel reads.
+
+Counterpart of python/instinct/paged_kv.py. Every attention layer keeps its
+keys and values in one arena of token rows, ``[rows, kv_heads, head_dim]``
+fp16 (paged_kv.py:156-235); a page is ``page_size`` consecutive rows and the
+row of logical position t is ``table[t // P] * P + t % P`` (:259-265). The
+arenas live in device memory as torch tensors, sized once for the whole page
+budget: with 288 GB of HBM per MI355X the arena is allocated at its capacity
+rather than grown by doubling (:237-250), so the decode path never
+reallocates.
+"""
+
+from __future__ import annotations
+
+import heapq
+from collections.abc import Iterable, Sequence
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+
+@dataclass(frozen=True)
+class KVGroup:
+    """Attention layers that share a K/V shape and window (paged_kv.py:34-47)."""
+
+    name: str
+    layers: tuple[int, ...]
+    kv_heads: int
+    head_dim: int
+    window: int = 0  # 0 for full attention
+
+    def bytes_per_token(self, bits: int = 16) -> int:
+        row = self.head_dim * bits // 8 + (2 if bits == 8 else 0)
+        return 2 * len(self.layers) * self.kv_heads * row
+
+
+class PagePool:
+    """Physical page ids with reference counts and reservations
+    (paged_kv.py:79-153): the lowest free id is handed out first, so the arena
+    only has to cover the high-water mark; ``retain``/``release`` let several
+    tables hold one page (prefix sharing)."""
+
+    def __init__(self, capacity: int) -> None:
+        if capacity <= 0:
+            raise ValueError("a page pool needs at least one page")
+        self.capacity = capacity
+        self._free = list(range(capacity))
+        self._refs = np.zeros(capacity, dtype=np.int32)
+        self.reserved = 0
+        self.high_water = 0
+
+    @property
+    def free(self) -> int:
+        return len(self._free)
+
+    @property
+    def available(self) -> int:
+        return len(self._free) - self.reserved
+
+    @property
+    def used(self) -> int:
+        return self.capacity - len(self._free)
+
+    def reserve(self, count: int) -> bool:
+        if count > self.available:
+            return False
+        self.reserved += count
+        return True
+
+    def unreserve(self, count: int) -> None:
+        if not 0 <= count <= self.reserved:
+            raise RuntimeError("released more pages than were reserved")
+        self.reserved -= count
+
+    def allocate(self, *, reserved: bool) -> int:
+        """Take one page, from the caller's reservation if ``reserved``."""
+        if reserved:
+            self.unreserve(1)
+        elif self.available <= 0:
+            raise RuntimeError("the K/V page pool is exhausted")
+        page = heapq.heappop(self._free)
+        self._refs[page] = 1
+        self.high_water = max(self.high_water, page + 1)
+        return page
+
+    def retain(self, pages: Iterable[int]) -> None:
+        for page in pages:
+            if page >= 0:
+                if self._refs[page] <= 0:
+                    raise RuntimeError("retained a page that isn't allocated")
+                self._refs[page] += 1
+
+    def release(self, pages: Iterable[int]) -> None:
+        for page in pages:
+            if page < 0:
+                continue
+            if self._refs[page] <= 0:
+                raise RuntimeError("released a page that isn't allocated")
+            self._refs[page] -= 1
+            if self._refs[page] == 0:
+                heapq.heappush(self._free, page)
+
+    def shared(self, page: int) -> bool:
+        return bool(self._refs[page] > 1)
+
+    def held_only_by(self, counts: np.ndarray) -> int:
+        return int(np.count_nonzero((counts > 0) & (self._refs == counts)))
+
+
+class KVCache:
+    """Per-layer fp16 K/V arenas in device memory plus one page pool per
+    group (paged_kv.py:156-292, 16-bit K/V)."""
+
+    def __init__(
+        self,
+        groups: Sequence[KVGroup],
+        *,
+        page_size: int,
+        capacities: dict[str, int],
+        device: torch.device | str = "cuda",
+        dtype: torch.dtype = torch.float16,
+    ) -> None:
+        self.page_size = page_size
+        self.dtype = dtype
+        self.device = torch.device(device)
+        self.groups = {group.name: group for group in groups}
+        self.layer_group = {layer: group for group in groups for layer in group.layers}
+        self.pools = {group.name: PagePool(capacities[group.name]) for group in groups}
+        self.keys: dict[int, torch.Tensor] = {}
+        self.values: dict[int, torch.Tensor] = {}
+        for group in groups:
+            rows = capacities[group.name] * page_size
+            for layer in group.layers:
+                shape = (rows, group.kv_heads, group.head_dim)
+                self.keys[layer] = torch.zeros(shape, dtype=dtype, device=self.device)
+                self.values[layer] = torch.zeros(shape, dtype=dtype, device=self.device)
+
+    @property
+    def device_bytes(self) -> int:
+        return sum(t.numel() * t.element_size()
+                   for store in (self.keys, self.values) for t in store.values())
+
+    def rows(self, table: np.ndarray, start: int, end: int) -> np.ndarray:
+        """Physical rows of logical positions ``[start, end)`` (paged_kv.py:259-265)."""
+        positions = np.arange(start, end, dtype=np.int64)
+        pages = np.asarray(table)[positions // self.page_size]
+        if np.any(pages < 0):
+            raise RuntimeError("K/V range includes a released page")
+        return (pages * self.page_size + positions % self.page_size).astype(np.int32)
+
+    def copy_page(self, group: KVGroup, source: int, target: int, count: int) -> None:
+        """Copy the first ``count`` rows of a page (copy-on-write of a shared
+        tail, paged_kv.py:267-274)."""
+        src = slice(source * self.page_size, source * self.page_size + count)
+        dst = slice(target * self.page_size, target * self.page_size + count)
+        for layer in group.layers:
+            self.keys[layer][dst] = self.keys[layer][src]
+            self.values[layer][dst] = self.values[layer][src]
+
+    def write(self, layer: int, rows: torch.Tensor, keys: torch.Tensor,
+              values: torch.Tensor) -> None:
+        """Scatter new rows into the layer arena in place (paged_kv.py:278-283)."""
+        self.keys[layer].index_copy_(0, rows.long(), keys.to(self.dtype))
+        self.values[layer].index_copy_(0, rows.long(), values.to(self.dtype))
+
+    def gather(self, layer: int, rows: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        """Rows of the arena (paged_kv.py:285-292)."""
+        index = rows.long()
+        return self.keys[layer][index], self.values[layer][index]

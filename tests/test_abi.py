@@ -1,0 +1,104 @@
+"""libpda.so loads, exports every entry point include/pda.h declares, and
+validates its arguments on the host (no GPU call is made by these tests:
+every rejected call returns before touching HIP)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from instinct_amd import _lib
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "pda.h"
+FAKE = 0x10000  # an aligned, never-dereferenced address
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(pda_[a-z_]+)\s*\(", text)))
+
+
+def test_header_declares_the_expected_entry_points():
+    assert declared_functions() == sorted(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.library()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    assert lib.pda_version() >= 1
+
+
+def decode(**overrides):
+    args = dict(queries=FAKE, keys=FAKE, values=FAKE, tables=FAKE, lengths=FAKE, out=FAKE,
+                batch=4, q_heads=28, kv_heads=4, head_dim=128, page_size=16,
+                table_stride=64, arena_rows=4096, longest=1000, scale=0.088, window=0,
+                softcap=0.0, split_pages=0, workspace=FAKE * 16, workspace_bytes=1 << 30,
+                stream=None)
+    args.update(overrides)
+    lib = _lib.library()
+    return lib.pda_paged_decode_attention(*args.values())
+
+
+@pytest.mark.parametrize("overrides, code", [
+    (dict(q_heads=30), _lib.PDA_ERR_HEAD_RATIO),
+    (dict(head_dim=72), _lib.PDA_ERR_HEAD_DIM),
+    (dict(head_dim=4, q_heads=2, kv_heads=1), _lib.PDA_ERR_HEAD_DIM),
+    (dict(page_size=12), _lib.PDA_ERR_PAGE_SIZE),
+    (dict(page_size=4), _lib.PDA_ERR_PAGE_SIZE),
+    (dict(head_dim=256, page_size=2), _lib.PDA_ERR_PAGE_SIZE),
+    (dict(kv_heads=0), _lib.PDA_ERR_INVALID_ARGUMENT),
+    (dict(batch=-1), _lib.PDA_ERR_INVALID_ARGUMENT),
+    (dict(window=-1), _lib.PDA_ERR_INVALID_ARGUMENT),
+    (dict(queries=None), _lib.PDA_ERR_INVALID_ARGUMENT),
+    (dict(tables=None), _lib.PDA_ERR_INVALID_ARGUMENT),
+    (dict(arena_rows=8), _lib.PDA_ERR_INVALID_ARGUMENT),
+    (dict(scale=float("nan")), _lib.PDA_ERR_INVALID_ARGUMENT),
+    (dict(softcap=-1.0), _lib.PDA_ERR_INVALID_ARGUMENT),
+    (dict(split_pages=65), _lib.PDA_ERR_INVALID_ARGUMENT),
+    (dict(keys=FAKE + 2), _lib.PDA_ERR_ALIGNMENT),
+    (dict(out=FAKE + 8), _lib.PDA_ERR_ALIGNMENT),
+    (dict(lengths=FAKE + 2), _lib.PDA_ERR_ALIGNMENT),
+    (dict(workspace=None), _lib.PDA_ERR_WORKSPACE),
+    (dict(workspace_bytes=16), _lib.PDA_ERR_WORKSPACE),
+    (dict(workspace=FAKE + 64), _lib.PDA_ERR_ALIGNMENT),
+    (dict(table_stride=1 << 28), _lib.PDA_ERR_TOO_LONG),
+])
+def test_host_validation_rejects_bad_arguments(overrides, code):
+    assert decode(**overrides) == code
+    assert _lib.library().pda_last_error().decode() != ""
+
+
+def test_bad_head_ratio_raises_value_error_like_the_reference():
+    with pytest.raises(ValueError, match="multiple of kv heads"):
+        _lib.check(decode(q_heads=30))
+
+
+def test_empty_batch_is_a_no_op():
+    assert decode(batch=0, workspace=None, workspace_bytes=0) == _lib.PDA_OK
+    assert _lib.library().pda_last_error().decode() == ""
+
+
+def test_workspace_and_plan_are_consistent():
+    pages, splits = _lib.plan(64, 28, 4, 128, 16, 512, 8192, 0)
+    assert 4 <= pages <= 64 and splits == -(-512 // pages)
+    need = _lib.workspace_bytes(64, 28, 4, 128, 16, 512, 8192, 0)
+    zero = _lib.workspace_zero_bytes(64, 28, 4)
+    assert zero == 256 * -(-64 * 4 * 4 // 256)  # one uint32 per (seq, kv head)
+    units = 64 * 4
+    assert need >= zero + units * splits * 7 * (128 + 2) * 4
+    # A forced split size changes the plan but never below the data it needs.
+    assert _lib.plan(64, 28, 4, 128, 16, 512, 8192, 0, split_pages=8) == (8, 64)
+    # A window bounds the visible pages whatever the table width.
+    assert _lib.plan(32, 8, 4, 256, 16, 2048, 32768, 1024, split_pages=16) == (16, 5)
+    # More than 8 heads per kv head are served by several head groups.
+    assert _lib.workspace_zero_bytes(2, 16, 1) == 256
+    # One split needs no partials.
+    assert _lib.workspace_bytes(2, 8, 8, 64, 16, 4, 64, 0, split_pages=4) == 256
+
+
+def test_split_count_limit():
+    with pytest.raises(_lib.PdaError) as err:
+        _lib.plan(1, 8, 8, 128, 16, 1 << 20, 1 << 24, 0, split_pages=16)
+    assert err.value.code == _lib.PDA_ERR_TOO_LONG

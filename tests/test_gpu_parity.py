@@ -1,0 +1,271 @@
+"""Parity of the MI355X kernel (libpda.so via the C-ABI) with the float64
+oracle on the same seeded inputs.
+
+Bar: max-abs error <= 2e-3 and mean-abs error <= 2e-4
+for the fp16 output against a float64-accumulated result. The oracle is the
+threaded C++ restatement of the reference's portable path
+(oracle/cpu_attention.cpp), itself pinned by tests/test_oracle.py.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from instinct_amd import workloads
+from instinct_amd.hip_kernels import paged_decode_attention
+from oracle import cpu_oracle
+from oracle import paged_attention as pa
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS = 2e-3
+MEAN_ABS = 2e-4
+
+
+def run(w, split_pages=0, longest=None):
+    out = paged_decode_attention(
+        w.q, w.keys, w.values, w.tables, w.lengths, page_size=w.page_size,
+        longest=w.longest if longest is None else longest, scale=w.scale,
+        window=w.window, softcap=w.softcap, split_pages=split_pages)
+    torch.cuda.synchronize()
+    return out
+
+
+def oracle(w):
+    q, k, v, t, n = w.numpy()
+    return cpu_oracle.decode_f64(q, k, v, t, n, page_size=w.page_size, scale=w.scale,
+                                 window=w.window, softcap=w.softcap)
+
+
+def assert_parity(got, expected, what=""):
+    got = got.float().cpu().numpy() if isinstance(got, torch.Tensor) else got
+    assert np.isfinite(got).all(), f"{what}: non-finite output"
+    err_max, err_mean = pa.error_stats(got, expected)
+    print(f"{what}: max_abs={err_max:.3e} mean_abs={err_mean:.3e}", flush=True)
+    assert err_max <= MAX_ABS and err_mean <= MEAN_ABS, (what, err_max, err_mean)
+
+
+def test_closed_form_from_cuda_tests_at_kernel_page_size(gpu):
+    """tests/cuda_tests.cu:207-262 generalised to page 16 and head_dim 64: key
+    (1,0,..) at position 0, (0,1,..) at 1..15 (physical page 1), (1,1,..) at 16
+    (physical page 0); values (1,2,3,4,..), (5,6,7,8,..), (2,4,6,8,..)."""
+    D, P = 64, 16
+    keys = torch.zeros((2 * P, 1, D), dtype=torch.float16)
+    values = torch.zeros((2 * P, 1, D), dtype=torch.float16)
+    k0, k1, k2 = [1, 0, 0, 0], [0, 1, 0, 0], [1, 1, 0, 0]
+    v0, v1, v2 = [1, 2, 3, 4], [5, 6, 7, 8], [2, 4, 6, 8]
+    keys[P + 0, 0, :4] = torch.tensor(k0)
+    values[P + 0, 0, :4] = torch.tensor(v0)
+    for t in range(1, P):
+        keys[P + t, 0, :4] = torch.tensor(k1)
+        values[P + t, 0, :4] = torch.tensor(v1)
+    keys[0, 0, :4] = torch.tensor(k2)
+    values[0, 0, :4] = torch.tensor(v2)
+    q = torch.zeros((1, 2, D), dtype=torch.float16)
+    q[0, :, :2] = 1.0
+    tables = torch.tensor([[1, 0]], dtype=torch.int32)
+    lengths = torch.tensor([17], dtype=torch.int32)
+    out = paged_decode_attention(q.to(gpu), keys.to(gpu), values.to(gpu), tables.to(gpu),
+                                 lengths.to(gpu), page_size=P, longest=17, scale=0.5)
+    e5, e1 = math.exp(0.5), math.exp(1.0)
+    expected = (e5 * np.array(v0) + 15 * e5 * np.array(v1) + e1 * np.array(v2)) / (16 * e5 + e1)
+    got = out.float().cpu().numpy()
+    for h in range(2):
+        np.testing.assert_allclose(got[0, h, :4], expected, atol=MAX_ABS)
+        assert not got[0, h, 4:].any()
+
+
+SMALL = {
+    1: dict(batch=4, length=1024),
+    2: dict(batch=8, low=512, high=2048),
+    3: dict(batch=1, length=8192),
+    4: dict(batch=6, low=2000, high=5000),
+    5: dict(batch=24, low=16, high=8192, shared=6, prefix=1024),
+}
+
+
+@pytest.mark.parametrize("config", [1, 2, 3, 4, 5])
+def test_configs_reduced(gpu, config):
+    w = workloads.CONFIGS[config](device=gpu, **SMALL[config])
+    assert_parity(run(w), oracle(w), f"config{config}-reduced")
+
+
+@pytest.mark.parametrize("config", [1, 2, 4])
+def test_configs_full_size(gpu, config):
+    w = workloads.CONFIGS[config](device=gpu)
+    assert_parity(run(w), oracle(w), f"config{config}-full")
+
+
+@pytest.mark.parametrize("batch, length", [(1, 32768), (2, 131072)])
+def test_config3_long_context_full_size(gpu, batch, length):
+    w = workloads.config3(device=gpu, batch=batch, length=length)
+    assert_parity(run(w), oracle(w), f"config3-b{batch}-{length}")
+
+
+def test_config5_full_size(gpu):
+    w = workloads.config5(device=gpu)
+    expected = oracle(w)
+    got = run(w)
+    assert_parity(got, expected, "config5-full")
+    assert w.unique_kv_bytes() < w.kv_bytes()
+
+
+def test_split_size_does_not_change_the_result(gpu):
+    """The output is independent of the split plan (fp32 rounding aside)."""
+    w = workloads.config2(device=gpu)
+    expected = oracle(w)
+    outs = []
+    for split_pages in (4, 9, 16, 64):
+        out = run(w, split_pages=split_pages)
+        assert_parity(out, expected, f"config2 split_pages={split_pages}")
+        outs.append(out.float())
+    for other in outs[1:]:
+        assert (other - outs[0]).abs().max().item() <= 2e-3
+
+
+def test_longest_hint_understated_stays_correct(gpu):
+    w = workloads.config2(device=gpu, batch=8, low=512, high=4096)
+    assert_parity(run(w, longest=16), oracle(w), "longest=16")
+
+
+@pytest.mark.parametrize("shape", [s for s in workloads.REFERENCE_TEST_SHAPES if s[2] != 4])
+def test_reference_kernel_test_shapes(gpu, shape):
+    """The five shapes of test_mlx_engine.py:422-431 (16-bit), except head_dim
+    4, which has no MI355X kernel (the C-ABI rejects it)."""
+    w = workloads.reference_test_case(*shape, device=gpu)
+    assert_parity(run(w), oracle(w), f"reftest{shape[:3]}")
+
+
+@pytest.mark.parametrize("q_heads, kv_heads, head_dim, page", [
+    (8, 8, 64, 16), (14, 2, 64, 16), (16, 2, 64, 32), (12, 4, 80, 16), (24, 4, 96, 64),
+    (32, 4, 128, 16), (16, 1, 128, 16), (24, 2, 128, 16), (11, 1, 128, 16),
+    (10, 2, 256, 16), (8, 1, 512, 16),
+])
+def test_head_shapes_and_page_sizes(gpu, q_heads, kv_heads, head_dim, page):
+    rng = np.random.default_rng(q_heads * 1000 + head_dim + page)
+    lengths = rng.integers(1, 1500, 5)
+    lengths[0] = 1
+    need = [math.ceil(n / page) for n in lengths]
+    arena = sum(need) + 2
+    order = rng.permutation(arena)
+    tables = np.zeros((5, max(need)), dtype=np.int32)
+    c = 0
+    for b, n in enumerate(need):
+        tables[b, :n] = order[c:c + n]
+        c += n
+    w = workloads.build("shape", lengths=lengths, tables=tables, arena_pages=arena,
+                        q_heads=q_heads, kv_heads=kv_heads, head_dim=head_dim,
+                        page_size=page, scale=head_dim ** -0.5, device=gpu, seed=7)
+    assert_parity(run(w), oracle(w), f"shape{q_heads}/{kv_heads}/{head_dim}/P{page}")
+    assert_parity(run(w, split_pages=4), oracle(w), "split4")
+
+
+def test_edge_lengths_and_empty_sequences(gpu):
+    lengths = [0, 1, 15, 16, 17, 31, 32, 33, 255, 256, 257, -3]
+    page = 16
+    need = [max(0, math.ceil(n / page)) for n in lengths]
+    arena = sum(need) + 1
+    order = np.random.default_rng(3).permutation(arena)
+    tables = np.zeros((len(lengths), max(need)), dtype=np.int32)
+    c = 0
+    for b, n in enumerate(need):
+        tables[b, :n] = order[c:c + n]
+        c += n
+    w = workloads.build("edges", lengths=lengths, tables=tables, arena_pages=arena,
+                        q_heads=28, kv_heads=4, head_dim=128, page_size=page,
+                        scale=128 ** -0.5, device=gpu, seed=9)
+    for split_pages in (0, 4):
+        got = run(w, split_pages=split_pages)
+        assert_parity(got, oracle(w), f"edges split={split_pages}")
+        assert not got[0].any() and not got[-1].any()
+
+
+def test_window_released_pages_and_poison(gpu):
+    """Rows outside every window, released (-1) pages and padding never leak
+    into the result, even when they hold NaN/inf (config 4 layout)."""
+    w = workloads.config4(device=gpu, batch=8, low=1100, high=6000, window=300)
+    clean = run(w).float().cpu()
+    tables = w.tables.cpu().numpy()
+    n = w.lengths.cpu().numpy()
+    visible = torch.zeros(w.keys.shape[0], dtype=torch.bool)
+    for b in range(w.batch):
+        pos = np.arange(n[b] - w.window, n[b])
+        rows = tables[b][pos // 16].astype(np.int64) * 16 + pos % 16
+        visible[torch.as_tensor(rows)] = True
+    hidden = (~visible).nonzero().squeeze(1).to(gpu)
+    w.keys[hidden] = float("nan")
+    w.values[hidden] = float("inf")
+    poisoned = run(w).float().cpu()
+    assert torch.equal(clean, poisoned)
+    assert_parity(poisoned, oracle(w), "poisoned window")
+
+
+def test_released_page_inside_window_is_masked(gpu):
+    w = workloads.config2(device=gpu, batch=4, low=600, high=900)
+    t = w.tables.cpu().numpy()
+    t[1, 3] = -1
+    t[2, 0] = -1
+    t[3, 5] = 10**9  # beyond the arena: masked as well
+    w.tables = torch.as_tensor(t, device=gpu)
+    expected = oracle(w)
+    assert_parity(run(w), expected, "released inside range")
+
+
+def test_softcap(gpu):
+    w = workloads.config2(device=gpu, batch=6, low=100, high=3000)
+    w.softcap = 1.5
+    assert_parity(run(w), oracle(w), "softcap")
+
+
+def test_repeated_calls_reuse_the_workspace(gpu):
+    """The split counters return to zero: alternate shapes on one workspace."""
+    a = workloads.config2(device=gpu, batch=6, low=2000, high=6000)
+    b = workloads.config5(device=gpu, batch=12, low=16, high=6000, shared=3, prefix=512)
+    ea, eb = oracle(a), oracle(b)
+    first = run(a, split_pages=4)
+    for _ in range(3):
+        assert_parity(run(b, split_pages=8), eb, "alt-b")
+        again = run(a, split_pages=4)
+        assert torch.equal(again, first)
+    assert_parity(first, ea, "alt-a")
+
+
+def test_decode_batch_writes_then_attends(gpu):
+    """DecodeBatch (batches.py:142-226 counterpart): the new token's K/V is
+    scattered into the arena before attention reads it."""
+    from instinct_amd.batches import DecodeBatch
+    from instinct_amd.paged_kv import KVCache, KVGroup
+
+    rng = np.random.default_rng(21)
+    page = 16
+    groups = [KVGroup("full", (0, 1), kv_heads=2, head_dim=128),
+              KVGroup("local", (2,), kv_heads=2, head_dim=128, window=64)]
+    cache = KVCache(groups, page_size=page, capacities={"full": 64, "local": 64}, device=gpu)
+    positions = np.array([0, 15, 16, 100, 333])
+    tables = {}
+    for name in ("full", "local"):
+        pool = cache.pools[name]
+        tables[name] = [np.array([pool.allocate(reserved=False)
+                                  for _ in range(p // page + 1)]) for p in positions]
+    gen = torch.Generator(device=gpu).manual_seed(0)
+    for layer in range(3):
+        cache.keys[layer].normal_(generator=gen)
+        cache.values[layer].normal_(generator=gen)
+    batch = DecodeBatch(cache, torch.zeros(5, device=gpu), positions=positions, tables=tables)
+    for layer in range(3):
+        group = cache.layer_group[layer]
+        q = torch.randn((5, 16, 128), generator=gen, device=gpu).half()
+        k = torch.randn((5, 2, 128), generator=gen, device=gpu).half()
+        v = torch.randn((5, 2, 128), generator=gen, device=gpu).half()
+        out = batch.attend(layer, q, k, v, scale=128 ** -0.5)
+        assert out.shape == (5, 16 * 128)
+        packed = batch._tables[group.name].cpu().numpy()
+        rows = packed[np.arange(5), positions // page] * page + positions % page
+        assert torch.equal(cache.keys[layer][torch.as_tensor(rows, device=gpu).long()], k)
+        expected = cpu_oracle.decode_f64(
+            q.cpu().numpy(), cache.keys[layer].cpu().numpy(),
+            cache.values[layer].cpu().numpy(), packed, positions + 1, page_size=page,
+            scale=128 ** -0.5, window=group.window)
+        assert_parity(out.view(5, 16, 128), expected, f"layer{layer}")
