@@ -68,18 +68,20 @@ const char* pda_last_error(void);
 /* Bytes of device workspace pda_paged_decode_attention needs for this shape.
  * Replaces the per-call allocation of the split partials
  * (metal_kernels.py:228-239 output_shapes: partial_o [B,HQ,S,D],
- * partial_m / partial_l [B,HQ,S] in float32). The first
- * pda_workspace_zero_bytes() bytes of a workspace hold split counters: they
- * must be zero before the workspace is first used (the kernel leaves them at
- * zero when it finishes). `longest` and `split_pages` as for the decode call. */
+ * partial_m / partial_l [B,HQ,S] in float32). Every workspace starts with a
+ * fixed header of pda_workspace_zero_bytes() bytes of split counters, the
+ * same for every shape: the header must be zero before the workspace is first
+ * used, and each call leaves it at zero, so one workspace serves calls of any
+ * shape in turn (e.g. sliding-window and global layers). batch * kv_heads *
+ * ceil(group / 8) must not exceed 65536. `longest` and `split_pages` as for
+ * the decode call. */
 int pda_workspace_bytes(int32_t batch, int32_t q_heads, int32_t kv_heads,
                         int32_t head_dim, int32_t page_size,
                         int32_t table_stride, int32_t longest, int32_t window,
                         int32_t split_pages, size_t* bytes);
 
-/* Leading bytes of a workspace of this shape that must start at zero. */
-int pda_workspace_zero_bytes(int32_t batch, int32_t q_heads, int32_t kv_heads,
-                             size_t* bytes);
+/* Size of the zero-initialised counter header at the start of a workspace. */
+int pda_workspace_zero_bytes(size_t* bytes);
 
 /* The split plan the decode call would use: pages per split and the largest
  * split count of any sequence. Replaces KEYS_PER_SPLIT / MAX_SPLITS and the

@@ -53,6 +53,10 @@ constexpr int kWaves = 4;            // waves per workgroup
 constexpr int kThreads = kWaves * 64;
 constexpr int kMaxSplitPages = 64;   // table entries of a split live in one VGPR
 constexpr int kMaxSplits = 4096;
+// Split counters: one uint32 per (sequence, kv head, head group), in a
+// fixed header at the start of every workspace.
+constexpr int kMaxUnits = 65536;
+constexpr size_t kCounterBytes = kMaxUnits * sizeof(uint32_t);
 constexpr int kNbuf = 2;             // K/V steps in flight per wave
 // The planner sizes splits for this many compute units (MI355X: 256), so the
 // workspace size is a pure function of the shape.
@@ -266,7 +270,11 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(const Params p) 
     const int t = t0 + kk;
     const bool valid = t >= first && t < len;
     if (!(t0 >= first && t0 + KPS <= len)) {
-      // Boundary step: rows outside [first, len) may hold anything.
+      // Boundary step. A step with no visible key is skipped: before the
+      // first visible key the running max is still -inf, and -inf - -inf
+      // would poison the sums. Rows outside [first, len) may hold anything,
+      // so their values are zeroed.
+      if (!__any(valid)) return;
 #pragma unroll
       for (int v = 0; v < NV; ++v) vd[v] = zero_unless(vd[v], valid);
     }
@@ -573,14 +581,20 @@ int make_plan(int32_t batch, int32_t q_heads, int32_t kv_heads, int32_t head_dim
   pl.split_pages = sp;
   pl.max_splits = (int)splits;
   const size_t units = (size_t)batch * kv_heads * pl.nhg;
-  pl.zero_bytes = align256(units * sizeof(uint32_t));
-  pl.off_ml = pl.zero_bytes;
+  if (units > kMaxUnits)
+    return fail(PDA_ERR_INVALID_ARGUMENT,
+                "batch * kv_heads * head groups = %zu above %d", units, kMaxUnits);
+  // Layout: a fixed counter header (the same for every shape, so counters
+  // left at zero by one call are zero for the next call of any shape), then
+  // the (max, sum) pairs and the unnormalised partial outputs.
+  pl.zero_bytes = kCounterBytes;
+  pl.off_ml = kCounterBytes;
   const size_t ml_bytes = align256(units * pl.max_splits * pl.G * sizeof(float2));
   pl.off_o = pl.off_ml + ml_bytes;
   const size_t o_bytes =
       align256(units * pl.max_splits * (size_t)pl.G * head_dim * sizeof(float));
   // Sequences with one split never touch the partials, but any may split.
-  pl.total = pl.max_splits > 1 ? pl.off_o + o_bytes : pl.zero_bytes;
+  pl.total = pl.max_splits > 1 ? pl.off_o + o_bytes : kCounterBytes;
   *out = pl;
   return PDA_OK;
 }
@@ -606,16 +620,9 @@ int pda_workspace_bytes(int32_t batch, int32_t q_heads, int32_t kv_heads,
   return ok();
 }
 
-int pda_workspace_zero_bytes(int32_t batch, int32_t q_heads, int32_t kv_heads,
-                             size_t* bytes) {
+int pda_workspace_zero_bytes(size_t* bytes) {
   if (!bytes) return fail(PDA_ERR_INVALID_ARGUMENT, "bytes is null");
-  if (batch < 0 || q_heads <= 0 || kv_heads <= 0)
-    return fail(PDA_ERR_INVALID_ARGUMENT, "non-positive size");
-  if (q_heads % kv_heads)
-    return fail(PDA_ERR_HEAD_RATIO, "query heads must be a multiple of kv heads");
-  const int gtot = q_heads / kv_heads;
-  const int nhg = gtot / heads_per_group(gtot);
-  *bytes = align256((size_t)batch * kv_heads * nhg * sizeof(uint32_t));
+  *bytes = kCounterBytes;
   return ok();
 }
 

@@ -34,10 +34,7 @@ SIGNATURES = {
         ctypes.c_int,
         [c_int32] * 9 + [ctypes.POINTER(c_size_t)],
     ),
-    "pda_workspace_zero_bytes": (
-        ctypes.c_int,
-        [c_int32] * 3 + [ctypes.POINTER(c_size_t)],
-    ),
+    "pda_workspace_zero_bytes": (ctypes.c_int, [ctypes.POINTER(c_size_t)]),
     "pda_plan": (
         ctypes.c_int,
         [c_int32] * 9 + [ctypes.POINTER(c_int32), ctypes.POINTER(c_int32)],
@@ -99,9 +96,9 @@ def workspace_bytes(batch, q_heads, kv_heads, head_dim, page_size, table_stride,
     return out.value
 
 
-def workspace_zero_bytes(batch, q_heads, kv_heads) -> int:
+def workspace_zero_bytes() -> int:
     out = c_size_t(0)
-    check(library().pda_workspace_zero_bytes(batch, q_heads, kv_heads, ctypes.byref(out)))
+    check(library().pda_workspace_zero_bytes(ctypes.byref(out)))
     return out.value
 
 

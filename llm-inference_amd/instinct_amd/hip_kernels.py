@@ -26,11 +26,12 @@ from . import _lib
 _workspaces: dict[tuple[int, int], torch.Tensor] = {}
 
 
-def workspace(device: torch.device, nbytes: int, zero_bytes: int) -> torch.Tensor:
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     """A cached, 256-byte aligned device workspace of at least ``nbytes``.
 
-    The leading ``zero_bytes`` hold split counters that start at zero and that
-    the kernel returns to zero, so the buffer is zeroed once when created."""
+    Its fixed header holds split counters that must start at zero and that
+    every call returns to zero, whatever its shape, so a buffer is zeroed once
+    when it is created and then reused by calls of any shape."""
     index = device.index if device.index is not None else torch.cuda.current_device()
     key = (index, 0)
     buf = _workspaces.get(key)
@@ -40,7 +41,6 @@ def workspace(device: torch.device, nbytes: int, zero_bytes: int) -> torch.Tenso
             size = max(size, 2 * buf.numel())
         buf = torch.zeros(size, dtype=torch.uint8, device=device)
         _workspaces[key] = buf
-    del zero_bytes  # the kernel keeps the counters at zero between calls
     return buf
 
 
@@ -92,8 +92,7 @@ def paged_decode_attention(
     stride = int(tables.shape[1])
     need = _lib.workspace_bytes(batch, q_heads, kv_heads, head_dim, page_size, stride,
                                 int(longest), int(window), int(split_pages))
-    zero = _lib.workspace_zero_bytes(batch, q_heads, kv_heads)
-    ws = workspace(device, need, zero)
+    ws = workspace(device, need)
     stream = torch.cuda.current_stream(device).cuda_stream
     rc = _lib.library().pda_paged_decode_attention(
         queries.data_ptr(), keys.data_ptr(), values.data_ptr(), tables.data_ptr(),

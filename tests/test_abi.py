@@ -84,18 +84,26 @@ def test_workspace_and_plan_are_consistent():
     pages, splits = _lib.plan(64, 28, 4, 128, 16, 512, 8192, 0)
     assert 4 <= pages <= 64 and splits == -(-512 // pages)
     need = _lib.workspace_bytes(64, 28, 4, 128, 16, 512, 8192, 0)
-    zero = _lib.workspace_zero_bytes(64, 28, 4)
-    assert zero == 256 * -(-64 * 4 * 4 // 256)  # one uint32 per (seq, kv head)
+    zero = _lib.workspace_zero_bytes()
+    assert zero == 65536 * 4  # fixed header: one uint32 per (seq, kv head, head group)
     units = 64 * 4
     assert need >= zero + units * splits * 7 * (128 + 2) * 4
     # A forced split size changes the plan but never below the data it needs.
     assert _lib.plan(64, 28, 4, 128, 16, 512, 8192, 0, split_pages=8) == (8, 64)
     # A window bounds the visible pages whatever the table width.
     assert _lib.plan(32, 8, 4, 256, 16, 2048, 32768, 1024, split_pages=16) == (16, 5)
+    # One split needs no partials, only the header.
+    assert _lib.workspace_bytes(2, 8, 8, 64, 16, 4, 64, 0, split_pages=4) == zero
     # More than 8 heads per kv head are served by several head groups.
-    assert _lib.workspace_zero_bytes(2, 16, 1) == 256
-    # One split needs no partials.
-    assert _lib.workspace_bytes(2, 8, 8, 64, 16, 4, 64, 0, split_pages=4) == 256
+    one = _lib.workspace_bytes(2, 8, 1, 128, 16, 64, 1024, 0, split_pages=4)
+    two = _lib.workspace_bytes(2, 16, 1, 128, 16, 64, 1024, 0, split_pages=4)
+    assert two - zero == 2 * (one - zero)
+
+
+def test_too_many_counter_units_are_rejected():
+    with pytest.raises(_lib.PdaError) as err:
+        _lib.workspace_bytes(65535, 16, 2, 128, 16, 64, 1024, 0)
+    assert err.value.code == _lib.PDA_ERR_INVALID_ARGUMENT
 
 
 def test_split_count_limit():

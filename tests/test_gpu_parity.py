@@ -232,6 +232,21 @@ def test_repeated_calls_reuse_the_workspace(gpu):
     assert_parity(first, ea, "alt-a")
 
 
+def test_one_workspace_serves_shapes_with_different_layouts(gpu):
+    """Regression: a window/D=256 call with few units leaves float partials
+    where a larger batch keeps its split counters unless the counters live in
+    a fixed header. Alternate the two layouts on one workspace."""
+    from instinct_amd import hip_kernels
+
+    hip_kernels._workspaces.clear()
+    a = workloads.config4(device=gpu, batch=6, low=2000, high=5000)
+    b = workloads.config5(device=gpu, batch=24, low=16, high=8192, shared=6, prefix=1024)
+    ea, eb = oracle(a), oracle(b)
+    for i in range(2):
+        assert_parity(run(a, split_pages=4), ea, f"layout-a{i}")
+        assert_parity(run(b), eb, f"layout-b{i}")
+
+
 def test_decode_batch_writes_then_attends(gpu):
     """DecodeBatch (batches.py:142-226 counterpart): the new token's K/V is
     scattered into the arena before attention reads it."""
