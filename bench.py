@@ -8,8 +8,9 @@ resident in HBM.
 
 Timing: W warmup calls, then K timed calls, each bracketed by HIP events on
 the stream the kernel runs on. Between timed calls a 1 GiB buffer is written
-so the 256 MB Infinity Cache and the L2s hold none of the arena (flushed =
-HBM numbers); a second pass without the flush is reported as "warm".
+and another 1 GiB read, so the 256 MB Infinity Cache and the L2s hold none of
+the arena and no dirty lines (flushed = HBM numbers); a second pass without
+the flush is reported as "warm".
 value = algorithmic K/V bytes / median call time (GB/s). The CPU baseline is
 the oracle's threaded C++ restatement of the reference's split-K algorithm,
 timed on a bounded sample of the same workload on this host's cores.
@@ -35,6 +36,7 @@ for _p in (ROOT, ROOT / "llm-inference_amd"):
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
 METRIC = "decode-attention effective K/V GB/s (% of HBM peak) + µs/layer-step"
 TRAFFIC_FILE = ROOT / "profiles" / "traffic_config2.json"
+SPIN_CYCLES = 2_000_000  # torch.cuda._sleep before each timed call
 
 
 def parse():
@@ -48,6 +50,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="approximate CPU time budget of the CPU-baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB (rocprof counter scale)")
     return ap.parse_args()
 
 
@@ -62,6 +66,9 @@ def time_calls(call, steps, flush=None):
     for i in range(steps):
         if flush is not None:
             flush()
+        # A bounded spin keeps the queue busy while the host enqueues the
+        # events and the call, so no host time falls between the events.
+        torch.cuda._sleep(SPIN_CYCLES)
         starts[i].record(stream)
         call()
         ends[i].record(stream)
@@ -124,6 +131,18 @@ def main():
 
     import torch
 
+    if args.copy_calibration:
+        # A plain copy of known size: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on
+        # this run gives the factor between counter readings and bytes moved.
+        n = args.copy_calibration << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(max(1, args.steps)):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": n, "launches": max(1, args.steps)}))
+        return
+
     from instinct_amd import _lib, workloads
     from instinct_amd.hip_kernels import paged_decode_attention
 
@@ -143,9 +162,14 @@ def main():
         call()
     torch.cuda.synchronize()
     flush_buf = torch.empty(1 << 30, dtype=torch.uint8, device=device)
+    read_buf = torch.ones(1 << 28, dtype=torch.int32, device=device)
 
     def flush():
+        # Write 1 GiB, then read 1 GiB: the caches end up holding clean lines
+        # of neither the arena nor the write (whose write-back would otherwise
+        # land inside the timed region).
         flush_buf.fill_(1)
+        read_buf.sum()
 
     ms_flush, wall = (None, None) if args.no_flush else time_calls(call, args.steps, flush)
     ms_warm, _ = time_calls(call, args.steps)
@@ -154,8 +178,8 @@ def main():
     mean = statistics.fmean(ms)
     value = kv_bytes / (med * 1e-3) / 1e9
     achieved = kv_bytes / (mean * 1e-3) / 1e9
-    pages, splits = _lib.plan(w.batch, w.q_heads, w.kv_heads, w.head_dim, w.page_size,
-                              int(w.tables.shape[1]), w.longest, w.window, args.split_pages)
+    waves, _ = _lib.plan(w.batch, w.q_heads, w.kv_heads, w.head_dim, w.page_size,
+                         int(w.tables.shape[1]), w.longest, w.window, args.split_pages)
     traffic = None
     if TRAFFIC_FILE.exists() and args.config == 2:
         traffic = json.loads(TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
@@ -177,8 +201,8 @@ def main():
             "batch": w.batch, "q_heads": w.q_heads, "kv_heads": w.kv_heads,
             "head_dim": w.head_dim, "page_size": w.page_size, "window": w.window,
             "longest": w.longest, "kv_bytes": kv_bytes,
-            "split_pages": pages, "max_splits": splits,
-            "cache": "flushed (1 GiB write between calls)" if ms_flush else "warm",
+            "split_pages": args.split_pages, "stream_waves_max": waves,
+            "cache": "flushed (1 GiB write + 1 GiB read between calls)" if ms_flush else "warm",
         },
         "us_per_layer_step": round(med * 1e3, 2),
         "steps_per_s": round(1e3 / med, 1),
@@ -192,7 +216,7 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "kernel": "paged_decode_kernel<128,7> (split + fused merge, one launch)",
+            "kernel": "paged_decode_kernel<128,7> + paged_decode_merge_kernel (one call)",
             "us_mean": round(mean * 1e3, 2),
         },
     }

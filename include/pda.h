@@ -68,29 +68,24 @@ const char* pda_last_error(void);
 /* Bytes of device workspace pda_paged_decode_attention needs for this shape.
  * Replaces the per-call allocation of the split partials
  * (metal_kernels.py:228-239 output_shapes: partial_o [B,HQ,S,D],
- * partial_m / partial_l [B,HQ,S] in float32). Every workspace starts with a
- * fixed header of pda_workspace_zero_bytes() bytes of split counters, the
- * same for every shape: the header must be zero before the workspace is first
- * used, and each call leaves it at zero, so one workspace serves calls of any
- * shape in turn (e.g. sliding-window and global layers). batch * kv_heads *
- * ceil(group / 8) must not exceed 65536. `longest` and `split_pages` as for
- * the decode call. */
+ * partial_m / partial_l [B,HQ,S] in float32): here a per-sequence page
+ * prefix plus two partial slots per resident wave. The workspace needs no
+ * initialisation and holds nothing between calls, so one buffer serves calls
+ * of any shape in turn. `longest` and `split_pages` as for the decode call. */
 int pda_workspace_bytes(int32_t batch, int32_t q_heads, int32_t kv_heads,
                         int32_t head_dim, int32_t page_size,
                         int32_t table_stride, int32_t longest, int32_t window,
                         int32_t split_pages, size_t* bytes);
 
-/* Size of the zero-initialised counter header at the start of a workspace. */
-int pda_workspace_zero_bytes(size_t* bytes);
-
-/* The split plan the decode call would use: pages per split and the largest
- * split count of any sequence. Replaces KEYS_PER_SPLIT / MAX_SPLITS and the
- * batch-wide split rule (metal_kernels.py:126-127,193-194), which the MI355X
- * kernel replaces by a per-sequence split of fixed-size page chunks. */
+/* The split plan for a batch whose lengths all equal `longest`: the number of
+ * waves the visible pages are spread over and the pages each wave reads.
+ * Informational. Replaces KEYS_PER_SPLIT / MAX_SPLITS and the batch-wide
+ * split rule (metal_kernels.py:126-127,193-194): the MI355X kernel splits the
+ * stream of all visible pages of the batch into equal per-wave ranges. */
 int pda_plan(int32_t batch, int32_t q_heads, int32_t kv_heads,
              int32_t head_dim, int32_t page_size, int32_t table_stride,
              int32_t longest, int32_t window, int32_t split_pages,
-             int32_t* pages_per_split, int32_t* max_splits);
+             int32_t* waves, int32_t* pages_per_wave);
 
 /* Paged decode attention for one new token per sequence.
  * Replaces paged_decode_attention (metal_kernels.py:164-248): same inputs and
@@ -98,9 +93,10 @@ int pda_plan(int32_t batch, int32_t q_heads, int32_t kv_heads,
  * softcap * tanh(score / softcap) (metal_kernels.py:53); `window` 0 = full
  * attention. `longest` is the host-side largest length, as in the reference
  * (a planning hint only: results never depend on it, and lengths above it
- * stay correct). `split_pages` = 0 lets the planner choose the pages per
- * split; a positive value forces it (tuning and tests). `arena_rows` is the
- * row count of the keys/values arenas. Stream-ordered; calls that share a
+ * stay correct). `split_pages` is the fewest pages a wave reads before the
+ * stream is spread over fewer waves (0 = 8; results do not depend on it).
+ * `arena_rows` is the row count of the keys/values arenas; batch <= 8191.
+ * Launches a split kernel and a merge kernel on `stream`; calls that share a
  * workspace must not overlap. */
 int pda_paged_decode_attention(const void* queries, const void* keys,
                                const void* values, const int32_t* tables,

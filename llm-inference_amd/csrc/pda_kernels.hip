@@ -7,11 +7,16 @@
 // keys are [max(0, len - window), len), pages with a negative id are masked.
 //
 // MI355X design (not a translation of the Metal kernel):
-//  * One workgroup = 4 wave64s = one (sequence, kv head, split). A split is a
-//    fixed run of `split_pages` pages of that sequence, so each sequence gets
-//    its own split count ceil(pages / split_pages) instead of the reference's
-//    batch-wide count taken from the longest sequence (:193-194). Workgroups
-//    beyond a sequence's split count exit at once.
+//  * Stream-K split. A unit is (sequence, kv head group); the visible pages of
+//    all units, in order, form one stream of T pages. A persistent grid of W
+//    resident wave64s takes equal contiguous ranges of that stream, so every
+//    wave reads the same number of K/V bytes whatever the mix of context
+//    lengths (the reference splits every sequence by the longest one,
+//    metal_kernels.py:193-194). A unit that lies inside one wave's range is
+//    normalised and written by that wave (as _SINGLE_WRITE); a unit cut by a
+//    range boundary leaves unnormalised partials (as _SPLIT_WRITE) that the
+//    merge kernel combines (as _DECODE_MERGE). A wave cuts at most the first
+//    and the last unit of its range, so there are at most 2 W partials.
 //  * Inside a wave, R lanes share one key row (R = head_dim / EPL, EPL = 8 or
 //    16 fp16 per lane, i.e. one or two 16-byte loads per lane per row), so a
 //    wave covers 64 / R keys per step. Every step reads K and V rows once and
@@ -22,20 +27,21 @@
 //    accumulators are rescaled only when a score exceeds the running max by
 //    more than 2^8, so steady-state steps do no rescaling.
 //  * K/V loads run NBUF steps ahead of the math through a register ring.
-//  * The last workgroup of a sequence's splits to finish merges the partials
-//    (log-sum-exp, as _DECODE_MERGE) behind an agent-scope release/acquire
-//    counter, so a call is one kernel launch. Sequences with one split
-//    normalise and write their output directly (as _SINGLE_WRITE).
+//  * No cross-workgroup synchronisation: the split kernel only writes, the
+//    merge kernel runs after it on the same stream.
 
 #include <hip/hip_runtime.h>
 
 #include <math.h>
 
 #include <algorithm>
+#include <map>
+#include <mutex>
 #include <stdarg.h>
 #include <stddef.h>
 #include <stdint.h>
 #include <stdio.h>
+#include <utility>
 
 #include "pda.h"
 
@@ -49,18 +55,15 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 constexpr float kLog2e = 1.44269504088896340736f;
 // Lazy rescale threshold (log2 units): probabilities stay below 2^8.
 constexpr float kSlack = 8.0f;
-constexpr int kWaves = 4;            // waves per workgroup
+constexpr int kWaves = 4;              // waves per workgroup
 constexpr int kThreads = kWaves * 64;
-constexpr int kMaxSplitPages = 64;   // table entries of a split live in one VGPR
-constexpr int kMaxSplits = 4096;
-// Split counters: one uint32 per (sequence, kv head, head group), in a
-// fixed header at the start of every workspace.
-constexpr int kMaxUnits = 65536;
-constexpr size_t kCounterBytes = kMaxUnits * sizeof(uint32_t);
-constexpr int kNbuf = 2;             // K/V steps in flight per wave
-// The planner sizes splits for this many compute units (MI355X: 256), so the
-// workspace size is a pure function of the shape.
-constexpr int kPlanCUs = 256;
+constexpr int kNbuf = 2;               // K/V steps in flight per wave
+constexpr int kTablePages = 64;        // page-table entries held per VGPR refill
+constexpr int kMaxGroups = 512;        // resident workgroups (MI355X: 256 CUs x 2)
+constexpr int kMaxWaves = kMaxGroups * kWaves;
+constexpr int kSlots = 2 * kMaxWaves;  // partial slots: first and last unit of a wave
+constexpr int kMinPagesPerWave = 8;    // default: spread no thinner than this
+constexpr int kMaxBatch = 8191;        // per-sequence tables in LDS: (2B + 1) ints
 
 struct Params {
   const f16* q;
@@ -69,10 +72,11 @@ struct Params {
   const int32_t* tables;
   const int32_t* lengths;
   f16* out;
-  float* part_o;      // [B * HKV * NHG][max_splits][G][D]
-  float2* part_ml;    // [B * HKV * NHG][max_splits][G] (running max, sum)
-  uint32_t* counters; // [B * HKV * NHG]
+  int32_t* prefix;    // [B + 1] visible pages before each sequence (workspace)
+  float2* part_ml;    // [kSlots][G] (running max, sum) of cut units
+  float* part_o;      // [kSlots][G][D] unnormalised outputs of cut units
   int64_t arena_pages;
+  int32_t batch;
   int32_t table_stride;
   int32_t page_size;
   int32_t hq;
@@ -80,11 +84,12 @@ struct Params {
   int32_t gtot;       // query heads per kv head
   int32_t nhg;        // head groups per kv head (gtot / G)
   int32_t window;
-  int32_t split_pages;
-  int32_t max_splits;
+  int32_t grid_waves; // waves of the split kernel's grid
+  int32_t min_pages;  // fewest pages per wave before the stream uses fewer waves
   float scale_log2;   // scale * log2(e)
-  float scale;
-  float softcap;
+  float softcap;      // 0 = off
+  float cap_in;       // 2 * log2(e) * scale / softcap
+  float cap_out;      // softcap * log2(e)
 };
 
 constexpr int next_pow2(int x) {
@@ -144,10 +149,6 @@ __device__ __forceinline__ float wave_max(float x) {
       float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, x)));
 }
 
-__device__ __forceinline__ f16x8 load16(const f16* p) {
-  return *reinterpret_cast<const f16x8*>(p);
-}
-
 __device__ __forceinline__ f16x8 zero_unless(f16x8 x, bool keep) {
   i32x4 bits = __builtin_bit_cast(i32x4, x);
   bits.x = keep ? bits.x : 0;
@@ -157,18 +158,85 @@ __device__ __forceinline__ f16x8 zero_unless(f16x8 x, bool keep) {
   return __builtin_bit_cast(f16x8, bits);
 }
 
-// One workgroup: (split, kv head group, sequence) = (blockIdx.x, .y, .z).
+struct SeqGeometry {
+  int len, first, first_page, npages;
+};
+
+// Visible range [first, len) of sequence b (metal_kernels.py:32-36, length
+// clamped to the table) and the pages it touches.
+__device__ __forceinline__ SeqGeometry sequence_geometry(const Params& p, int b) {
+  SeqGeometry g;
+  const int P = p.page_size;
+  g.len = min(max(p.lengths[b], 0), p.table_stride * P);
+  g.first = p.window > 0 ? max(0, g.len - p.window) : 0;
+  g.first_page = g.first / P;
+  g.npages = g.len > g.first ? (g.len - 1) / P - g.first_page + 1 : 0;
+  return g;
+}
+
+// Waves the stream of `total` pages is spread over (both kernels agree).
+__device__ __forceinline__ int stream_waves(int64_t total, const Params& p) {
+  if (total <= 0) return 0;
+  const int64_t want = (total + p.min_pages - 1) / p.min_pages;
+  return (int)min<int64_t>(want, p.grid_waves);
+}
+
+// First page of wave w's range, and the wave whose range holds page x.
+__device__ __forceinline__ int64_t range_start(int w, int64_t total, int waves) {
+  return (int64_t)w * total / waves;
+}
+__device__ __forceinline__ int wave_of(int64_t x, int64_t total, int waves) {
+  return (int)(((x + 1) * waves - 1) / total);
+}
+
+// Exclusive prefix of visible pages over the batch, into LDS (all threads of
+// the workgroup), plus each sequence's clamped length.
+__device__ void build_prefix(const Params& p, int* s_prefix, int* s_len) {
+  __shared__ int s_wsum[kWaves];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int B = p.batch;
+  int carry = 0;
+  for (int base = 0; base < B; base += kThreads) {
+    const int b = base + tid;
+    int x = 0;
+    if (b < B) {
+      const SeqGeometry g = sequence_geometry(p, b);
+      x = g.npages;
+      s_len[b] = g.len;
+    }
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int y = __shfl_up(x, off);
+      if (lane >= off) x += y;
+    }
+    if (lane == 63) s_wsum[w] = x;
+    __syncthreads();
+    int before = carry, block = 0;
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) {
+      before += i < w ? s_wsum[i] : 0;
+      block += s_wsum[i];
+    }
+    if (b < B) s_prefix[b + 1] = before + x;
+    carry += block;
+    __syncthreads();
+  }
+  if (tid == 0) s_prefix[0] = 0;
+  __syncthreads();
+}
+
+// Split kernel: a persistent grid; wave wv walks pages [x0, x1) of the stream.
+// At least two waves per SIMD (<= 256 registers): with G = 7 or 8 heads the
+// few values that do not fit live outside the main loop.
 template <int D, int G>
-__global__ __launch_bounds__(kThreads) void paged_decode_kernel(const Params p) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
+void paged_decode_kernel(const Params p) {
   using Gm = Geom<D>;
   constexpr int EPL = Gm::EPL, NV = Gm::NV, R = Gm::R, KPS = Gm::KPS;
-
-  __shared__ float s_m[kWaves][G];
-  __shared__ float s_l[kWaves][G];
-  __shared__ float s_M[G];
-  __shared__ float s_L[G];
-  __shared__ float s_o[G * D];
-  __shared__ int s_last;
+  extern __shared__ int s_dyn[];
+  const int B = p.batch;
+  int* const s_prefix = s_dyn;         // [B + 1]
+  int* const s_len = s_dyn + B + 1;    // [B]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -177,281 +245,346 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(const Params p) 
   const int r = lane % R;   // slice of the head this lane holds
   const bool active = r < Gm::SLICES;
   const int d0 = active ? r * EPL : 0;
-
-  const int split = blockIdx.x;
-  const int kvg = blockIdx.y;
-  const int b = blockIdx.z;
-  const int kvh = kvg / p.nhg;
-  const int hg = kvg - kvh * p.nhg;
   const int P = p.page_size;
+  const int nkvg = p.hkv * p.nhg;
 
-  // Geometry of this sequence (metal_kernels.py:32-36), page-aligned splits.
-  int len = p.lengths[b];
-  len = min(max(len, 0), p.table_stride * P);
-  const int first = p.window > 0 ? max(0, len - p.window) : 0;
-  const int first_page = first / P;
-  const int npages = len > first ? (len - 1) / P - first_page + 1 : 0;
-  const int nsplit =
-      max(1, min((npages + p.split_pages - 1) / p.split_pages, p.max_splits));
-  if (split >= nsplit) return;
-  const int split_first = first_page + split * p.split_pages;
-  const int split_npages = max(0, min(p.split_pages, npages - split * p.split_pages));
-  const int wave_npages =
-      split_npages > w ? (split_npages - w + kWaves - 1) / kWaves : 0;
+  build_prefix(p, s_prefix, s_len);
+  if (blockIdx.x == 0)
+    for (int i = tid; i <= B; i += kThreads) p.prefix[i] = s_prefix[i];
+  const int64_t total = (int64_t)s_prefix[B] * nkvg;
+  const int nwaves = stream_waves(total, p);
+  const int wv = blockIdx.x * kWaves + w;
+  if (wv >= nwaves) return;
+  const int64_t x0 = range_start(wv, total, nwaves);
+  const int64_t x1 = range_start(wv + 1, total, nwaves);
+
+  // Sequence holding page x0: the last b with nkvg * prefix[b] <= x0 (it is
+  // never an empty sequence, since x0 < total).
+  int b = 0;
+  {
+    int lo = 0, hi = B - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if ((int64_t)s_prefix[mid] * nkvg <= x0) lo = mid; else hi = mid - 1;
+    }
+    b = lo;
+  }
+  int npg = s_prefix[b + 1] - s_prefix[b];
+  if (npg <= 0) return;  // cannot happen for x0 < total; guards the division
+  const int64_t rel = x0 - (int64_t)s_prefix[b] * nkvg;
+  int kvg = (int)(rel / npg);
+  int pa = (int)(rel - (int64_t)kvg * npg);
+
+  const int64_t row_bytes = (int64_t)p.hkv * D * 2;  // bytes between arena rows
+  const char* const kbase = reinterpret_cast<const char*>(p.k);
+  const char* const vbase = reinterpret_cast<const char*>(p.v);
   const int spp = P / KPS;  // steps per page
-  const int nsteps = wave_npages * spp;
 
-  // Lane i holds the physical id of split page i.
-  int tbl = -1;
-  if (lane < split_npages)
-    tbl = p.tables[(int64_t)b * p.table_stride + split_first + lane];
+  int64_t x = x0;
+  bool first_unit = true;
+  while (x < x1 && b < B) {
+    npg = s_prefix[b + 1] - s_prefix[b];
+    const int cnt = (int)min<int64_t>(npg - pa, x1 - x);
+    const bool whole = pa == 0 && cnt == npg;
+    const int len = s_len[b];
+    const int first = p.window > 0 ? max(0, len - p.window) : 0;
+    const int first_page = first / P;
+    const int kvh = kvg / p.nhg;
+    const int h0 = kvh * p.gtot + (kvg - kvh * p.nhg) * G;
 
-  // Queries of the G heads, this lane's slice, as fp16 pairs for v_dot2.
-  const int h0 = kvh * p.gtot + hg * G;
-  f16x2 q[G][EPL / 2];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const f16* qp = p.q + ((int64_t)b * p.hq + h0 + g) * D + d0;
-#pragma unroll
-    for (int v = 0; v < NV; ++v) {
-      f16x8 x = zero_unless(load16(qp + 8 * v), active);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) q[g][4 * v + i] = f16x2{x[2 * i], x[2 * i + 1]};
-    }
-  }
-
-  float o[G][EPL];
-  float l[G];
-  float m[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    l[g] = 0.0f;
-    m[g] = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < EPL; ++i) o[g][i] = 0.0f;
-  }
-
-  const int64_t row_stride = (int64_t)p.hkv * D;  // elements between arena rows
-  const f16* kbase = p.k + (int64_t)kvh * D + d0 + kk * row_stride;
-  const f16* vbase = p.v + (int64_t)kvh * D + d0 + kk * row_stride;
-
-  f16x8 kb[kNbuf][NV], vb[kNbuf][NV];
-  int ld_pl = 0, ld_sub = 0;  // next step to load: (wave page, step in page)
-  int cp_pl = 0, cp_sub = 0;  // next step to compute
-
-  auto load_step = [&](f16x8(&kd)[NV], f16x8(&vd)[NV]) {
-    int pid = __builtin_amdgcn_readlane(tbl, w + ld_pl * kWaves);
-    pid = (pid >= 0 && pid < p.arena_pages) ? pid : 0;
-    const int64_t off = ((int64_t)pid * P + ld_sub * KPS) * row_stride;
-#pragma unroll
-    for (int v = 0; v < NV; ++v) {
-      kd[v] = load16(kbase + off + 8 * v);
-      vd[v] = load16(vbase + off + 8 * v);
-    }
-    // Advance, staying on the last step once there (the ring keeps loading
-    // it; those reloads hit the cache and their data is never used).
-    if (ld_pl * spp + ld_sub + 1 < nsteps) {
-      if (++ld_sub == spp) {
-        ld_sub = 0;
-        ++ld_pl;
-      }
-    }
-  };
-
-  auto compute_step = [&](f16x8(&kd)[NV], f16x8(&vd)[NV]) {
-    const int pidx = w + cp_pl * kWaves;
-    const int pid = __builtin_amdgcn_readlane(tbl, pidx);
-    const int t0 = (split_first + pidx) * P + cp_sub * KPS;
-    if (++cp_sub == spp) {
-      cp_sub = 0;
-      ++cp_pl;
-    }
-    if (pid < 0 || pid >= p.arena_pages) return;  // released page: masked
-    const int t = t0 + kk;
-    const bool valid = t >= first && t < len;
-    if (!(t0 >= first && t0 + KPS <= len)) {
-      // Boundary step. A step with no visible key is skipped: before the
-      // first visible key the running max is still -inf, and -inf - -inf
-      // would poison the sums. Rows outside [first, len) may hold anything,
-      // so their values are zeroed.
-      if (!__any(valid)) return;
-#pragma unroll
-      for (int v = 0; v < NV; ++v) vd[v] = zero_unless(vd[v], valid);
-    }
-    float s[G];
+    // Queries of the G heads, this lane's slice, as fp16 pairs for v_dot2.
+    f16x2 q[G][EPL / 2];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      float acc = 0.0f;
+      const f16* qp = p.q + ((int64_t)b * p.hq + h0 + g) * D + d0;
 #pragma unroll
       for (int v = 0; v < NV; ++v) {
+        f16x8 xq = zero_unless(*reinterpret_cast<const f16x8*>(qp + 8 * v), active);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const f16x2 kp = f16x2{kd[v][2 * i], kd[v][2 * i + 1]};
-          acc = __builtin_amdgcn_fdot2(q[g][4 * v + i], kp, acc, false);
+        for (int i = 0; i < 4; ++i) q[g][4 * v + i] = f16x2{xq[2 * i], xq[2 * i + 1]};
+      }
+    }
+
+    float o[G][EPL];
+    float l[G];
+    float m[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      l[g] = 0.0f;
+      m[g] = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) o[g][i] = 0.0f;
+    }
+
+    // Addressing: a wave-uniform byte offset per step (page row base) plus a
+    // 32-bit per-lane offset (its key within the step, kv head and slice).
+    const uint32_t lane_off = (uint32_t)(kk * row_bytes + ((int64_t)kvh * D + d0) * 2);
+
+    for (int sp0 = pa; sp0 < pa + cnt; sp0 += kTablePages) {
+      const int n = min(kTablePages, pa + cnt - sp0);
+      const int page0 = first_page + sp0;  // logical page of table lane 0
+      // Lane i holds the physical id of logical page page0 + i.
+      int tbl = -1;
+      if (lane < n) tbl = p.tables[(int64_t)b * p.table_stride + page0 + lane];
+      const int nsteps = n * spp;
+
+      f16x8 kb[kNbuf][NV], vb[kNbuf][NV];
+      int ld_pg = 0, ld_sub = 0;  // next step to load: (page, step in page)
+      int cp_pg = 0, cp_sub = 0;  // next step to compute
+
+      auto load_step = [&](f16x8(&kd)[NV], f16x8(&vd)[NV]) {
+        int pid = __builtin_amdgcn_readlane(tbl, ld_pg);
+        pid = (pid >= 0 && pid < p.arena_pages) ? pid : 0;
+        const int64_t uoff = ((int64_t)pid * P + ld_sub * KPS) * row_bytes;
+        const char* kp = kbase + uoff + lane_off;
+        const char* vp = vbase + uoff + lane_off;
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+          kd[v] = *reinterpret_cast<const f16x8*>(kp + 16 * v);
+          vd[v] = *reinterpret_cast<const f16x8*>(vp + 16 * v);
         }
-      }
-      s[g] = acc;
-    }
-    bool grow = false;
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float x = group_sum<R>(s[g]);
-      if (p.softcap > 0.0f) {
-        x = tanhf(x * p.scale / p.softcap) * p.softcap * kLog2e;
-      } else {
-        x *= p.scale_log2;
-      }
-      x = valid ? x : -INFINITY;
-      s[g] = x;
-      grow |= x > m[g] + kSlack;
-    }
-    if (__any(grow)) {
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float mn = fmaxf(m[g], wave_max(s[g]));
-        const float f = __builtin_amdgcn_exp2f(m[g] - mn);
-        m[g] = mn;
-        l[g] *= f;
-#pragma unroll
-        for (int i = 0; i < EPL; ++i) o[g][i] *= f;
-      }
-    }
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float pr = __builtin_amdgcn_exp2f(s[g] - m[g]);
-      l[g] += pr;
-#pragma unroll
-      for (int v = 0; v < NV; ++v) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-          o[g][8 * v + i] = __builtin_fmaf(pr, (float)vd[v][i], o[g][8 * v + i]);
-      }
-    }
-  };
+        // Advance, staying on the last step once there (the ring keeps
+        // loading it; those reloads hit the cache and are never used).
+        if (ld_pg * spp + ld_sub + 1 < nsteps) {
+          if (++ld_sub == spp) {
+            ld_sub = 0;
+            ++ld_pg;
+          }
+        }
+      };
 
-  if (nsteps > 0) {
-#pragma unroll
-    for (int u = 0; u < kNbuf; ++u) load_step(kb[u], vb[u]);
-    for (int j0 = 0; j0 < nsteps; j0 += kNbuf) {
-#pragma unroll
-      for (int u = 0; u < kNbuf; ++u) {
-        if (j0 + u < nsteps) compute_step(kb[u], vb[u]);
-        load_step(kb[u], vb[u]);
-      }
-    }
-  }
+      auto compute_step = [&](f16x8(&kd)[NV], f16x8(&vd)[NV]) {
+        const int pid = __builtin_amdgcn_readlane(tbl, cp_pg);
+        const int t0 = (page0 + cp_pg) * P + cp_sub * KPS;
+        if (++cp_sub == spp) {
+          cp_sub = 0;
+          ++cp_pg;
+        }
+        if (pid < 0 || pid >= p.arena_pages) return;  // released page: masked
 
-  // Fold the wave's key subsets, then the waves of the workgroup
-  // (metal_kernels.py:63-81, with per-wave running maxima).
+        // q.k for every head of the group: v_dot2 over this lane's slice,
+        // then the butterfly over the R lanes of the key.
+        float s[G];
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    l[g] = subset_sum<R>(l[g]);
+        for (int g = 0; g < G; ++g) {
+          float acc = 0.0f;
 #pragma unroll
-    for (int i = 0; i < EPL; ++i) o[g][i] = subset_sum<R>(o[g][i]);
-  }
-  if (lane == 0) {
+          for (int v = 0; v < NV; ++v) {
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      s_m[w][g] = m[g];
-      s_l[w][g] = l[g];
-    }
-  }
-  __syncthreads();
-  if (tid < G) {
-    float mx = -INFINITY;
+            for (int i = 0; i < 4; ++i) {
+              const f16x2 kp = f16x2{kd[v][2 * i], kd[v][2 * i + 1]};
+              acc = __builtin_amdgcn_fdot2(q[g][4 * v + i], kp, acc, false);
+            }
+          }
+          s[g] = acc;
+        }
 #pragma unroll
-    for (int x = 0; x < kWaves; ++x) mx = fmaxf(mx, s_m[x][tid]);
-    float sum = 0.0f;
+        for (int g = 0; g < G; ++g) s[g] = group_sum<R>(s[g]);
+        // Scores in log2 units; softcap c * tanh(x / c) (metal_kernels.py:53)
+        // as c * (1 - 2 / (e^(2x/c) + 1)).
+        if (p.softcap > 0.0f) {
 #pragma unroll
-    for (int x = 0; x < kWaves; ++x)
-      if (s_m[x][tid] != -INFINITY)
-        sum += s_l[x][tid] * __builtin_amdgcn_exp2f(s_m[x][tid] - mx);
-    s_M[tid] = mx;
-    s_L[tid] = sum;
-  }
-  __syncthreads();
-  float f[G];
+          for (int g = 0; g < G; ++g) {
+            const float e = __builtin_amdgcn_exp2f(s[g] * p.cap_in);
+            s[g] = (1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f)) * p.cap_out;
+          }
+        } else {
 #pragma unroll
-  for (int g = 0; g < G; ++g)
-    f[g] = m[g] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m[g] - s_M[g]);
+          for (int g = 0; g < G; ++g) s[g] *= p.scale_log2;
+        }
+        if (!(t0 >= first && t0 + KPS <= len)) {
+          // Boundary step. A step with no visible key is skipped: before the
+          // first visible key the running max is still -inf, and -inf - -inf
+          // would poison the sums. Rows outside [first, len) may hold
+          // anything, so their scores are masked and their values zeroed.
+          const int t = t0 + kk;
+          const bool valid = t >= first && t < len;
+          if (!__any(valid)) return;
 #pragma unroll
-  for (int x = 0; x < kWaves; ++x) {
-    if (w == x && kk == 0 && active) {
+          for (int g = 0; g < G; ++g) s[g] = valid ? s[g] : -INFINITY;
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
+          for (int v = 0; v < NV; ++v) vd[v] = zero_unless(vd[v], valid);
+        }
+        bool grow = false;
 #pragma unroll
-        for (int i = 0; i < EPL; ++i) {
-          const float val = o[g][i] * f[g];
-          float* dst = &s_o[g * D + d0 + i];
-          *dst = x == 0 ? val : *dst + val;
+        for (int g = 0; g < G; ++g) grow |= s[g] > m[g] + kSlack;
+        if (__any(grow)) {
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            const float mn = fmaxf(m[g], wave_max(s[g]));
+            const float f = __builtin_amdgcn_exp2f(m[g] - mn);
+            m[g] = mn;
+            l[g] *= f;
+#pragma unroll
+            for (int i = 0; i < EPL; ++i) o[g][i] *= f;
+          }
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const float pr = __builtin_amdgcn_exp2f(s[g] - m[g]);
+          l[g] += pr;
+#pragma unroll
+          for (int v = 0; v < NV; ++v) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+              o[g][8 * v + i] = __builtin_fmaf(pr, (float)vd[v][i], o[g][8 * v + i]);
+          }
+        }
+      };
+
+#pragma unroll
+      for (int u = 0; u < kNbuf; ++u) load_step(kb[u], vb[u]);
+      for (int j0 = 0; j0 < nsteps; j0 += kNbuf) {
+#pragma unroll
+        for (int u = 0; u < kNbuf; ++u) {
+          if (j0 + u < nsteps) compute_step(kb[u], vb[u]);
+          load_step(kb[u], vb[u]);
         }
       }
     }
-    __syncthreads();
-  }
 
-  const int nkvg = gridDim.y;
-  if (nsplit == 1) {
-    // Single split: normalise and write (metal_kernels.py:87-91).
-    for (int idx = tid; idx < G * D; idx += kThreads) {
-      const int g = idx / D;
-      const int d = idx - g * D;
-      const float sum = s_L[g];
-      const float val = sum > 0.0f ? s_o[idx] / sum : 0.0f;
-      p.out[((int64_t)b * p.hq + h0 + g) * D + d] = (f16)val;
+    // Fold the wave's key subsets (metal_kernels.py:63-81); every lane then
+    // holds the totals of its slice. The lanes of key subset kk write the
+    // heads g with g % KPS == kk.
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      l[g] = subset_sum<R>(l[g]);
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) o[g][i] = subset_sum<R>(o[g][i]);
     }
+    if (whole) {
+      // The whole unit is here: normalise and write (metal_kernels.py:87-91).
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        if (g % KPS != kk || !active) continue;
+        const float inv = l[g] > 0.0f ? 1.0f / l[g] : 0.0f;
+        f16* dst = p.out + ((int64_t)b * p.hq + h0 + g) * D + d0;
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+          f16x8 y;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) y[i] = (f16)(o[g][8 * v + i] * inv);
+          *reinterpret_cast<f16x8*>(dst + 8 * v) = y;
+        }
+      }
+    } else {
+      // Cut unit: unnormalised partial (metal_kernels.py:93-101) in this
+      // wave's slot 0 (its first unit) or 1 (its last unit).
+      const int64_t slot = (int64_t)wv * 2 + (first_unit ? 0 : 1);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        if (g % KPS != kk || !active) continue;
+        float* dst = p.part_o + (slot * G + g) * D + d0;
+#pragma unroll
+        for (int i = 0; i < EPL; i += 4)
+          *reinterpret_cast<float4*>(dst + i) =
+              make_float4(o[g][i], o[g][i + 1], o[g][i + 2], o[g][i + 3]);
+        if (r == 0) p.part_ml[slot * G + g] = make_float2(m[g], l[g]);
+      }
+    }
+
+    x += cnt;
+    first_unit = false;
+    pa = 0;
+    if (++kvg == nkvg) {
+      kvg = 0;
+      do {
+        ++b;
+      } while (b < B && s_prefix[b + 1] == s_prefix[b]);
+    }
+  }
+}
+
+// Merge kernel (metal_kernels.py:103-124): one workgroup per unit (kv head
+// group, sequence). A unit with no visible page gets zeros; a unit inside one
+// wave's range was written by the split kernel; a cut unit combines the
+// partials of the waves whose ranges cover it with log-sum-exp weights
+// (pieces whose max is -inf hold no visible key and weigh 0; a zero total
+// gives 0, :116,122). Wave w takes every fourth piece; lanes cover 64 output
+// elements at a time, so all loads of a wave go out together; the waves'
+// sums meet in LDS.
+template <int D, int G>
+__global__ __launch_bounds__(kThreads) void paged_decode_merge_kernel(const Params p) {
+  constexpr int kChunks = (D + 63) / 64;
+  __shared__ float s_acc[kWaves][G][kChunks * 64];
+  __shared__ float s_sum[kWaves][G];
+  __shared__ float s_top[G];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = tid >> 6;
+  const int kvg = blockIdx.x;
+  const int b = blockIdx.y;
+  const int kvh = kvg / p.nhg;
+  const int h0 = kvh * p.gtot + (kvg - kvh * p.nhg) * G;
+  f16* const dst = p.out + ((int64_t)b * p.hq + h0) * D;  // G x D outputs
+  const int nkvg = p.hkv * p.nhg;
+  const int pb0 = p.prefix[b];
+  const int npg = p.prefix[b + 1] - pb0;
+  if (npg == 0) {
+    for (int i = tid; i < G * D; i += kThreads) dst[i] = (f16)0.0f;
     return;
   }
-
-  // Several splits: publish the unnormalised partial (metal_kernels.py:93-101).
-  const int64_t unit = (int64_t)b * nkvg + kvg;
-  const int64_t slot = unit * p.max_splits + split;
-  float* po = p.part_o + slot * (G * D);
-  for (int idx = tid; idx < G * D; idx += kThreads) po[idx] = s_o[idx];
-  if (tid < G) p.part_ml[slot * G + tid] = make_float2(s_M[tid], s_L[tid]);
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-  __syncthreads();
-  if (tid == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(
-        &p.counters[unit], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = prev == (uint32_t)(nsplit - 1);
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-
-  // Last split to finish: log-sum-exp merge (metal_kernels.py:103-124).
-  const float2* ml = p.part_ml + unit * p.max_splits * G;
-  const float* ob = p.part_o + unit * p.max_splits * (G * D);
+  const int64_t total = (int64_t)p.prefix[p.batch] * nkvg;
+  const int waves = stream_waves(total, p);
+  const int64_t start = (int64_t)pb0 * nkvg + (int64_t)kvg * npg;
+  const int wf = wave_of(start, total, waves);
+  const int wl = wave_of(start + npg - 1, total, waves);
+  if (wf == wl) return;
+  const int nseg = wl - wf + 1;
+  // The first covering wave holds the unit in slot 0 if its range starts
+  // with the unit, else in slot 1 (its last unit); later waves in slot 0.
+  const int64_t slot0 = (int64_t)wf * 2 + (range_start(wf, total, waves) < start ? 1 : 0);
+  auto slot_of = [&](int s) { return s == 0 ? slot0 : (int64_t)(wf + s) * 2; };
   if (w == 0) {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      float mx = -INFINITY;
-      for (int s = lane; s < nsplit; s += 64) mx = fmaxf(mx, ml[s * G + g].x);
-      mx = wave_max(mx);
-      if (lane == 0) s_M[g] = mx;
+      float top = -INFINITY;
+      for (int s = lane; s < nseg; s += 64) top = fmaxf(top, p.part_ml[slot_of(s) * G + g].x);
+      top = wave_max(top);
+      if (lane == 0) s_top[g] = top;
     }
   }
   __syncthreads();
-  for (int idx = tid; idx < G * D; idx += kThreads) {
-    const int g = idx / D;
-    const int d = idx - g * D;
-    const float top = s_M[g];
-    float acc = 0.0f, sum = 0.0f;
-#pragma unroll 4
-    for (int s = 0; s < nsplit; ++s) {
-      const float2 e = ml[s * G + g];
-      if (e.x == -INFINITY) continue;
-      const float wgt = __builtin_amdgcn_exp2f(e.x - top);
-      acc = __builtin_fmaf(wgt, ob[(int64_t)s * (G * D) + idx], acc);
-      sum = __builtin_fmaf(wgt, e.y, sum);
-    }
-    const float val = sum > 0.0f ? acc / sum : 0.0f;
-    p.out[((int64_t)b * p.hq + h0 + g) * D + d] = (f16)val;
+  float acc[G][kChunks], sum[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    sum[g] = 0.0f;
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c) acc[g][c] = 0.0f;
   }
-  if (tid == 0)
-    __hip_atomic_store(&p.counters[unit], 0u, __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
+  for (int s = w; s < nseg; s += kWaves) {
+    const int64_t slot = slot_of(s);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float2 e = p.part_ml[slot * G + g];
+      const float wgt = e.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(e.x - s_top[g]);
+      sum[g] = __builtin_fmaf(wgt, e.y, sum[g]);
+#pragma unroll
+      for (int c = 0; c < kChunks; ++c) {
+        const int d = c * 64 + lane;
+        const float part = d < D ? p.part_o[(slot * G + g) * D + d] : 0.0f;
+        acc[g][c] = __builtin_fmaf(wgt, part, acc[g][c]);
+      }
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c) s_acc[w][g][c * 64 + lane] = acc[g][c];
+    if (lane == 0) s_sum[w][g] = sum[g];
+  }
+  __syncthreads();
+  for (int i = tid; i < G * D; i += kThreads) {
+    const int g = i / D;
+    const int d = i - g * D;
+    float a = 0.0f, t = 0.0f;
+#pragma unroll
+    for (int x = 0; x < kWaves; ++x) {
+      a += s_acc[x][g][d];
+      t += s_sum[x][g];
+    }
+    dst[i] = (f16)(t > 0.0f ? a / t : 0.0f);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -474,31 +607,41 @@ int ok() {
 
 using KernelFn = void (*)(Params);
 
-template <int D>
-KernelFn kernel_for_g(int g) {
-  switch (g) {
-    case 1: return paged_decode_kernel<D, 1>;
-    case 2: return paged_decode_kernel<D, 2>;
-    case 3: return paged_decode_kernel<D, 3>;
-    case 4: return paged_decode_kernel<D, 4>;
-    case 5: return paged_decode_kernel<D, 5>;
-    case 6: return paged_decode_kernel<D, 6>;
-    case 7: return paged_decode_kernel<D, 7>;
-    case 8: return paged_decode_kernel<D, 8>;
-  }
-  return nullptr;
+struct KernelPair {
+  KernelFn split = nullptr;
+  KernelFn merge = nullptr;
+};
+
+template <int D, int G>
+KernelPair pair() {
+  return {paged_decode_kernel<D, G>, paged_decode_merge_kernel<D, G>};
 }
 
-KernelFn kernel_for(int d, int g) {
-  switch (d) {
-    case 64: return kernel_for_g<64>(g);
-    case 80: return kernel_for_g<80>(g);
-    case 96: return kernel_for_g<96>(g);
-    case 128: return kernel_for_g<128>(g);
-    case 256: return kernel_for_g<256>(g);
-    case 512: return kernel_for_g<512>(g);
+template <int D>
+KernelPair kernels_for_g(int g) {
+  switch (g) {
+    case 1: return pair<D, 1>();
+    case 2: return pair<D, 2>();
+    case 3: return pair<D, 3>();
+    case 4: return pair<D, 4>();
+    case 5: return pair<D, 5>();
+    case 6: return pair<D, 6>();
+    case 7: return pair<D, 7>();
+    case 8: return pair<D, 8>();
   }
-  return nullptr;
+  return {};
+}
+
+KernelPair kernels_for(int d, int g) {
+  switch (d) {
+    case 64: return kernels_for_g<64>(g);
+    case 80: return kernels_for_g<80>(g);
+    case 96: return kernels_for_g<96>(g);
+    case 128: return kernels_for_g<128>(g);
+    case 256: return kernels_for_g<256>(g);
+    case 512: return kernels_for_g<512>(g);
+  }
+  return {};
 }
 
 int keys_per_step(int d) {
@@ -522,8 +665,9 @@ int heads_per_group(int gtot) {
 }
 
 struct Plan {
-  int G = 0, nhg = 0, split_pages = 0, max_splits = 0, pages_max = 0;
-  size_t off_ml = 0, off_o = 0, zero_bytes = 0, total = 0;
+  int G = 0, nhg = 0, min_pages = 0;
+  int64_t pages_est = 0;  // visible pages of the batch if every length = longest
+  size_t off_ml = 0, off_o = 0, total = 0;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
@@ -540,7 +684,7 @@ int make_plan(int32_t batch, int32_t q_heads, int32_t kv_heads, int32_t head_dim
                 window, split_pages);
   if (q_heads % kv_heads)
     return fail(PDA_ERR_HEAD_RATIO, "query heads must be a multiple of kv heads");
-  if (!kernel_for(head_dim, 1))
+  if (!kernels_for(head_dim, 1).split)
     return fail(PDA_ERR_HEAD_DIM,
                 "head_dim %d has no kernel (supported: 64, 80, 96, 128, 256, 512)",
                 head_dim);
@@ -551,59 +695,58 @@ int make_plan(int32_t batch, int32_t q_heads, int32_t kv_heads, int32_t head_dim
                 page_size, kps, head_dim);
   if ((int64_t)table_stride * page_size > INT32_MAX)
     return fail(PDA_ERR_TOO_LONG, "table_stride * page_size exceeds 2^31");
+  if (batch > kMaxBatch)
+    return fail(PDA_ERR_INVALID_ARGUMENT, "batch %d above %d", batch, kMaxBatch);
   Plan pl;
   const int gtot = q_heads / kv_heads;
   pl.G = heads_per_group(gtot);
   pl.nhg = gtot / pl.G;
-  if (batch > 65535 || (int64_t)kv_heads * pl.nhg > 65535)
-    return fail(PDA_ERR_INVALID_ARGUMENT, "batch or kv head count above 65535");
-  // Upper bound of visible pages of any sequence.
-  int pages_max = table_stride;
-  if (window > 0) pages_max = (int)std::min<int64_t>(pages_max, (window - 1) / page_size + 2);
-  pl.pages_max = pages_max;
-  int sp = split_pages;
-  if (sp == 0) {
-    int64_t est = pages_max;
-    if (longest > 0) est = std::min<int64_t>(est, (longest + page_size - 1) / page_size + 1);
-    const int64_t units = (int64_t)batch * kv_heads * pl.nhg;
-    const int64_t target = (int64_t)kPlanCUs * 4;
-    int64_t want = (units * est + target - 1) / target;
-    if (want < kWaves) want = kWaves;
-    if (want > kMaxSplitPages) want = kMaxSplitPages;
-    sp = (int)want;
-  }
-  if (sp > kMaxSplitPages)
-    return fail(PDA_ERR_INVALID_ARGUMENT, "split_pages %d above %d", sp, kMaxSplitPages);
-  const int64_t splits = (pages_max + sp - 1) / sp;
-  if (splits > kMaxSplits)
-    return fail(PDA_ERR_TOO_LONG, "%lld splits of %d pages exceed %d",
-                (long long)splits, sp, kMaxSplits);
-  pl.split_pages = sp;
-  pl.max_splits = (int)splits;
-  const size_t units = (size_t)batch * kv_heads * pl.nhg;
-  if (units > kMaxUnits)
-    return fail(PDA_ERR_INVALID_ARGUMENT,
-                "batch * kv_heads * head groups = %zu above %d", units, kMaxUnits);
-  // Layout: a fixed counter header (the same for every shape, so counters
-  // left at zero by one call are zero for the next call of any shape), then
-  // the (max, sum) pairs and the unnormalised partial outputs.
-  pl.zero_bytes = kCounterBytes;
-  pl.off_ml = kCounterBytes;
-  const size_t ml_bytes = align256(units * pl.max_splits * pl.G * sizeof(float2));
-  pl.off_o = pl.off_ml + ml_bytes;
-  const size_t o_bytes =
-      align256(units * pl.max_splits * (size_t)pl.G * head_dim * sizeof(float));
-  // Sequences with one split never touch the partials, but any may split.
-  pl.total = pl.max_splits > 1 ? pl.off_o + o_bytes : kCounterBytes;
+  if ((int64_t)kv_heads * pl.nhg > 65535)
+    return fail(PDA_ERR_INVALID_ARGUMENT, "kv heads x head groups above 65535");
+  // Visible pages of one sequence are bounded by the table width and, with a
+  // window, by the pages a window can touch.
+  int64_t pages_max = table_stride;
+  if (window > 0) pages_max = std::min<int64_t>(pages_max, (window - 1) / page_size + 2);
+  if ((int64_t)batch * pages_max * kv_heads * pl.nhg > INT32_MAX)
+    return fail(PDA_ERR_TOO_LONG, "more than 2^31 visible pages in one call");
+  int64_t est = pages_max;
+  if (longest > 0) est = std::min<int64_t>(est, (longest + page_size - 1) / page_size + 1);
+  pl.pages_est = (int64_t)batch * kv_heads * pl.nhg * est;
+  pl.min_pages = split_pages > 0 ? split_pages : kMinPagesPerWave;
+  // Workspace: the per-sequence page prefix, the (max, sum) pairs and the
+  // unnormalised partial outputs of the cut units (two slots per wave).
+  pl.off_ml = align256((size_t)(batch + 1) * sizeof(int32_t));
+  pl.off_o = pl.off_ml + align256((size_t)kSlots * pl.G * sizeof(float2));
+  pl.total = pl.off_o + align256((size_t)kSlots * pl.G * head_dim * sizeof(float));
   *out = pl;
   return PDA_OK;
+}
+
+// Resident workgroups of a split kernel on the current device (cached).
+int resident_groups(KernelFn fn, size_t lds_bytes) {
+  static std::mutex mu;
+  static std::map<std::pair<int, std::pair<const void*, size_t>>, int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return -1;
+  const auto key = std::make_pair(dev, std::make_pair((const void*)fn, lds_bytes));
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache.find(key);
+  if (it != cache.end()) return it->second;
+  int cus = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(fn),
+                                                   kThreads, lds_bytes) != hipSuccess)
+    return -1;
+  const int groups = std::max(1, std::min(kMaxGroups, cus * std::max(1, per_cu)));
+  cache[key] = groups;
+  return groups;
 }
 
 }  // namespace
 
 extern "C" {
 
-int pda_version(void) { return (0 << 16) | 1; }
+int pda_version(void) { return (0 << 16) | 2; }
 
 const char* pda_last_error(void) { return g_error; }
 
@@ -620,24 +763,19 @@ int pda_workspace_bytes(int32_t batch, int32_t q_heads, int32_t kv_heads,
   return ok();
 }
 
-int pda_workspace_zero_bytes(size_t* bytes) {
-  if (!bytes) return fail(PDA_ERR_INVALID_ARGUMENT, "bytes is null");
-  *bytes = kCounterBytes;
-  return ok();
-}
-
 int pda_plan(int32_t batch, int32_t q_heads, int32_t kv_heads,
              int32_t head_dim, int32_t page_size, int32_t table_stride,
              int32_t longest, int32_t window, int32_t split_pages,
-             int32_t* pages_per_split, int32_t* max_splits) {
-  if (!pages_per_split || !max_splits)
+             int32_t* waves, int32_t* pages_per_wave) {
+  if (!waves || !pages_per_wave)
     return fail(PDA_ERR_INVALID_ARGUMENT, "output pointer is null");
   Plan pl;
   const int rc = make_plan(batch, q_heads, kv_heads, head_dim, page_size,
                            table_stride, longest, window, split_pages, &pl);
   if (rc) return rc;
-  *pages_per_split = pl.split_pages;
-  *max_splits = pl.max_splits;
+  const int64_t want = (pl.pages_est + pl.min_pages - 1) / pl.min_pages;
+  *waves = (int32_t)std::max<int64_t>(1, std::min<int64_t>(want, kMaxWaves));
+  *pages_per_wave = (int32_t)((pl.pages_est + *waves - 1) / *waves);
   return ok();
 }
 
@@ -675,6 +813,11 @@ int pda_paged_decode_attention(const void* queries, const void* keys,
   if ((uintptr_t)workspace & 255)
     return fail(PDA_ERR_ALIGNMENT, "workspace must be 256-byte aligned");
 
+  const KernelPair kp = kernels_for(head_dim, pl.G);
+  const size_t lds = (size_t)(2 * batch + 1) * sizeof(int32_t);
+  const int groups = resident_groups(kp.split, lds);
+  if (groups < 0) return fail(PDA_ERR_HIP, "device query failed");
+
   Params prm;
   prm.q = static_cast<const f16*>(queries);
   prm.k = static_cast<const f16*>(keys);
@@ -683,10 +826,11 @@ int pda_paged_decode_attention(const void* queries, const void* keys,
   prm.lengths = lengths;
   prm.out = static_cast<f16*>(out);
   char* ws = static_cast<char*>(workspace);
-  prm.counters = reinterpret_cast<uint32_t*>(ws);
+  prm.prefix = reinterpret_cast<int32_t*>(ws);
   prm.part_ml = reinterpret_cast<float2*>(ws + pl.off_ml);
   prm.part_o = reinterpret_cast<float*>(ws + pl.off_o);
   prm.arena_pages = arena_rows / page_size;
+  prm.batch = batch;
   prm.table_stride = table_stride;
   prm.page_size = page_size;
   prm.hq = q_heads;
@@ -694,18 +838,20 @@ int pda_paged_decode_attention(const void* queries, const void* keys,
   prm.gtot = q_heads / kv_heads;
   prm.nhg = pl.nhg;
   prm.window = window;
-  prm.split_pages = pl.split_pages;
-  prm.max_splits = pl.max_splits;
-  prm.scale = scale;
+  prm.grid_waves = groups * kWaves;
+  prm.min_pages = pl.min_pages;
   prm.scale_log2 = scale * kLog2e;
   prm.softcap = softcap;
+  prm.cap_in = softcap > 0.0f ? 2.0f * kLog2e * scale / softcap : 0.0f;
+  prm.cap_out = softcap * kLog2e;
 
-  KernelFn fn = kernel_for(head_dim, pl.G);
-  const dim3 grid(pl.max_splits, kv_heads * pl.nhg, batch);
-  const dim3 block(kThreads);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
   void* args[] = {&prm};
-  hipError_t err = hipLaunchKernel(reinterpret_cast<const void*>(fn), grid, block,
-                                   args, 0, static_cast<hipStream_t>(stream));
+  hipError_t err = hipLaunchKernel(reinterpret_cast<const void*>(kp.split), dim3(groups),
+                                   dim3(kThreads), args, lds, st);
+  if (err == hipSuccess)
+    err = hipLaunchKernel(reinterpret_cast<const void*>(kp.merge),
+                          dim3(kv_heads * pl.nhg, batch), dim3(kThreads), args, 0, st);
   if (err != hipSuccess)
     return fail(PDA_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(err));
   return ok();

@@ -34,7 +34,6 @@ SIGNATURES = {
         ctypes.c_int,
         [c_int32] * 9 + [ctypes.POINTER(c_size_t)],
     ),
-    "pda_workspace_zero_bytes": (ctypes.c_int, [ctypes.POINTER(c_size_t)]),
     "pda_plan": (
         ctypes.c_int,
         [c_int32] * 9 + [ctypes.POINTER(c_int32), ctypes.POINTER(c_int32)],
@@ -93,12 +92,6 @@ def workspace_bytes(batch, q_heads, kv_heads, head_dim, page_size, table_stride,
     check(library().pda_workspace_bytes(batch, q_heads, kv_heads, head_dim, page_size,
                                         table_stride, longest, window, split_pages,
                                         ctypes.byref(out)))
-    return out.value
-
-
-def workspace_zero_bytes() -> int:
-    out = c_size_t(0)
-    check(library().pda_workspace_zero_bytes(ctypes.byref(out)))
     return out.value
 
 

@@ -27,11 +27,9 @@ _workspaces: dict[tuple[int, int], torch.Tensor] = {}
 
 
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """A cached, 256-byte aligned device workspace of at least ``nbytes``.
-
-    Its fixed header holds split counters that must start at zero and that
-    every call returns to zero, whatever its shape, so a buffer is zeroed once
-    when it is created and then reused by calls of any shape."""
+    """A cached, 256-byte aligned device workspace of at least ``nbytes``,
+    grown on demand and shared by calls of any shape (it holds nothing
+    between calls)."""
     index = device.index if device.index is not None else torch.cuda.current_device()
     key = (index, 0)
     buf = _workspaces.get(key)
@@ -39,7 +37,7 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
         size = max(nbytes, 1 << 20)
         if buf is not None:
             size = max(size, 2 * buf.numel())
-        buf = torch.zeros(size, dtype=torch.uint8, device=device)
+        buf = torch.empty(size, dtype=torch.uint8, device=device)
         _workspaces[key] = buf
     return buf
 

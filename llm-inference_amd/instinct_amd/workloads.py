@@ -51,7 +51,11 @@ class Workload:
 
     @property
     def longest(self) -> int:
-        return int(self.lengths.max().item()) if self.batch else 0
+        """Largest length (the reference's host-side ``longest``), computed
+        once: callers pass it on every call without a device sync."""
+        if "longest" not in self.meta:
+            self.meta["longest"] = int(self.lengths.max().item()) if self.batch else 0
+        return self.meta["longest"]
 
     def spans(self) -> np.ndarray:
         n = self.lengths.cpu().numpy().astype(np.int64)
@@ -228,14 +232,16 @@ def config5(device="cpu", seed=5, batch=256, low=16, high=65536, shared=64,
             prefix=2048) -> Workload:
     """Continuous-batching mix: B=256, 32/8 heads, D=128, P=16, lengths
     log-uniform in [16, 65536]; ``shared`` sequences map logical pages
-    0..prefix/P-1 onto the same physical pages 0..prefix/P-1 (their lengths
-    are redrawn above the prefix so all of it is visible)."""
+    0..prefix/P-1 onto the same physical pages 0..prefix/P-1. Their lengths
+    are redrawn log-uniformly in (prefix, 65536] so the whole prefix is
+    visible."""
     rng = np.random.default_rng(seed)
     P = 16
     lengths = np.floor(np.exp(rng.uniform(math.log(low), math.log(high), batch))).astype(np.int64)
     lengths = np.clip(lengths, low, high)
     sharers = rng.choice(batch, size=shared, replace=False)
-    lengths[sharers] = rng.integers(prefix + 1, high + 1, shared)
+    lengths[sharers] = np.clip(np.floor(np.exp(rng.uniform(
+        math.log(prefix + 1), math.log(high), shared))).astype(np.int64), prefix + 1, high)
     prefix_pages = prefix // P
     need_private = []
     for b in range(batch):

@@ -56,12 +56,13 @@ def decode(**overrides):
     (dict(arena_rows=8), _lib.PDA_ERR_INVALID_ARGUMENT),
     (dict(scale=float("nan")), _lib.PDA_ERR_INVALID_ARGUMENT),
     (dict(softcap=-1.0), _lib.PDA_ERR_INVALID_ARGUMENT),
-    (dict(split_pages=65), _lib.PDA_ERR_INVALID_ARGUMENT),
+    (dict(batch=9000), _lib.PDA_ERR_INVALID_ARGUMENT),
     (dict(keys=FAKE + 2), _lib.PDA_ERR_ALIGNMENT),
     (dict(out=FAKE + 8), _lib.PDA_ERR_ALIGNMENT),
     (dict(lengths=FAKE + 2), _lib.PDA_ERR_ALIGNMENT),
     (dict(workspace=None), _lib.PDA_ERR_WORKSPACE),
     (dict(workspace_bytes=16), _lib.PDA_ERR_WORKSPACE),
+    (dict(batch=1, workspace=None, workspace_bytes=0), _lib.PDA_ERR_WORKSPACE),
     (dict(workspace=FAKE + 64), _lib.PDA_ERR_ALIGNMENT),
     (dict(table_stride=1 << 28), _lib.PDA_ERR_TOO_LONG),
 ])
@@ -81,32 +82,31 @@ def test_empty_batch_is_a_no_op():
 
 
 def test_workspace_and_plan_are_consistent():
-    pages, splits = _lib.plan(64, 28, 4, 128, 16, 512, 8192, 0)
-    assert 4 <= pages <= 64 and splits == -(-512 // pages)
-    need = _lib.workspace_bytes(64, 28, 4, 128, 16, 512, 8192, 0)
-    zero = _lib.workspace_zero_bytes()
-    assert zero == 65536 * 4  # fixed header: one uint32 per (seq, kv head, head group)
-    units = 64 * 4
-    assert need >= zero + units * splits * 7 * (128 + 2) * 4
-    # A forced split size changes the plan but never below the data it needs.
-    assert _lib.plan(64, 28, 4, 128, 16, 512, 8192, 0, split_pages=8) == (8, 64)
+    waves, per_wave = _lib.plan(64, 28, 4, 128, 16, 512, 8192, 0)
+    assert waves == 2048 and per_wave * waves >= 64 * 4 * 512
+    # Few pages: the stream uses fewer waves, each with at least split_pages pages.
+    assert _lib.plan(1, 8, 8, 128, 16, 64, 64, 0) == (5, 8)
+    assert _lib.plan(1, 8, 8, 128, 16, 64, 64, 0, split_pages=2) == (20, 2)
     # A window bounds the visible pages whatever the table width.
-    assert _lib.plan(32, 8, 4, 256, 16, 2048, 32768, 1024, split_pages=16) == (16, 5)
-    # One split needs no partials, only the header.
-    assert _lib.workspace_bytes(2, 8, 8, 64, 16, 4, 64, 0, split_pages=4) == zero
-    # More than 8 heads per kv head are served by several head groups.
-    one = _lib.workspace_bytes(2, 8, 1, 128, 16, 64, 1024, 0, split_pages=4)
-    two = _lib.workspace_bytes(2, 16, 1, 128, 16, 64, 1024, 0, split_pages=4)
-    assert two - zero == 2 * (one - zero)
+    assert _lib.plan(32, 8, 4, 256, 16, 2048, 32768, 1024, split_pages=16)[0] == 32 * 4 * 65 // 16
+    need = _lib.workspace_bytes(64, 28, 4, 128, 16, 512, 8192, 0)
+    slots = 2 * 2048
+    assert need >= 65 * 4 + slots * 7 * (128 + 2) * 4
+    # The workspace does not grow with the context length.
+    assert _lib.workspace_bytes(64, 28, 4, 128, 16, 8192, 131072, 0) == need
+    # More than 8 heads per kv head are served by several head groups (8 each).
+    one = _lib.workspace_bytes(2, 8, 1, 128, 16, 64, 1024, 0)
+    two = _lib.workspace_bytes(2, 16, 1, 128, 16, 64, 1024, 0)
+    assert two == one
 
 
-def test_too_many_counter_units_are_rejected():
+def test_batch_limit():
     with pytest.raises(_lib.PdaError) as err:
-        _lib.workspace_bytes(65535, 16, 2, 128, 16, 64, 1024, 0)
+        _lib.workspace_bytes(8192, 16, 2, 128, 16, 64, 1024, 0)
     assert err.value.code == _lib.PDA_ERR_INVALID_ARGUMENT
 
 
-def test_split_count_limit():
+def test_page_count_limit():
     with pytest.raises(_lib.PdaError) as err:
-        _lib.plan(1, 8, 8, 128, 16, 1 << 20, 1 << 24, 0, split_pages=16)
+        _lib.plan(4096, 64, 8, 128, 16, 1 << 24, 1 << 28, 0)
     assert err.value.code == _lib.PDA_ERR_TOO_LONG
