@@ -109,6 +109,26 @@ int pda_paged_decode_attention(const void* queries, const void* keys,
                                int32_t split_pages, void* workspace,
                                size_t workspace_bytes, void* stream);
 
+/* The two passes of pda_paged_decode_attention, for callers that schedule or
+ * time them separately; the reference's host wrapper launches the same two
+ * kernels (metal_kernels.py:228-239 split, :240-247 merge). Call
+ * pda_decode_split, then pda_decode_merge with the same arguments on the same
+ * stream (or after it); the output is complete only after the merge. */
+int pda_decode_split(const void* queries, const void* keys, const void* values,
+                     const int32_t* tables, const int32_t* lengths, void* out,
+                     int32_t batch, int32_t q_heads, int32_t kv_heads,
+                     int32_t head_dim, int32_t page_size, int32_t table_stride,
+                     int64_t arena_rows, int32_t longest, float scale,
+                     int32_t window, float softcap, int32_t split_pages,
+                     void* workspace, size_t workspace_bytes, void* stream);
+int pda_decode_merge(const void* queries, const void* keys, const void* values,
+                     const int32_t* tables, const int32_t* lengths, void* out,
+                     int32_t batch, int32_t q_heads, int32_t kv_heads,
+                     int32_t head_dim, int32_t page_size, int32_t table_stride,
+                     int64_t arena_rows, int32_t longest, float scale,
+                     int32_t window, float softcap, int32_t split_pages,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

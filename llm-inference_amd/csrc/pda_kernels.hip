@@ -779,16 +779,20 @@ int pda_plan(int32_t batch, int32_t q_heads, int32_t kv_heads,
   return ok();
 }
 
-int pda_paged_decode_attention(const void* queries, const void* keys,
-                               const void* values, const int32_t* tables,
-                               const int32_t* lengths, void* out,
-                               int32_t batch, int32_t q_heads,
-                               int32_t kv_heads, int32_t head_dim,
-                               int32_t page_size, int32_t table_stride,
-                               int64_t arena_rows, int32_t longest,
-                               float scale, int32_t window, float softcap,
-                               int32_t split_pages, void* workspace,
-                               size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+constexpr int kPassSplit = 1;
+constexpr int kPassMerge = 2;
+
+// Validates, plans and launches the split pass, the merge pass or both.
+int decode(int passes, const void* queries, const void* keys, const void* values,
+           const int32_t* tables, const int32_t* lengths, void* out, int32_t batch,
+           int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t page_size,
+           int32_t table_stride, int64_t arena_rows, int32_t longest, float scale,
+           int32_t window, float softcap, int32_t split_pages, void* workspace,
+           size_t workspace_bytes, void* stream) {
   Plan pl;
   int rc = make_plan(batch, q_heads, kv_heads, head_dim, page_size, table_stride,
                      longest, window, split_pages, &pl);
@@ -847,14 +851,40 @@ int pda_paged_decode_attention(const void* queries, const void* keys,
 
   const hipStream_t st = static_cast<hipStream_t>(stream);
   void* args[] = {&prm};
-  hipError_t err = hipLaunchKernel(reinterpret_cast<const void*>(kp.split), dim3(groups),
-                                   dim3(kThreads), args, lds, st);
-  if (err == hipSuccess)
+  hipError_t err = hipSuccess;
+  if (passes & kPassSplit)
+    err = hipLaunchKernel(reinterpret_cast<const void*>(kp.split), dim3(groups),
+                          dim3(kThreads), args, lds, st);
+  if (err == hipSuccess && (passes & kPassMerge))
     err = hipLaunchKernel(reinterpret_cast<const void*>(kp.merge),
                           dim3(kv_heads * pl.nhg, batch), dim3(kThreads), args, 0, st);
   if (err != hipSuccess)
     return fail(PDA_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(err));
   return ok();
 }
+
+}  // namespace
+
+extern "C" {
+
+#define PDA_DECODE_PARAMS                                                      \
+  const void *queries, const void *keys, const void *values,                   \
+      const int32_t *tables, const int32_t *lengths, void *out, int32_t batch, \
+      int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t page_size,  \
+      int32_t table_stride, int64_t arena_rows, int32_t longest, float scale,  \
+      int32_t window, float softcap, int32_t split_pages, void *workspace,     \
+      size_t workspace_bytes, void *stream
+#define PDA_DECODE_ARGS                                                        \
+  queries, keys, values, tables, lengths, out, batch, q_heads, kv_heads,       \
+      head_dim, page_size, table_stride, arena_rows, longest, scale, window,   \
+      softcap, split_pages, workspace, workspace_bytes, stream
+
+int pda_paged_decode_attention(PDA_DECODE_PARAMS) {
+  return decode(kPassSplit | kPassMerge, PDA_DECODE_ARGS);
+}
+
+int pda_decode_split(PDA_DECODE_PARAMS) { return decode(kPassSplit, PDA_DECODE_ARGS); }
+
+int pda_decode_merge(PDA_DECODE_PARAMS) { return decode(kPassMerge, PDA_DECODE_ARGS); }
 
 }  // extern "C"

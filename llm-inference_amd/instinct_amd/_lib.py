@@ -38,13 +38,12 @@ SIGNATURES = {
         ctypes.c_int,
         [c_int32] * 9 + [ctypes.POINTER(c_int32), ctypes.POINTER(c_int32)],
     ),
-    "pda_paged_decode_attention": (
-        ctypes.c_int,
-        [c_void_p] * 6
-        + [c_int32] * 6
-        + [c_int64, c_int32, c_float, c_int32, c_float, c_int32, c_void_p, c_size_t, c_void_p],
-    ),
 }
+_DECODE_ARGS = ([c_void_p] * 6 + [c_int32] * 6
+                + [c_int64, c_int32, c_float, c_int32, c_float, c_int32, c_void_p, c_size_t,
+                   c_void_p])
+for _name in ("pda_paged_decode_attention", "pda_decode_split", "pda_decode_merge"):
+    SIGNATURES[_name] = (ctypes.c_int, _DECODE_ARGS)
 
 _lib: ctypes.CDLL | None = None
 

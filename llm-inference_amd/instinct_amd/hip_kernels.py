@@ -57,10 +57,13 @@ def paged_decode_attention(
     scales: tuple[Any, Any] | None = None,
     split_pages: int = 0,
     out: torch.Tensor | None = None,
+    passes: str = "both",
 ) -> torch.Tensor:
     """Attention for one new token per sequence over its paged keys
-    (metal_kernels.py:164-186). ``split_pages`` (0 = planner's choice) forces
-    the pages per split; the result does not depend on it."""
+    (metal_kernels.py:164-186). ``split_pages`` is the fewest pages a wave
+    reads before the batch is spread over fewer waves (0 = default); the
+    result does not depend on it. ``passes`` = "split" or "merge" launches
+    one of the two kernels only (the output is complete after the merge)."""
     if scales is not None:
         raise NotImplementedError("8-bit K/V (scales) has no MI355X kernel yet")
     batch, q_heads, head_dim = (int(n) for n in queries.shape)
@@ -92,7 +95,9 @@ def paged_decode_attention(
                                 int(longest), int(window), int(split_pages))
     ws = workspace(device, need)
     stream = torch.cuda.current_stream(device).cuda_stream
-    rc = _lib.library().pda_paged_decode_attention(
+    entry = {"both": "pda_paged_decode_attention", "split": "pda_decode_split",
+             "merge": "pda_decode_merge"}[passes]
+    rc = getattr(_lib.library(), entry)(
         queries.data_ptr(), keys.data_ptr(), values.data_ptr(), tables.data_ptr(),
         lengths.data_ptr(), out.data_ptr(), batch, q_heads, kv_heads, head_dim,
         int(page_size), stride, int(keys.shape[0]), int(longest), float(scale),

@@ -232,6 +232,20 @@ def test_repeated_calls_reuse_the_workspace(gpu):
     assert_parity(first, ea, "alt-a")
 
 
+def test_separate_passes_equal_the_combined_call(gpu):
+    """pda_decode_split then pda_decode_merge == pda_paged_decode_attention."""
+    w = workloads.config2(device=gpu, batch=12, low=300, high=5000)
+    combined = run(w)
+    kw = dict(page_size=w.page_size, longest=w.longest, scale=w.scale)
+    out = torch.full_like(w.q, float("nan"))
+    paged_decode_attention(w.q, w.keys, w.values, w.tables, w.lengths, out=out,
+                           passes="split", **kw)
+    paged_decode_attention(w.q, w.keys, w.values, w.tables, w.lengths, out=out,
+                           passes="merge", **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(out, combined)
+
+
 def test_one_workspace_serves_shapes_with_different_layouts(gpu):
     """Regression: a window/D=256 call with few units leaves float partials
     where a larger batch keeps its split counters unless the counters live in
