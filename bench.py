@@ -46,6 +46,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
     ap.add_argument("--split-pages", type=int, default=0)
+    ap.add_argument("--layout", choices=["pages", "rows"], default="pages",
+                    help="K/V arena layout: page tiles (MI355X) or the reference's rows")
     ap.add_argument("--no-flush", action="store_true", help="skip the flushed pass")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="approximate CPU time budget of the CPU-baseline sample")
@@ -153,7 +155,7 @@ def main():
 
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
-    w = workloads.CONFIGS[args.config](device=device)
+    w = workloads.CONFIGS[args.config](device=device).to_layout(args.layout)
     kv_bytes = w.kv_bytes()
     out = torch.empty_like(w.q)
 
@@ -216,6 +218,7 @@ def main():
             "workload": w.name,
             "batch": w.batch, "q_heads": w.q_heads, "kv_heads": w.kv_heads,
             "head_dim": w.head_dim, "page_size": w.page_size, "window": w.window,
+            "layout": w.layout,
             "longest": w.longest, "kv_bytes": kv_bytes,
             "split_pages": args.split_pages, "stream_waves_max": waves,
             "cache": "warm (no flush)" if args.no_flush else "flushed (1 GiB write + 1 GiB read between calls)",

@@ -13,13 +13,22 @@
  *   attention layer per decode step from DecodeBatch.attend
  *   (python/instinct/batches.py:203-226).
  *
- * Layouts (identical to the reference's KVCache, paged_kv.py:156-292):
+ * Layouts:
  *   queries  [batch, q_heads, head_dim]            fp16
- *   keys     [arena_rows, kv_heads, head_dim]      fp16, one layer's arena
- *   values   [arena_rows, kv_heads, head_dim]      fp16
+ *   keys, values: one layer's K/V arena, fp16, in one of two layouts:
+ *     PDA_LAYOUT_ROWS   [arena_rows, kv_heads, head_dim] — the reference's
+ *                       KVCache arena (paged_kv.py:156-292); a page is
+ *                       page_size consecutive rows
+ *     PDA_LAYOUT_PAGES  [arena_rows / page_size, kv_heads, page_size,
+ *                       head_dim] — page tiles: the page_size rows of one
+ *                       (page, kv head) are contiguous (4 KiB at head_dim 128,
+ *                       page 16), so the kernel reads whole tiles; the same
+ *                       logical rows, permuted within each page
  *   tables   [batch, table_stride]                 int32, physical page ids;
  *            row of logical position t = tables[b][t / page_size] * page_size
- *            + t % page_size (paged_kv.py:259-265, metal_kernels.py:47)
+ *            + t % page_size (paged_kv.py:259-265, metal_kernels.py:47); in
+ *            the page layout that row lives in tile [row / page_size][kv head],
+ *            slot row % page_size
  *   lengths  [batch]                               int32, keys per sequence,
  *            the new token included (batches.py:162-164)
  *   out      [batch, q_heads, head_dim]            fp16
@@ -56,6 +65,10 @@ extern "C" {
 #define PDA_ERR_ALIGNMENT (-6)        /* fp16 buffers must be 16-byte aligned */
 #define PDA_ERR_TOO_LONG (-7)         /* context beyond the split planner     */
 #define PDA_ERR_HIP (-8)              /* a HIP runtime call failed            */
+
+/* K/V arena layouts (the `layout` argument of the decode calls). */
+#define PDA_LAYOUT_ROWS 0  /* [rows, kv_heads, head_dim], the reference's   */
+#define PDA_LAYOUT_PAGES 1 /* [pages, kv_heads, page_size, head_dim] tiles  */
 
 /* Library version, (major << 16) | minor. No reference counterpart. */
 int pda_version(void);
@@ -95,7 +108,9 @@ int pda_plan(int32_t batch, int32_t q_heads, int32_t kv_heads,
  * (a planning hint only: results never depend on it, and lengths above it
  * stay correct). `split_pages` is the fewest pages a wave reads before the
  * stream is spread over fewer waves (0 = 8; results do not depend on it).
- * `arena_rows` is the row count of the keys/values arenas; batch <= 8191.
+ * `arena_rows` is the row count of the keys/values arenas (pages x
+ * page_size) and `layout` is PDA_LAYOUT_ROWS or PDA_LAYOUT_PAGES (the reference
+ * has one layout, rows); batch <= 8184.
  * Launches a split kernel and a merge kernel on `stream`; calls that share a
  * workspace must not overlap. */
 int pda_paged_decode_attention(const void* queries, const void* keys,
@@ -104,8 +119,9 @@ int pda_paged_decode_attention(const void* queries, const void* keys,
                                int32_t batch, int32_t q_heads,
                                int32_t kv_heads, int32_t head_dim,
                                int32_t page_size, int32_t table_stride,
-                               int64_t arena_rows, int32_t longest,
-                               float scale, int32_t window, float softcap,
+                               int64_t arena_rows, int32_t layout,
+                               int32_t longest, float scale, int32_t window,
+                               float softcap,
                                int32_t split_pages, void* workspace,
                                size_t workspace_bytes, void* stream);
 
@@ -118,15 +134,17 @@ int pda_decode_split(const void* queries, const void* keys, const void* values,
                      const int32_t* tables, const int32_t* lengths, void* out,
                      int32_t batch, int32_t q_heads, int32_t kv_heads,
                      int32_t head_dim, int32_t page_size, int32_t table_stride,
-                     int64_t arena_rows, int32_t longest, float scale,
-                     int32_t window, float softcap, int32_t split_pages,
+                     int64_t arena_rows, int32_t layout, int32_t longest,
+                     float scale, int32_t window, float softcap,
+                     int32_t split_pages,
                      void* workspace, size_t workspace_bytes, void* stream);
 int pda_decode_merge(const void* queries, const void* keys, const void* values,
                      const int32_t* tables, const int32_t* lengths, void* out,
                      int32_t batch, int32_t q_heads, int32_t kv_heads,
                      int32_t head_dim, int32_t page_size, int32_t table_stride,
-                     int64_t arena_rows, int32_t longest, float scale,
-                     int32_t window, float softcap, int32_t split_pages,
+                     int64_t arena_rows, int32_t layout, int32_t longest,
+                     float scale, int32_t window, float softcap,
+                     int32_t split_pages,
                      void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus

@@ -7,16 +7,24 @@
 // keys are [max(0, len - window), len), pages with a negative id are masked.
 //
 // MI355X design (not a translation of the Metal kernel):
-//  * Stream-K split. A unit is (sequence, kv head group); the visible pages of
-//    all units, in order, form one stream of T pages. A persistent grid of W
-//    resident wave64s takes equal contiguous ranges of that stream, so every
-//    wave reads the same number of K/V bytes whatever the mix of context
-//    lengths (the reference splits every sequence by the longest one,
-//    metal_kernels.py:193-194). A unit that lies inside one wave's range is
-//    normalised and written by that wave (as _SINGLE_WRITE); a unit cut by a
-//    range boundary leaves unnormalised partials (as _SPLIT_WRITE) that the
-//    merge kernel combines (as _DECODE_MERGE). A wave cuts at most the first
-//    and the last unit of its range, so there are at most 2 W partials.
+//  * Stream split. A unit is (sequence, kv head group); the visible pages of
+//    all units, in order, form one stream of T pages. A persistent grid of
+//    eight-wave workgroups (one per CU at two waves per SIMD) cuts the stream
+//    into equal contiguous ranges, one per wave pair. The two waves of a pair
+//    share a SIMD (waves i and i + 4 of a workgroup); the SIMD's issue arbiter
+//    favours the older of two waves, which then streams up to ~20% faster, so
+//    a fixed split would leave half the waves idle at the end. The pair
+//    therefore takes its range from both ends, the first wave forward and the
+//    second backward, one page per ticket of a shared LDS counter, and meets
+//    wherever the tickets run out. Each wave still ends with one contiguous
+//    range, cut by the meeting point instead of a fixed boundary (the
+//    reference splits every sequence by the longest one,
+//    metal_kernels.py:193-194).
+//  * A unit that lies inside one wave's range is normalised and written by
+//    that wave (as _SINGLE_WRITE); a unit cut by a range boundary leaves
+//    unnormalised partials (as _SPLIT_WRITE) in one of the wave's two slots,
+//    which the merge kernel combines (as _DECODE_MERGE). The first wave of
+//    each pair records the meeting point for the merge.
 //  * Inside a wave, R lanes share one key row (R = head_dim / EPL, EPL = 8 or
 //    16 fp16 per lane, i.e. one or two 16-byte loads per lane per row), so a
 //    wave covers 64 / R keys per step. Every step reads K and V rows once and
@@ -26,7 +34,8 @@
 //  * Online softmax in the log2 domain with a lazy running max: the
 //    accumulators are rescaled only when a score exceeds the running max by
 //    more than 2^8, so steady-state steps do no rescaling.
-//  * K/V loads run NBUF steps ahead of the math through a register ring.
+//  * K/V loads run NBUF steps ahead of the math through a register ring, and
+//    the ticket for the next page is taken one page ahead.
 //  * No cross-workgroup synchronisation: the split kernel only writes, the
 //    merge kernel runs after it on the same stream.
 
@@ -55,15 +64,18 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 constexpr float kLog2e = 1.44269504088896340736f;
 // Lazy rescale threshold (log2 units): probabilities stay below 2^8.
 constexpr float kSlack = 8.0f;
-constexpr int kWaves = 4;              // waves per workgroup
-constexpr int kThreads = kWaves * 64;
-constexpr int kNbuf = 2;               // K/V steps in flight per wave
-constexpr int kTablePages = 64;        // page-table entries held per VGPR refill
-constexpr int kMaxGroups = 512;        // resident workgroups (MI355X: 256 CUs x 2)
-constexpr int kMaxWaves = kMaxGroups * kWaves;
-constexpr int kSlots = 2 * kMaxWaves;  // partial slots: first and last unit of a wave
-constexpr int kMinPagesPerWave = 8;    // default: spread no thinner than this
-constexpr int kMaxBatch = 8191;        // per-sequence tables in LDS: (2B + 1) ints
+constexpr int kSplitWaves = 8;                 // waves per split workgroup
+constexpr int kSplitThreads = kSplitWaves * 64;
+constexpr int kPairs = kSplitWaves / 2;        // wave pairs per workgroup
+constexpr int kNbuf = 2;                       // K/V steps in flight per wave
+constexpr int kTablePages = 64;                // page-table entries held per VGPR refill
+constexpr int kMaxGroups = 512;                // resident split workgroups (256 CUs x 2)
+constexpr int kMaxWaves = kMaxGroups * kSplitWaves;
+constexpr int kMaxPairs = kMaxWaves / 2;
+constexpr int kSlots = 2 * kMaxWaves;          // partial slots: first and last unit of a wave
+constexpr int kMinPagesPerWave = 8;            // default: spread no thinner than this
+constexpr int kMaxBatch = 8184;                // per-sequence tables in LDS: (2B + 1) ints
+constexpr int kMergeMaxWaves = 16;             // waves per merge workgroup, at most
 
 struct Params {
   const f16* q;
@@ -73,9 +85,13 @@ struct Params {
   const int32_t* lengths;
   f16* out;
   int32_t* prefix;    // [B + 1] visible pages before each sequence (workspace)
+  int32_t* meet;      // [pairs] pages the first wave of each pair took (workspace)
   float2* part_ml;    // [kSlots][G] (running max, sum) of cut units
   float* part_o;      // [kSlots][G][D] unnormalised outputs of cut units
   int64_t arena_pages;
+  int64_t page_bytes; // K/V arena: bytes between pages,
+  int32_t head_bytes; //   between kv heads of one page,
+  int32_t row_bytes;  //   between rows (keys) of one page and kv head
   int32_t batch;
   int32_t table_stride;
   int32_t page_size;
@@ -84,8 +100,8 @@ struct Params {
   int32_t gtot;       // query heads per kv head
   int32_t nhg;        // head groups per kv head (gtot / G)
   int32_t window;
-  int32_t grid_waves; // waves of the split kernel's grid
-  int32_t min_pages;  // fewest pages per wave before the stream uses fewer waves
+  int32_t grid_pairs; // wave pairs of the split kernel's grid
+  int32_t min_pages;  // fewest pages per wave before the stream uses fewer pairs
   float scale_log2;   // scale * log2(e)
   float softcap;      // 0 = off
   float cap_in;       // 2 * log2(e) * scale / softcap
@@ -98,14 +114,19 @@ constexpr int next_pow2(int x) {
   return p;
 }
 
+// Lane geometry of a head_dim. R lanes share one key; each active lane holds
+// EPL elements of it as NV chunks of 8 (one 16-byte load each). Chunk c of
+// lane r covers elements [c * DC + r * 8, c * DC + r * 8 + 8), DC = D / NV, so
+// one load instruction of the wave reads whole 128-byte lines of KPS rows.
 template <int D>
 struct Geom {
   static constexpr int EPL = (D >= 80 && D % 16 == 0) ? 16 : 8;  // fp16 per lane
   static constexpr int NV = EPL / 8;                              // 16-byte loads
+  static constexpr int DC = D / NV;                               // chunk stride
   static constexpr int SLICES = D / EPL;
   static constexpr int R = next_pow2(SLICES);                     // lanes per key
   static constexpr int KPS = 64 / R;                              // keys per step
-  static_assert(D % EPL == 0, "head_dim must be a multiple of 8");
+  static_assert(D % EPL == 0 && DC % 8 == 0, "head_dim must be a multiple of 8");
   static_assert(R <= 32, "head_dim too large");
 };
 
@@ -149,6 +170,16 @@ __device__ __forceinline__ float wave_max(float x) {
       float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, x)));
 }
 
+__device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+// s_waitcnt on the vector memory counter alone: at most N loads outstanding
+// (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]).
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
 __device__ __forceinline__ f16x8 zero_unless(f16x8 x, bool keep) {
   i32x4 bits = __builtin_bit_cast(i32x4, x);
   bits.x = keep ? bits.x : 0;
@@ -174,24 +205,26 @@ __device__ __forceinline__ SeqGeometry sequence_geometry(const Params& p, int b)
   return g;
 }
 
-// Waves the stream of `total` pages is spread over (both kernels agree).
-__device__ __forceinline__ int stream_waves(int64_t total, const Params& p) {
+// Wave pairs the stream of `total` pages is spread over (both kernels agree).
+__device__ __forceinline__ int stream_pairs(int64_t total, const Params& p) {
   if (total <= 0) return 0;
-  const int64_t want = (total + p.min_pages - 1) / p.min_pages;
-  return (int)min<int64_t>(want, p.grid_waves);
+  const int64_t want = (total + 2 * p.min_pages - 1) / (2 * p.min_pages);
+  return (int)min<int64_t>(want, p.grid_pairs);
 }
 
-// First page of wave w's range, and the wave whose range holds page x.
-__device__ __forceinline__ int64_t range_start(int w, int64_t total, int waves) {
-  return (int64_t)w * total / waves;
+// First page of pair q's range, and the pair whose range holds page x.
+__device__ __forceinline__ int64_t range_start(int q, int64_t total, int pairs) {
+  return (int64_t)q * total / pairs;
 }
-__device__ __forceinline__ int wave_of(int64_t x, int64_t total, int waves) {
-  return (int)(((x + 1) * waves - 1) / total);
+__device__ __forceinline__ int pair_of(int64_t x, int64_t total, int pairs) {
+  return (int)(((x + 1) * pairs - 1) / total);
 }
 
 // Exclusive prefix of visible pages over the batch, into LDS (all threads of
 // the workgroup), plus each sequence's clamped length.
+template <int kThreads>
 __device__ void build_prefix(const Params& p, int* s_prefix, int* s_len) {
+  constexpr int kWaves = kThreads / 64;
   __shared__ int s_wsum[kWaves];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int B = p.batch;
@@ -225,72 +258,91 @@ __device__ void build_prefix(const Params& p, int* s_prefix, int* s_len) {
   __syncthreads();
 }
 
-// Split kernel: a persistent grid; wave wv walks pages [x0, x1) of the stream.
+// Split kernel: a persistent grid of wave pairs (see the file comment).
 // At least two waves per SIMD (<= 256 registers): with G = 7 or 8 heads the
 // few values that do not fit live outside the main loop.
 template <int D, int G>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void paged_decode_kernel(const Params p) {
   using Gm = Geom<D>;
-  constexpr int EPL = Gm::EPL, NV = Gm::NV, R = Gm::R, KPS = Gm::KPS;
+  constexpr int EPL = Gm::EPL, NV = Gm::NV, DC = Gm::DC, R = Gm::R, KPS = Gm::KPS;
   extern __shared__ int s_dyn[];
+  __shared__ int s_ticket[kPairs];
   const int B = p.batch;
   int* const s_prefix = s_dyn;         // [B + 1]
   int* const s_len = s_dyn + B + 1;    // [B]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
+  const int w = uniform(tid >> 6);
   const int kk = lane / R;  // key of the step this lane works on
   const int r = lane % R;   // slice of the head this lane holds
   const bool active = r < Gm::SLICES;
-  const int d0 = active ? r * EPL : 0;
+  const int d0 = active ? r * 8 : 0;  // first element of chunk 0
   const int P = p.page_size;
+  const int spp = P / KPS;  // steps per page
   const int nkvg = p.hkv * p.nhg;
 
-  build_prefix(p, s_prefix, s_len);
+  if (tid < kPairs) s_ticket[tid] = 0;
+  build_prefix<kSplitThreads>(p, s_prefix, s_len);  // ends with a barrier
   if (blockIdx.x == 0)
-    for (int i = tid; i <= B; i += kThreads) p.prefix[i] = s_prefix[i];
+    for (int i = tid; i <= B; i += kSplitThreads) p.prefix[i] = s_prefix[i];
   const int64_t total = (int64_t)s_prefix[B] * nkvg;
-  const int nwaves = stream_waves(total, p);
-  const int wv = blockIdx.x * kWaves + w;
-  if (wv >= nwaves) return;
-  const int64_t x0 = range_start(wv, total, nwaves);
-  const int64_t x1 = range_start(wv + 1, total, nwaves);
+  const int npairs = stream_pairs(total, p);
+  const int pl = w % kPairs;
+  const bool back = w >= kPairs;  // takes its pair's range from the end
+  const int pair = blockIdx.x * kPairs + pl;
+  if (pair >= npairs) return;
+  const int64_t x0 = range_start(pair, total, npairs);
+  const int n_range = (int)(range_start(pair + 1, total, npairs) - x0);
+  const int dir = back ? -1 : 1;
+  const int64_t vw = 2 * (int64_t)pair + (back ? 1 : 0);  // slots 2 vw, 2 vw + 1
 
-  // Sequence holding page x0: the last b with nkvg * prefix[b] <= x0 (it is
-  // never an empty sequence, since x0 < total).
+  // One ticket per page; a ticket below n_range is a page of the range. All
+  // lanes take part without a branch, lane 0 adding 1 and the others 0, so
+  // lane 0 always reads the count before its own add. The result stays in a
+  // VGPR until it is needed, one page later.
+  auto take_ticket = [&]() -> int {
+    return __hip_atomic_fetch_add(&s_ticket[pl], lane == 0 ? 1 : 0, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_WORKGROUP);
+  };
+  auto granted = [&](int t) -> bool { return uniform(t) < n_range; };
+
+  // Unit holding the first page this wave would take: the last b with
+  // nkvg * prefix[b] <= x (never an empty sequence, since x < total).
+  const int64_t xs = back ? x0 + n_range - 1 : x0;
   int b = 0;
   {
     int lo = 0, hi = B - 1;
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
-      if ((int64_t)s_prefix[mid] * nkvg <= x0) lo = mid; else hi = mid - 1;
+      if ((int64_t)s_prefix[mid] * nkvg <= xs) lo = mid; else hi = mid - 1;
     }
     b = lo;
   }
   int npg = s_prefix[b + 1] - s_prefix[b];
-  if (npg <= 0) return;  // cannot happen for x0 < total; guards the division
-  const int64_t rel = x0 - (int64_t)s_prefix[b] * nkvg;
-  int kvg = (int)(rel / npg);
-  int pa = (int)(rel - (int64_t)kvg * npg);
+  if (npg <= 0) return;  // cannot happen for xs < total; guards the division
+  int kvg, pa;
+  {
+    const int64_t rel = xs - (int64_t)s_prefix[b] * nkvg;
+    kvg = (int)(rel / npg);
+    pa = (int)(rel - (int64_t)kvg * npg);
+  }
 
-  const int64_t row_bytes = (int64_t)p.hkv * D * 2;  // bytes between arena rows
   const char* const kbase = reinterpret_cast<const char*>(p.k);
   const char* const vbase = reinterpret_cast<const char*>(p.v);
-  const int spp = P / KPS;  // steps per page
-
-  int64_t x = x0;
+  int taken = 0;               // pages this wave processed
   bool first_unit = true;
-  while (x < x1 && b < B) {
-    npg = s_prefix[b + 1] - s_prefix[b];
-    const int cnt = (int)min<int64_t>(npg - pa, x1 - x);
-    const bool whole = pa == 0 && cnt == npg;
+  bool pending = granted(take_ticket());  // the next page along the wave's way is ours
+
+  while (pending) {
+    // Unit (b, kvg): pages pa, pa + dir, ... while tickets last.
     const int len = s_len[b];
     const int first = p.window > 0 ? max(0, len - p.window) : 0;
     const int first_page = first / P;
     const int kvh = kvg / p.nhg;
     const int h0 = kvh * p.gtot + (kvg - kvh * p.nhg) * G;
+    const int32_t* const table = p.tables + (int64_t)b * p.table_stride + first_page;
 
     // Queries of the G heads, this lane's slice, as fp16 pairs for v_dot2.
     f16x2 q[G][EPL / 2];
@@ -299,7 +351,7 @@ void paged_decode_kernel(const Params p) {
       const f16* qp = p.q + ((int64_t)b * p.hq + h0 + g) * D + d0;
 #pragma unroll
       for (int v = 0; v < NV; ++v) {
-        f16x8 xq = zero_unless(*reinterpret_cast<const f16x8*>(qp + 8 * v), active);
+        f16x8 xq = zero_unless(*reinterpret_cast<const f16x8*>(qp + DC * v), active);
 #pragma unroll
         for (int i = 0; i < 4; ++i) q[g][4 * v + i] = f16x2{xq[2 * i], xq[2 * i + 1]};
       }
@@ -316,132 +368,182 @@ void paged_decode_kernel(const Params p) {
       for (int i = 0; i < EPL; ++i) o[g][i] = 0.0f;
     }
 
-    // Addressing: a wave-uniform byte offset per step (page row base) plus a
-    // 32-bit per-lane offset (its key within the step, kv head and slice).
-    const uint32_t lane_off = (uint32_t)(kk * row_bytes + ((int64_t)kvh * D + d0) * 2);
+    // Addressing: a wave-uniform byte offset per step (page and first key of
+    // the step) plus a 32-bit per-lane offset (its key, kv head and chunk).
+    const uint32_t lane_off = (uint32_t)(kk * p.row_bytes + kvh * p.head_bytes + d0 * 2);
 
-    for (int sp0 = pa; sp0 < pa + cnt; sp0 += kTablePages) {
-      const int n = min(kTablePages, pa + cnt - sp0);
-      const int page0 = first_page + sp0;  // logical page of table lane 0
-      // Lane i holds the physical id of logical page page0 + i.
-      int tbl = -1;
-      if (lane < n) tbl = p.tables[(int64_t)b * p.table_stride + page0 + lane];
-      const int nsteps = n * spp;
+    // Page-table window: lane i holds the physical id of unit page
+    // win + dir * i (lanes past the unit's ends hold an end entry and are
+    // never read). One load for all lanes, no branch.
+    int win = pa;
+    int tbl = 0;
+    auto load_window = [&]() {
+      const int e = win + dir * lane;
+      tbl = table[min(max(e, 0), npg - 1)];
+    };
+    load_window();
 
-      f16x8 kb[kNbuf][NV], vb[kNbuf][NV];
-      int ld_pg = 0, ld_sub = 0;  // next step to load: (page, step in page)
-      int cp_pg = 0, cp_sub = 0;  // next step to compute
+    // Loader state: the page being loaded (lpa, its id) and the next step in
+    // it; `loading` turns false when the unit or the tickets run out.
+    int lpa = pa;
+    int lsub = 0;
+    int lpid = 0;
+    bool loading = true;
+    int next_ticket = 0;
+    bool start_page = true;
+    int cnt = 0;  // pages of this unit taken by this wave
+    // Per ring slot: is it a real step, its first key position, page usable.
+    bool s_real[kNbuf];
+    int s_t0[kNbuf];
+    bool s_ok[kNbuf];
+    int64_t last_off = 0;
 
-      auto load_step = [&](f16x8(&kd)[NV], f16x8(&vd)[NV]) {
-        int pid = __builtin_amdgcn_readlane(tbl, ld_pg);
-        pid = (pid >= 0 && pid < p.arena_pages) ? pid : 0;
-        const int64_t uoff = ((int64_t)pid * P + ld_sub * KPS) * row_bytes;
-        const char* kp = kbase + uoff + lane_off;
-        const char* vp = vbase + uoff + lane_off;
-#pragma unroll
-        for (int v = 0; v < NV; ++v) {
-          kd[v] = *reinterpret_cast<const f16x8*>(kp + 16 * v);
-          vd[v] = *reinterpret_cast<const f16x8*>(vp + 16 * v);
-        }
-        // Advance, staying on the last step once there (the ring keeps
-        // loading it; those reloads hit the cache and are never used).
-        if (ld_pg * spp + ld_sub + 1 < nsteps) {
-          if (++ld_sub == spp) {
-            ld_sub = 0;
-            ++ld_pg;
-          }
-        }
-      };
+    f16x8 kb[kNbuf][NV], vb[kNbuf][NV];
 
-      auto compute_step = [&](f16x8(&kd)[NV], f16x8(&vd)[NV]) {
-        const int pid = __builtin_amdgcn_readlane(tbl, cp_pg);
-        const int t0 = (page0 + cp_pg) * P + cp_sub * KPS;
-        if (++cp_sub == spp) {
-          cp_sub = 0;
-          ++cp_pg;
-        }
-        if (pid < 0 || pid >= p.arena_pages) return;  // released page: masked
-
-        // q.k for every head of the group: v_dot2 over this lane's slice,
-        // then the butterfly over the R lanes of the key.
-        float s[G];
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          float acc = 0.0f;
-#pragma unroll
-          for (int v = 0; v < NV; ++v) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const f16x2 kp = f16x2{kd[v][2 * i], kd[v][2 * i + 1]};
-              acc = __builtin_amdgcn_fdot2(q[g][4 * v + i], kp, acc, false);
-            }
-          }
-          s[g] = acc;
-        }
-#pragma unroll
-        for (int g = 0; g < G; ++g) s[g] = group_sum<R>(s[g]);
-        // Scores in log2 units; softcap c * tanh(x / c) (metal_kernels.py:53)
-        // as c * (1 - 2 / (e^(2x/c) + 1)).
-        if (p.softcap > 0.0f) {
-#pragma unroll
-          for (int g = 0; g < G; ++g) {
-            const float e = __builtin_amdgcn_exp2f(s[g] * p.cap_in);
-            s[g] = (1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f)) * p.cap_out;
-          }
+    auto load_step = [&](int u) {
+      if (loading && start_page) {
+        // Start page lpa: its ticket was granted (`pending`); take the ticket
+        // of the page after it now, while this one loads.
+        if (!pending) {
+          loading = false;
         } else {
-#pragma unroll
-          for (int g = 0; g < G; ++g) s[g] *= p.scale_log2;
-        }
-        if (!(t0 >= first && t0 + KPS <= len)) {
-          // Boundary step. A step with no visible key is skipped: before the
-          // first visible key the running max is still -inf, and -inf - -inf
-          // would poison the sums. Rows outside [first, len) may hold
-          // anything, so their scores are masked and their values zeroed.
-          const int t = t0 + kk;
-          const bool valid = t >= first && t < len;
-          if (!__any(valid)) return;
-#pragma unroll
-          for (int g = 0; g < G; ++g) s[g] = valid ? s[g] : -INFINITY;
-#pragma unroll
-          for (int v = 0; v < NV; ++v) vd[v] = zero_unless(vd[v], valid);
-        }
-        bool grow = false;
-#pragma unroll
-        for (int g = 0; g < G; ++g) grow |= s[g] > m[g] + kSlack;
-        if (__any(grow)) {
-#pragma unroll
-          for (int g = 0; g < G; ++g) {
-            const float mn = fmaxf(m[g], wave_max(s[g]));
-            const float f = __builtin_amdgcn_exp2f(m[g] - mn);
-            m[g] = mn;
-            l[g] *= f;
-#pragma unroll
-            for (int i = 0; i < EPL; ++i) o[g][i] *= f;
+          pending = false;
+          ++cnt;
+          ++taken;
+          const int idx = dir * (lpa - win);
+          if (idx < 0 || idx >= kTablePages) {
+            // Rare: the next 64 entries. Read here, so the common path never
+            // waits on this load.
+            win = lpa;
+            load_window();
+            lpid = __builtin_amdgcn_readlane(tbl, 0);
+          } else {
+            lpid = __builtin_amdgcn_readlane(tbl, idx);
           }
-        }
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          const float pr = __builtin_amdgcn_exp2f(s[g] - m[g]);
-          l[g] += pr;
-#pragma unroll
-          for (int v = 0; v < NV; ++v) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i)
-              o[g][8 * v + i] = __builtin_fmaf(pr, (float)vd[v][i], o[g][8 * v + i]);
-          }
-        }
-      };
-
-#pragma unroll
-      for (int u = 0; u < kNbuf; ++u) load_step(kb[u], vb[u]);
-      for (int j0 = 0; j0 < nsteps; j0 += kNbuf) {
-#pragma unroll
-        for (int u = 0; u < kNbuf; ++u) {
-          if (j0 + u < nsteps) compute_step(kb[u], vb[u]);
-          load_step(kb[u], vb[u]);
+          start_page = false;
+          next_ticket = take_ticket();
         }
       }
-    }
+      if (loading) {
+        const bool ok = lpid >= 0 && lpid < p.arena_pages;
+        const int pid = ok ? lpid : 0;
+        last_off = (int64_t)pid * p.page_bytes + lsub * KPS * p.row_bytes;
+        s_real[u] = true;
+        s_t0[u] = (first_page + lpa) * P + lsub * KPS;
+        s_ok[u] = ok;
+        if (++lsub == spp) {
+          lsub = 0;
+          start_page = true;
+          lpa += dir;
+          // The ticket taken for the next page decides whether it is ours;
+          // past the unit's end it is the next unit's first page.
+          pending = granted(next_ticket);
+          if (lpa < 0 || lpa >= npg) loading = false;
+        }
+      } else {
+        s_real[u] = false;
+      }
+      // Once the unit is done the ring keeps reloading the last step (cache
+      // hits, never used), so every slot always has one load in flight.
+      const char* kp = kbase + last_off + lane_off;
+      const char* vp = vbase + last_off + lane_off;
+#pragma unroll
+      for (int v = 0; v < NV; ++v) {
+        kb[u][v] = *reinterpret_cast<const f16x8*>(kp + 2 * DC * v);
+        vb[u][v] = *reinterpret_cast<const f16x8*>(vp + 2 * DC * v);
+      }
+    };
+
+    auto compute_step = [&](int u) {
+      if (!s_ok[u]) return;  // released or out-of-range page: masked
+      const int t0 = s_t0[u];
+      f16x8(&kd)[NV] = kb[u];
+      f16x8(&vd)[NV] = vb[u];
+      // q.k for every head of the group: v_dot2 over this lane's slice,
+      // then the butterfly over the R lanes of the key.
+      float s[G];
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const f16x2 kp = f16x2{kd[v][2 * i], kd[v][2 * i + 1]};
+            acc = __builtin_amdgcn_fdot2(q[g][4 * v + i], kp, acc, false);
+          }
+        }
+        s[g] = acc;
+      }
+#pragma unroll
+      for (int g = 0; g < G; ++g) s[g] = group_sum<R>(s[g]);
+      // Scores in log2 units; softcap c * tanh(x / c) (metal_kernels.py:53)
+      // as c * (1 - 2 / (e^(2x/c) + 1)).
+      if (p.softcap > 0.0f) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const float e = __builtin_amdgcn_exp2f(s[g] * p.cap_in);
+          s[g] = (1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f)) * p.cap_out;
+        }
+      } else {
+#pragma unroll
+        for (int g = 0; g < G; ++g) s[g] *= p.scale_log2;
+      }
+      if (!(t0 >= first && t0 + KPS <= len)) {
+        // Boundary step. A step with no visible key is skipped: before the
+        // first visible key the running max is still -inf, and -inf - -inf
+        // would poison the sums. Rows outside [first, len) may hold
+        // anything, so their scores are masked and their values zeroed.
+        const int t = t0 + kk;
+        const bool valid = t >= first && t < len;
+        if (!__any(valid)) return;
+#pragma unroll
+        for (int g = 0; g < G; ++g) s[g] = valid ? s[g] : -INFINITY;
+#pragma unroll
+        for (int v = 0; v < NV; ++v) vd[v] = zero_unless(vd[v], valid);
+      }
+      bool grow = false;
+#pragma unroll
+      for (int g = 0; g < G; ++g) grow |= s[g] > m[g] + kSlack;
+      if (__any(grow)) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const float mn = fmaxf(m[g], wave_max(s[g]));
+          const float f = __builtin_amdgcn_exp2f(m[g] - mn);
+          m[g] = mn;
+          l[g] *= f;
+#pragma unroll
+          for (int i = 0; i < EPL; ++i) o[g][i] *= f;
+        }
+      }
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float pr = __builtin_amdgcn_exp2f(s[g] - m[g]);
+        l[g] += pr;
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            o[g][8 * v + i] = __builtin_fmaf(pr, (float)vd[v][i], o[g][8 * v + i]);
+        }
+      }
+    };
+
+#pragma unroll
+    for (int u = 0; u < kNbuf; ++u) load_step(u);
+    // The ring: every slot is waited for (its loads are complete once only
+    // the other slots' remain), computed if it holds a real step and
+    // reloaded, in issue order on every path, with the loop test at the
+    // bottom; the compiler's wait counts then stay those of a steady ring.
+    do {
+#pragma unroll
+      for (int u = 0; u < kNbuf; ++u) {
+        wait_vmem<(kNbuf - 1) * 2 * NV>();
+        if (s_real[u]) compute_step(u);
+        load_step(u);
+      }
+    } while (s_real[0]);
+    // `pending` now tells whether the page after this unit is ours too.
 
     // Fold the wave's key subsets (metal_kernels.py:63-81); every lane then
     // holds the totals of its slice. The lanes of key subset kk write the
@@ -452,7 +554,7 @@ void paged_decode_kernel(const Params p) {
 #pragma unroll
       for (int i = 0; i < EPL; ++i) o[g][i] = subset_sum<R>(o[g][i]);
     }
-    if (whole) {
+    if (cnt == npg) {
       // The whole unit is here: normalise and write (metal_kernels.py:87-91).
 #pragma unroll
       for (int g = 0; g < G; ++g) {
@@ -464,127 +566,178 @@ void paged_decode_kernel(const Params p) {
           f16x8 y;
 #pragma unroll
           for (int i = 0; i < 8; ++i) y[i] = (f16)(o[g][8 * v + i] * inv);
-          *reinterpret_cast<f16x8*>(dst + 8 * v) = y;
+          *reinterpret_cast<f16x8*>(dst + DC * v) = y;
         }
       }
     } else {
-      // Cut unit: unnormalised partial (metal_kernels.py:93-101) in this
-      // wave's slot 0 (its first unit) or 1 (its last unit).
-      const int64_t slot = (int64_t)wv * 2 + (first_unit ? 0 : 1);
+      // Cut unit: unnormalised partial (metal_kernels.py:93-101) in slot 0 if
+      // the unit holds the first page of this wave's final range (the first
+      // wave's first unit, the second wave's last), else in slot 1.
+      const bool holds_start = back ? !pending : first_unit;
+      const int64_t slot = 2 * vw + (holds_start ? 0 : 1);
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         if (g % KPS != kk || !active) continue;
         float* dst = p.part_o + (slot * G + g) * D + d0;
 #pragma unroll
         for (int i = 0; i < EPL; i += 4)
-          *reinterpret_cast<float4*>(dst + i) =
+          *reinterpret_cast<float4*>(dst + DC * (i / 8) + i % 8) =
               make_float4(o[g][i], o[g][i + 1], o[g][i + 2], o[g][i + 3]);
         if (r == 0) p.part_ml[slot * G + g] = make_float2(m[g], l[g]);
       }
     }
-
-    x += cnt;
     first_unit = false;
-    pa = 0;
-    if (++kvg == nkvg) {
-      kvg = 0;
-      do {
-        ++b;
-      } while (b < B && s_prefix[b + 1] == s_prefix[b]);
+    if (!pending) break;
+
+    // The next unit along the wave's way (empty sequences hold no pages).
+    if (!back) {
+      if (++kvg == nkvg) {
+        kvg = 0;
+        do {
+          ++b;
+        } while (b < B && s_prefix[b + 1] == s_prefix[b]);
+      }
+      if (b >= B) break;  // cannot happen: tickets never pass the range
+      npg = s_prefix[b + 1] - s_prefix[b];
+      pa = 0;
+    } else {
+      if (--kvg < 0) {
+        kvg = nkvg - 1;
+        do {
+          --b;
+        } while (b >= 0 && s_prefix[b + 1] == s_prefix[b]);
+      }
+      if (b < 0) break;  // cannot happen: tickets never pass the range
+      npg = s_prefix[b + 1] - s_prefix[b];
+      pa = npg - 1;
     }
   }
+  // The first wave of the pair records the meeting point for the merge.
+  if (!back && lane == 0) p.meet[pair] = taken;
 }
 
-// Merge kernel (metal_kernels.py:103-124): one workgroup per unit (kv head
-// group, sequence). A unit with no visible page gets zeros; a unit inside one
-// wave's range was written by the split kernel; a cut unit combines the
-// partials of the waves whose ranges cover it with log-sum-exp weights
-// (pieces whose max is -inf hold no visible key and weigh 0; a zero total
-// gives 0, :116,122). Wave w takes every fourth piece; lanes cover 64 output
-// elements at a time, so all loads of a wave go out together; the waves'
-// sums meet in LDS.
+// Merge kernel (metal_kernels.py:103-124): one workgroup of MW waves per
+// (sequence, kv head group, head of the group). A unit with no visible page
+// gets zeros. The unit's pages [s, e) of the stream lie in the ranges of pairs
+// qa..qb; pair q split its range [X, Xn) at M = X + meet[q] into the first
+// wave's [X, M) and the second wave's [M, Xn). Each of these ranges that meets
+// [s, e) holds one piece of the unit, in slot 0 of that wave if the range
+// starts inside the unit, else in slot 1. A unit with one piece was written by
+// the split kernel. The pieces are combined with log-sum-exp weights (pieces
+// whose max is -inf hold no visible key and weigh 0; a zero total gives 0,
+// :116,122): wave w takes every MW-th batch of pieces with a running maximum,
+// so the loads of a batch go out together, and the waves meet in LDS. The
+// piece list has a fixed order, so the result does not depend on timing.
 template <int D, int G>
-__global__ __launch_bounds__(kThreads) void paged_decode_merge_kernel(const Params p) {
-  constexpr int kChunks = (D + 63) / 64;
-  __shared__ float s_acc[kWaves][G][kChunks * 64];
-  __shared__ float s_sum[kWaves][G];
-  __shared__ float s_top[G];
+__global__ __launch_bounds__(kMergeMaxWaves * 64) void paged_decode_merge_kernel(const Params p) {
+  constexpr int kChunks = (D + 63) / 64;  // elements l, l + 64, ... of lane l
+  constexpr int kBatch = 32 / kChunks;    // pieces whose loads go out together
+  constexpr int kListPairs = 1024;        // pairs whose pieces are listed per pass
+  __shared__ int s_slot[2 * kListPairs];  // piece slots, -1 = none
+  __shared__ int s_count;
+  __shared__ float s_top[kMergeMaxWaves], s_sum[kMergeMaxWaves];
+  __shared__ float s_acc[kMergeMaxWaves][kChunks * 64];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int w = tid >> 6;
-  const int kvg = blockIdx.x;
+  const int w = uniform(tid >> 6);
+  const int mw = blockDim.x >> 6;
+  const int kvg = blockIdx.x / G;
+  const int g = blockIdx.x - kvg * G;
   const int b = blockIdx.y;
   const int kvh = kvg / p.nhg;
-  const int h0 = kvh * p.gtot + (kvg - kvh * p.nhg) * G;
-  f16* const dst = p.out + ((int64_t)b * p.hq + h0) * D;  // G x D outputs
+  const int h = kvh * p.gtot + (kvg - kvh * p.nhg) * G + g;
+  f16* const dst = p.out + ((int64_t)b * p.hq + h) * D;
   const int nkvg = p.hkv * p.nhg;
   const int pb0 = p.prefix[b];
   const int npg = p.prefix[b + 1] - pb0;
   if (npg == 0) {
-    for (int i = tid; i < G * D; i += kThreads) dst[i] = (f16)0.0f;
+    for (int i = tid; i < D; i += blockDim.x) dst[i] = (f16)0.0f;
     return;
   }
   const int64_t total = (int64_t)p.prefix[p.batch] * nkvg;
-  const int waves = stream_waves(total, p);
-  const int64_t start = (int64_t)pb0 * nkvg + (int64_t)kvg * npg;
-  const int wf = wave_of(start, total, waves);
-  const int wl = wave_of(start + npg - 1, total, waves);
-  if (wf == wl) return;
-  const int nseg = wl - wf + 1;
-  // The first covering wave holds the unit in slot 0 if its range starts
-  // with the unit, else in slot 1 (its last unit); later waves in slot 0.
-  const int64_t slot0 = (int64_t)wf * 2 + (range_start(wf, total, waves) < start ? 1 : 0);
-  auto slot_of = [&](int s) { return s == 0 ? slot0 : (int64_t)(wf + s) * 2; };
-  if (w == 0) {
+  const int pairs = stream_pairs(total, p);
+  const int64_t s = (int64_t)pb0 * nkvg + (int64_t)kvg * npg;
+  const int64_t e = s + npg;
+  const int qa = pair_of(s, total, pairs);
+  const int qb = pair_of(e - 1, total, pairs);
+
+  float top = -INFINITY, sum = 0.0f, acc[kChunks];
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float top = -INFINITY;
-      for (int s = lane; s < nseg; s += 64) top = fmaxf(top, p.part_ml[slot_of(s) * G + g].x);
-      top = wave_max(top);
-      if (lane == 0) s_top[g] = top;
+  for (int c = 0; c < kChunks; ++c) acc[c] = 0.0f;
+  for (int q0 = qa; q0 <= qb; q0 += kListPairs) {
+    // List the pieces of pairs q0 .. q1 in LDS: entries 2 (q - q0) and
+    // 2 (q - q0) + 1 hold the first and second wave's piece of pair q, or -1.
+    const int q1 = min(qb, q0 + kListPairs - 1);
+    const int count = 2 * (q1 - q0 + 1);
+    if (tid == 0) s_count = 0;
+    __syncthreads();
+    for (int q = q0 + tid; q <= q1; q += blockDim.x) {
+      const int64_t X = range_start(q, total, pairs);
+      const int64_t Xn = range_start(q + 1, total, pairs);
+      const int64_t M = X + p.meet[q];
+      const bool front = X < M && X < e && M > s;
+      const bool rear = M < Xn && M < e && Xn > s;
+      s_slot[2 * (q - q0)] = front ? 2 * (2 * q) + (X >= s ? 0 : 1) : -1;
+      s_slot[2 * (q - q0) + 1] = rear ? 2 * (2 * q + 1) + (M >= s ? 0 : 1) : -1;
+      if (front || rear) atomicAdd(&s_count, (int)front + (int)rear);
     }
-  }
-  __syncthreads();
-  float acc[G][kChunks], sum[G];
+    __syncthreads();
+    if (qa == qb && s_count <= 1) return;  // inside one wave's range: written whole
+    for (int i0 = w * kBatch; i0 < count; i0 += mw * kBatch) {
+      int sl[kBatch];
+      float2 ml[kBatch];
+      float part[kBatch][kChunks];
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    sum[g] = 0.0f;
+      for (int u = 0; u < kBatch; ++u) {
+        sl[u] = i0 + u < count ? s_slot[i0 + u] : -1;
+        const int64_t slot = sl[u] < 0 ? 0 : sl[u];
+        ml[u] = p.part_ml[slot * G + g];
 #pragma unroll
-    for (int c = 0; c < kChunks; ++c) acc[g][c] = 0.0f;
-  }
-  for (int s = w; s < nseg; s += kWaves) {
-    const int64_t slot = slot_of(s);
+        for (int c = 0; c < kChunks; ++c) {
+          const int d = c * 64 + lane;
+          part[u][c] = d < D ? p.part_o[(slot * G + g) * D + d] : 0.0f;
+        }
+      }
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float2 e = p.part_ml[slot * G + g];
-      const float wgt = e.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(e.x - s_top[g]);
-      sum[g] = __builtin_fmaf(wgt, e.y, sum[g]);
+      for (int u = 0; u < kBatch; ++u) {
+        if (sl[u] < 0 || ml[u].x == -INFINITY) continue;
+        const float mn = fmaxf(top, ml[u].x);
+        const float fo = __builtin_amdgcn_exp2f(top - mn);  // 0 while top = -inf
+        const float fn = __builtin_amdgcn_exp2f(ml[u].x - mn);
+        top = mn;
+        sum = sum * fo + ml[u].y * fn;
 #pragma unroll
-      for (int c = 0; c < kChunks; ++c) {
-        const int d = c * 64 + lane;
-        const float part = d < D ? p.part_o[(slot * G + g) * D + d] : 0.0f;
-        acc[g][c] = __builtin_fmaf(wgt, part, acc[g][c]);
+        for (int c = 0; c < kChunks; ++c) acc[c] = acc[c] * fo + part[u][c] * fn;
       }
     }
+    __syncthreads();  // the piece list is rewritten by the next pass
   }
+  if (mw > 1) {
+    // Combine the waves: each publishes its maximum, rescales to the common
+    // one and leaves its sums in LDS; wave 0 adds them in a fixed order.
+    if (lane == 0) s_top[w] = top;
+    __syncthreads();
+    float all = -INFINITY;
+    for (int x = 0; x < mw; ++x) all = fmaxf(all, s_top[x]);
+    const float f = top == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(top - all);
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
+    for (int c = 0; c < kChunks; ++c) s_acc[w][c * 64 + lane] = acc[c] * f;
+    if (lane == 0) s_sum[w] = sum * f;
+    __syncthreads();
+    if (w != 0) return;
+    sum = 0.0f;
 #pragma unroll
-    for (int c = 0; c < kChunks; ++c) s_acc[w][g][c * 64 + lane] = acc[g][c];
-    if (lane == 0) s_sum[w][g] = sum[g];
-  }
-  __syncthreads();
-  for (int i = tid; i < G * D; i += kThreads) {
-    const int g = i / D;
-    const int d = i - g * D;
-    float a = 0.0f, t = 0.0f;
+    for (int c = 0; c < kChunks; ++c) acc[c] = 0.0f;
+    for (int x = 0; x < mw; ++x) {
+      sum += s_sum[x];
 #pragma unroll
-    for (int x = 0; x < kWaves; ++x) {
-      a += s_acc[x][g][d];
-      t += s_sum[x][g];
+      for (int c = 0; c < kChunks; ++c) acc[c] += s_acc[x][c * 64 + lane];
     }
-    dst[i] = (f16)(t > 0.0f ? a / t : 0.0f);
   }
+  const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+#pragma unroll
+  for (int c = 0; c < kChunks; ++c)
+    if (c * 64 + lane < D) dst[c * 64 + lane] = (f16)(acc[c] * inv);
 }
 
 // ---------------------------------------------------------------------------
@@ -666,8 +819,9 @@ int heads_per_group(int gtot) {
 
 struct Plan {
   int G = 0, nhg = 0, min_pages = 0;
-  int64_t pages_est = 0;  // visible pages of the batch if every length = longest
-  size_t off_ml = 0, off_o = 0, total = 0;
+  int64_t pages_est = 0;       // visible pages of the batch if every length = longest
+  int64_t unit_pages_max = 0;  // visible pages of one unit, at most
+  size_t off_meet = 0, off_ml = 0, off_o = 0, total = 0;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
@@ -711,11 +865,14 @@ int make_plan(int32_t batch, int32_t q_heads, int32_t kv_heads, int32_t head_dim
     return fail(PDA_ERR_TOO_LONG, "more than 2^31 visible pages in one call");
   int64_t est = pages_max;
   if (longest > 0) est = std::min<int64_t>(est, (longest + page_size - 1) / page_size + 1);
+  pl.unit_pages_max = est;
   pl.pages_est = (int64_t)batch * kv_heads * pl.nhg * est;
   pl.min_pages = split_pages > 0 ? split_pages : kMinPagesPerWave;
-  // Workspace: the per-sequence page prefix, the (max, sum) pairs and the
-  // unnormalised partial outputs of the cut units (two slots per wave).
-  pl.off_ml = align256((size_t)(batch + 1) * sizeof(int32_t));
+  // Workspace: the per-sequence page prefix, the meeting points of the wave
+  // pairs, the (max, sum) pairs and the unnormalised partial outputs of the
+  // cut units (two slots per wave).
+  pl.off_meet = align256((size_t)(batch + 1) * sizeof(int32_t));
+  pl.off_ml = pl.off_meet + align256((size_t)kMaxPairs * sizeof(int32_t));
   pl.off_o = pl.off_ml + align256((size_t)kSlots * pl.G * sizeof(float2));
   pl.total = pl.off_o + align256((size_t)kSlots * pl.G * head_dim * sizeof(float));
   *out = pl;
@@ -735,18 +892,31 @@ int resident_groups(KernelFn fn, size_t lds_bytes) {
   int cus = 0, per_cu = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
       hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(fn),
-                                                   kThreads, lds_bytes) != hipSuccess)
+                                                   kSplitThreads, lds_bytes) != hipSuccess)
     return -1;
   const int groups = std::max(1, std::min(kMaxGroups, cus * std::max(1, per_cu)));
   cache[key] = groups;
   return groups;
 }
 
+// Waves of a merge workgroup: one batch of pieces per wave for the longest
+// unit (its pieces estimated from `longest`).
+int merge_waves(const Plan& pl, int head_dim, int grid_pairs) {
+  const int64_t pairs = std::max<int64_t>(
+      1, std::min<int64_t>(grid_pairs, (pl.pages_est + 2 * pl.min_pages - 1) /
+                                           (2 * pl.min_pages)));
+  const int64_t per_pair = std::max<int64_t>(1, pl.pages_est / pairs);
+  const int64_t pieces = 2 * (pl.unit_pages_max / per_pair + 2);
+  const int batch = 32 / ((head_dim + 63) / 64);
+  const int64_t mw = (pieces + batch - 1) / batch;
+  return (int)std::max<int64_t>(1, std::min<int64_t>(kMergeMaxWaves, mw));
+}
+
 }  // namespace
 
 extern "C" {
 
-int pda_version(void) { return (0 << 16) | 2; }
+int pda_version(void) { return (0 << 16) | 4; }
 
 const char* pda_last_error(void) { return g_error; }
 
@@ -773,8 +943,10 @@ int pda_plan(int32_t batch, int32_t q_heads, int32_t kv_heads,
   const int rc = make_plan(batch, q_heads, kv_heads, head_dim, page_size,
                            table_stride, longest, window, split_pages, &pl);
   if (rc) return rc;
-  const int64_t want = (pl.pages_est + pl.min_pages - 1) / pl.min_pages;
-  *waves = (int32_t)std::max<int64_t>(1, std::min<int64_t>(want, kMaxWaves));
+  // On MI355X (256 CUs, one eight-wave workgroup each): 1024 pairs at most.
+  const int64_t want = (pl.pages_est + 2 * pl.min_pages - 1) / (2 * pl.min_pages);
+  const int64_t pairs = std::max<int64_t>(1, std::min<int64_t>(want, 256 * kPairs));
+  *waves = (int32_t)(2 * pairs);
   *pages_per_wave = (int32_t)((pl.pages_est + *waves - 1) / *waves);
   return ok();
 }
@@ -790,8 +962,8 @@ constexpr int kPassMerge = 2;
 int decode(int passes, const void* queries, const void* keys, const void* values,
            const int32_t* tables, const int32_t* lengths, void* out, int32_t batch,
            int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t page_size,
-           int32_t table_stride, int64_t arena_rows, int32_t longest, float scale,
-           int32_t window, float softcap, int32_t split_pages, void* workspace,
+           int32_t table_stride, int64_t arena_rows, int32_t layout, int32_t longest,
+           float scale, int32_t window, float softcap, int32_t split_pages, void* workspace,
            size_t workspace_bytes, void* stream) {
   Plan pl;
   int rc = make_plan(batch, q_heads, kv_heads, head_dim, page_size, table_stride,
@@ -803,6 +975,11 @@ int decode(int passes, const void* queries, const void* keys, const void* values
   if (arena_rows < page_size)
     return fail(PDA_ERR_INVALID_ARGUMENT, "arena_rows %lld holds no whole page",
                 (long long)arena_rows);
+  if (layout != PDA_LAYOUT_ROWS && layout != PDA_LAYOUT_PAGES)
+    return fail(PDA_ERR_INVALID_ARGUMENT, "unknown K/V layout %d", layout);
+  const int64_t page_bytes = (int64_t)page_size * kv_heads * head_dim * 2;
+  if (page_bytes > INT32_MAX)
+    return fail(PDA_ERR_TOO_LONG, "one page of the arena exceeds 2^31 bytes");
   if (!(scale == scale) || isinf(scale) || !(softcap >= 0.0f) || isinf(softcap))
     return fail(PDA_ERR_INVALID_ARGUMENT, "scale must be finite and softcap >= 0");
   const uintptr_t mis = (uintptr_t)queries | (uintptr_t)keys | (uintptr_t)values |
@@ -831,9 +1008,18 @@ int decode(int passes, const void* queries, const void* keys, const void* values
   prm.out = static_cast<f16*>(out);
   char* ws = static_cast<char*>(workspace);
   prm.prefix = reinterpret_cast<int32_t*>(ws);
+  prm.meet = reinterpret_cast<int32_t*>(ws + pl.off_meet);
   prm.part_ml = reinterpret_cast<float2*>(ws + pl.off_ml);
   prm.part_o = reinterpret_cast<float*>(ws + pl.off_o);
   prm.arena_pages = arena_rows / page_size;
+  prm.page_bytes = page_bytes;
+  if (layout == PDA_LAYOUT_ROWS) {  // [rows, kv_heads, head_dim]
+    prm.row_bytes = kv_heads * head_dim * 2;
+    prm.head_bytes = head_dim * 2;
+  } else {  // [pages, kv_heads, page_size, head_dim]
+    prm.row_bytes = head_dim * 2;
+    prm.head_bytes = page_size * head_dim * 2;
+  }
   prm.batch = batch;
   prm.table_stride = table_stride;
   prm.page_size = page_size;
@@ -842,7 +1028,7 @@ int decode(int passes, const void* queries, const void* keys, const void* values
   prm.gtot = q_heads / kv_heads;
   prm.nhg = pl.nhg;
   prm.window = window;
-  prm.grid_waves = groups * kWaves;
+  prm.grid_pairs = groups * kPairs;
   prm.min_pages = pl.min_pages;
   prm.scale_log2 = scale * kLog2e;
   prm.softcap = softcap;
@@ -854,10 +1040,12 @@ int decode(int passes, const void* queries, const void* keys, const void* values
   hipError_t err = hipSuccess;
   if (passes & kPassSplit)
     err = hipLaunchKernel(reinterpret_cast<const void*>(kp.split), dim3(groups),
-                          dim3(kThreads), args, lds, st);
-  if (err == hipSuccess && (passes & kPassMerge))
+                          dim3(kSplitThreads), args, lds, st);
+  if (err == hipSuccess && (passes & kPassMerge)) {
+    const int mw = merge_waves(pl, head_dim, prm.grid_pairs);
     err = hipLaunchKernel(reinterpret_cast<const void*>(kp.merge),
-                          dim3(kv_heads * pl.nhg, batch), dim3(kThreads), args, 0, st);
+                          dim3(kv_heads * pl.nhg * pl.G, batch), dim3(64 * mw), args, 0, st);
+  }
   if (err != hipSuccess)
     return fail(PDA_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(err));
   return ok();
@@ -871,13 +1059,14 @@ extern "C" {
   const void *queries, const void *keys, const void *values,                   \
       const int32_t *tables, const int32_t *lengths, void *out, int32_t batch, \
       int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t page_size,  \
-      int32_t table_stride, int64_t arena_rows, int32_t longest, float scale,  \
-      int32_t window, float softcap, int32_t split_pages, void *workspace,     \
-      size_t workspace_bytes, void *stream
+      int32_t table_stride, int64_t arena_rows, int32_t layout,                \
+      int32_t longest, float scale, int32_t window, float softcap,             \
+      int32_t split_pages, void *workspace, size_t workspace_bytes,            \
+      void *stream
 #define PDA_DECODE_ARGS                                                        \
   queries, keys, values, tables, lengths, out, batch, q_heads, kv_heads,       \
-      head_dim, page_size, table_stride, arena_rows, longest, scale, window,   \
-      softcap, split_pages, workspace, workspace_bytes, stream
+      head_dim, page_size, table_stride, arena_rows, layout, longest, scale,   \
+      window, softcap, split_pages, workspace, workspace_bytes, stream
 
 int pda_paged_decode_attention(PDA_DECODE_PARAMS) {
   return decode(kPassSplit | kPassMerge, PDA_DECODE_ARGS);

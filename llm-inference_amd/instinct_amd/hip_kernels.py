@@ -3,10 +3,13 @@
 :func:`paged_decode_attention` keeps the signature and meaning of the
 reference's ``paged_decode_attention`` (python/instinct/backends/
 metal_kernels.py:164-248) with torch tensors on the GPU in place of MLX
-arrays: queries ``[batch, q_heads, head_dim]``, a layer's whole K/V arena
-``[rows, kv_heads, head_dim]``, page tables ``[batch, width]`` int32 and
-lengths ``[batch]`` int32 (the new key included). It returns
-``[batch, q_heads, head_dim]`` in the queries' dtype (fp16).
+arrays: queries ``[batch, q_heads, head_dim]``, a layer's whole K/V arena,
+page tables ``[batch, width]`` int32 and lengths ``[batch]`` int32 (the new
+key included). It returns ``[batch, q_heads, head_dim]`` in the queries'
+dtype (fp16). The arena is either the reference's ``[rows, kv_heads,
+head_dim]`` (3-D) or the page-tile layout ``[pages, kv_heads, page_size,
+head_dim]`` (4-D, see :mod:`instinct_amd.paged_kv`), which the kernel reads
+as whole contiguous tiles.
 
 The work happens in hand-written HIP kernels (libpda.so, see
 ``csrc/pda_kernels.hip``) called through the C-ABI of ``include/pda.h``; this
@@ -68,6 +71,16 @@ def paged_decode_attention(
         raise NotImplementedError("8-bit K/V (scales) has no MI355X kernel yet")
     batch, q_heads, head_dim = (int(n) for n in queries.shape)
     kv_heads = int(keys.shape[1])
+    if keys.dim() == 3:
+        layout, arena_rows, width = _lib.PDA_LAYOUT_ROWS, int(keys.shape[0]), int(keys.shape[2])
+    elif keys.dim() == 4:
+        if int(keys.shape[2]) != page_size:
+            raise ValueError("page-tile arena must be [pages, kv_heads, page_size, head_dim]")
+        layout = _lib.PDA_LAYOUT_PAGES
+        arena_rows, width = int(keys.shape[0]) * page_size, int(keys.shape[3])
+    else:
+        raise ValueError("keys must be [rows, kv_heads, head_dim] or "
+                         "[pages, kv_heads, page_size, head_dim]")
     if q_heads % kv_heads:
         raise ValueError("query heads must be a multiple of kv heads")
     for name, t in (("queries", queries), ("keys", keys), ("values", values)):
@@ -77,8 +90,8 @@ def paged_decode_attention(
             raise ValueError(f"{name} must be on a GPU")
         if not t.is_contiguous():
             raise ValueError(f"{name} must be contiguous")
-    if tuple(keys.shape) != tuple(values.shape) or int(keys.shape[2]) != head_dim:
-        raise ValueError("keys and values must both be [rows, kv_heads, head_dim]")
+    if tuple(keys.shape) != tuple(values.shape) or width != head_dim:
+        raise ValueError("keys and values must have the same shape and head_dim")
     if tables.dtype != torch.int32 or lengths.dtype != torch.int32:
         raise TypeError("tables and lengths must be int32")
     if tables.dim() != 2 or tables.shape[0] != batch or lengths.shape != (batch,):
@@ -100,7 +113,7 @@ def paged_decode_attention(
     rc = getattr(_lib.library(), entry)(
         queries.data_ptr(), keys.data_ptr(), values.data_ptr(), tables.data_ptr(),
         lengths.data_ptr(), out.data_ptr(), batch, q_heads, kv_heads, head_dim,
-        int(page_size), stride, int(keys.shape[0]), int(longest), float(scale),
+        int(page_size), stride, arena_rows, layout, int(longest), float(scale),
         int(window), float(softcap), int(split_pages), ws.data_ptr(),
         ws.numel(), ctypes.c_void_p(stream))
     _lib.check(rc)

@@ -2,12 +2,20 @@
 decode kernel reads.
 
 Counterpart of python/instinct/paged_kv.py. Every attention layer keeps its
-keys and values in one arena of token rows, ``[rows, kv_heads, head_dim]``
-fp16 (paged_kv.py:156-235); a page is ``page_size`` consecutive rows and the
-row of logical position t is ``table[t // P] * P + t % P`` (:259-265). The
-arenas live in device memory as torch tensors, sized once for the whole page
-budget: with 288 GB of HBM per MI355X the arena is allocated at its capacity
-rather than grown by doubling (:237-250), so the decode path never
+keys and values in one fp16 arena; a page holds ``page_size`` token rows and
+the row of logical position t is ``table[t // P] * P + t % P`` (:259-265).
+Two device layouts hold the same rows:
+
+* ``"rows"``: ``[rows, kv_heads, head_dim]``, the reference's arena
+  (paged_kv.py:156-235);
+* ``"pages"``: ``[pages, kv_heads, page_size, head_dim]`` page tiles, the
+  MI355X layout: the rows of one (page, kv head) are one contiguous run
+  (4 KiB at head_dim 128, page 16), which the decode kernel reads as whole
+  128-byte lines instead of 256-byte pieces strided by kv_heads * head_dim.
+
+The arenas live in device memory as torch tensors, sized once for the whole
+page budget: with 288 GB of HBM per MI355X the arena is allocated at its
+capacity rather than grown by doubling (:237-250), so the decode path never
 reallocates.
 """
 
@@ -19,6 +27,25 @@ from dataclasses import dataclass
 
 import numpy as np
 import torch
+
+
+LAYOUTS = ("rows", "pages")
+
+
+def rows_to_pages(arena: torch.Tensor, page_size: int) -> torch.Tensor:
+    """``[rows, kv_heads, head_dim]`` -> ``[pages, kv_heads, page_size,
+    head_dim]`` holding the same rows (a copy)."""
+    rows, heads, dim = arena.shape
+    if rows % page_size:
+        raise ValueError("the arena does not hold a whole number of pages")
+    return arena.view(rows // page_size, page_size, heads, dim).permute(0, 2, 1, 3).contiguous()
+
+
+def pages_to_rows(arena: torch.Tensor) -> torch.Tensor:
+    """``[pages, kv_heads, page_size, head_dim]`` -> ``[rows, kv_heads,
+    head_dim]`` (a copy)."""
+    pages, heads, page_size, dim = arena.shape
+    return arena.permute(0, 2, 1, 3).reshape(pages * page_size, heads, dim)
 
 
 @dataclass(frozen=True)
@@ -111,7 +138,8 @@ class PagePool:
 
 class KVCache:
     """Per-layer fp16 K/V arenas in device memory plus one page pool per
-    group (paged_kv.py:156-292, 16-bit K/V)."""
+    group (paged_kv.py:156-292, 16-bit K/V), in the ``"pages"`` tile layout
+    by default or the reference's ``"rows"`` layout."""
 
     def __init__(
         self,
@@ -121,7 +149,11 @@ class KVCache:
         capacities: dict[str, int],
         device: torch.device | str = "cuda",
         dtype: torch.dtype = torch.float16,
+        layout: str = "pages",
     ) -> None:
+        if layout not in LAYOUTS:
+            raise ValueError(f"layout must be one of {LAYOUTS}")
+        self.layout = layout
         self.page_size = page_size
         self.dtype = dtype
         self.device = torch.device(device)
@@ -131,9 +163,12 @@ class KVCache:
         self.keys: dict[int, torch.Tensor] = {}
         self.values: dict[int, torch.Tensor] = {}
         for group in groups:
-            rows = capacities[group.name] * page_size
+            pages = capacities[group.name]
+            if layout == "rows":
+                shape = (pages * page_size, group.kv_heads, group.head_dim)
+            else:
+                shape = (pages, group.kv_heads, page_size, group.head_dim)
             for layer in group.layers:
-                shape = (rows, group.kv_heads, group.head_dim)
                 self.keys[layer] = torch.zeros(shape, dtype=dtype, device=self.device)
                 self.values[layer] = torch.zeros(shape, dtype=dtype, device=self.device)
 
@@ -153,19 +188,35 @@ class KVCache:
     def copy_page(self, group: KVGroup, source: int, target: int, count: int) -> None:
         """Copy the first ``count`` rows of a page (copy-on-write of a shared
         tail, paged_kv.py:267-274)."""
-        src = slice(source * self.page_size, source * self.page_size + count)
-        dst = slice(target * self.page_size, target * self.page_size + count)
         for layer in group.layers:
-            self.keys[layer][dst] = self.keys[layer][src]
-            self.values[layer][dst] = self.values[layer][src]
+            for arena in (self.keys[layer], self.values[layer]):
+                if self.layout == "rows":
+                    src = slice(source * self.page_size, source * self.page_size + count)
+                    dst = slice(target * self.page_size, target * self.page_size + count)
+                    arena[dst] = arena[src]
+                else:
+                    arena[target, :, :count] = arena[source, :, :count]
+
+    def _split(self, rows: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        index = rows.long()
+        return torch.div(index, self.page_size, rounding_mode="floor"), index % self.page_size
 
     def write(self, layer: int, rows: torch.Tensor, keys: torch.Tensor,
               values: torch.Tensor) -> None:
-        """Scatter new rows into the layer arena in place (paged_kv.py:278-283)."""
-        self.keys[layer].index_copy_(0, rows.long(), keys.to(self.dtype))
-        self.values[layer].index_copy_(0, rows.long(), values.to(self.dtype))
+        """Scatter new rows ``[n, kv_heads, head_dim]`` into the layer arena
+        in place (paged_kv.py:278-283)."""
+        if self.layout == "rows":
+            self.keys[layer].index_copy_(0, rows.long(), keys.to(self.dtype))
+            self.values[layer].index_copy_(0, rows.long(), values.to(self.dtype))
+            return
+        page, slot = self._split(rows)
+        self.keys[layer][page, :, slot] = keys.to(self.dtype)
+        self.values[layer][page, :, slot] = values.to(self.dtype)
 
     def gather(self, layer: int, rows: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-        """Rows of the arena (paged_kv.py:285-292)."""
-        index = rows.long()
-        return self.keys[layer][index], self.values[layer][index]
+        """Rows of the arena, ``[n, kv_heads, head_dim]`` (paged_kv.py:285-292)."""
+        if self.layout == "rows":
+            index = rows.long()
+            return self.keys[layer][index], self.values[layer][index]
+        page, slot = self._split(rows)
+        return self.keys[layer][page, :, slot], self.values[layer][page, :, slot]

@@ -4,8 +4,9 @@ the reference's own kernel-test shapes.
 Page tables and lengths come from ``numpy.random.default_rng(seed)`` on the
 host (small); K/V/Q values are drawn with a seeded ``torch.Generator`` on the
 target device, so multi-GB arenas are generated in HBM without a host copy.
-Arena layout is the reference's ``[rows, kv_heads, head_dim]`` fp16
-(paged_kv.py:156-235); tables are ``[batch, width]`` int32, zero-padded like
+Arenas are generated in the reference's ``[rows, kv_heads, head_dim]`` fp16
+layout (paged_kv.py:156-235); :meth:`Workload.to_layout` converts them to the
+page-tile layout with the same rows. Tables are ``[batch, width]`` int32, zero-padded like
 ``DecodeBatch`` (batches.py:170-179), with -1 for pages released by the
 sliding-window trim (mlx_engine.py:349-372).
 """
@@ -18,13 +19,15 @@ from dataclasses import dataclass, field
 import numpy as np
 import torch
 
+from .paged_kv import pages_to_rows, rows_to_pages
+
 
 @dataclass
 class Workload:
     name: str
     q: torch.Tensor          # [B, HQ, D] fp16
-    keys: torch.Tensor       # [rows, HKV, D] fp16
-    values: torch.Tensor     # [rows, HKV, D] fp16
+    keys: torch.Tensor       # [rows, HKV, D] or [pages, HKV, P, D] fp16
+    values: torch.Tensor     # same shape as keys
     tables: torch.Tensor     # [B, width] int32
     lengths: torch.Tensor    # [B] int32
     page_size: int
@@ -48,6 +51,25 @@ class Workload:
     @property
     def head_dim(self) -> int:
         return int(self.q.shape[2])
+
+    @property
+    def layout(self) -> str:
+        return "pages" if self.keys.dim() == 4 else "rows"
+
+    def to_layout(self, layout: str) -> "Workload":
+        """Convert the arenas in place to ``"rows"`` or ``"pages"`` (same
+        rows, same results); returns self."""
+        if layout == self.layout:
+            return self
+        if layout == "pages":
+            self.keys = rows_to_pages(self.keys, self.page_size)
+            self.values = rows_to_pages(self.values, self.page_size)
+        elif layout == "rows":
+            self.keys = pages_to_rows(self.keys)
+            self.values = pages_to_rows(self.values)
+        else:
+            raise ValueError(f"unknown layout {layout!r}")
+        return self
 
     @property
     def longest(self) -> int:
@@ -82,9 +104,13 @@ class Workload:
         return len(rows) * self.kv_heads * self.head_dim * 2 * 2
 
     def numpy(self):
-        """Host copies for the oracle: (q, keys, values) as fp16 ndarrays,
-        tables and lengths as int32."""
-        return (self.q.cpu().numpy(), self.keys.cpu().numpy(), self.values.cpu().numpy(),
+        """Host copies for the oracle: (q, keys, values) as fp16 ndarrays with
+        the arenas as ``[rows, kv_heads, head_dim]``, tables and lengths as
+        int32."""
+        keys, values = self.keys, self.values
+        if self.layout == "pages":
+            keys, values = pages_to_rows(keys), pages_to_rows(values)
+        return (self.q.cpu().numpy(), keys.cpu().numpy(), values.cpu().numpy(),
                 self.tables.cpu().numpy(), self.lengths.cpu().numpy())
 
 

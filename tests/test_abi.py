@@ -33,7 +33,8 @@ def test_library_exports_every_declared_symbol():
 def decode(**overrides):
     args = dict(queries=FAKE, keys=FAKE, values=FAKE, tables=FAKE, lengths=FAKE, out=FAKE,
                 batch=4, q_heads=28, kv_heads=4, head_dim=128, page_size=16,
-                table_stride=64, arena_rows=4096, longest=1000, scale=0.088, window=0,
+                table_stride=64, arena_rows=4096, layout=_lib.PDA_LAYOUT_ROWS,
+                longest=1000, scale=0.088, window=0,
                 softcap=0.0, split_pages=0, workspace=FAKE * 16, workspace_bytes=1 << 30,
                 stream=None)
     args.update(overrides)
@@ -54,6 +55,10 @@ def decode(**overrides):
     (dict(queries=None), _lib.PDA_ERR_INVALID_ARGUMENT),
     (dict(tables=None), _lib.PDA_ERR_INVALID_ARGUMENT),
     (dict(arena_rows=8), _lib.PDA_ERR_INVALID_ARGUMENT),
+    (dict(layout=2), _lib.PDA_ERR_INVALID_ARGUMENT),
+    (dict(layout=-1), _lib.PDA_ERR_INVALID_ARGUMENT),
+    (dict(head_dim=512, q_heads=64, kv_heads=64, page_size=1 << 16, arena_rows=1 << 17),
+     _lib.PDA_ERR_TOO_LONG),
     (dict(scale=float("nan")), _lib.PDA_ERR_INVALID_ARGUMENT),
     (dict(softcap=-1.0), _lib.PDA_ERR_INVALID_ARGUMENT),
     (dict(batch=9000), _lib.PDA_ERR_INVALID_ARGUMENT),
@@ -84,8 +89,9 @@ def test_empty_batch_is_a_no_op():
 def test_workspace_and_plan_are_consistent():
     waves, per_wave = _lib.plan(64, 28, 4, 128, 16, 512, 8192, 0)
     assert waves == 2048 and per_wave * waves >= 64 * 4 * 512
-    # Few pages: the stream uses fewer waves, each with at least split_pages pages.
-    assert _lib.plan(1, 8, 8, 128, 16, 64, 64, 0) == (5, 8)
+    # Few pages: the stream uses fewer wave pairs, each wave with about
+    # split_pages pages (40 pages: 3 pairs of 7 pages a wave).
+    assert _lib.plan(1, 8, 8, 128, 16, 64, 64, 0) == (6, 7)
     assert _lib.plan(1, 8, 8, 128, 16, 64, 64, 0, split_pages=2) == (20, 2)
     # A window bounds the visible pages whatever the table width.
     assert _lib.plan(32, 8, 4, 256, 16, 2048, 32768, 1024, split_pages=16)[0] == 32 * 4 * 65 // 16

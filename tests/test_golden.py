@@ -52,18 +52,23 @@ def test_closed_form_fixture_matches_the_formula():
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("layout", ["rows", "pages"])
 @pytest.mark.parametrize("path", GOLDEN, ids=lambda p: p.stem)
-def test_kernel_matches_fixture(gpu, path):
+def test_kernel_matches_fixture(gpu, path, layout):
     import torch
 
     from instinct_amd.hip_kernels import paged_decode_attention
+    from instinct_amd.paged_kv import rows_to_pages
 
     c = load(path)
     t = {k: torch.as_tensor(c[k]).to(gpu) for k in ("q", "keys", "values", "tables", "lengths")}
+    if layout == "pages":
+        t["keys"] = rows_to_pages(t["keys"], c["page_size"])
+        t["values"] = rows_to_pages(t["values"], c["page_size"])
     out = paged_decode_attention(t["q"], t["keys"], t["values"], t["tables"], t["lengths"],
                                  page_size=c["page_size"], longest=int(c["lengths"].max()),
                                  scale=c["scale"], window=c["window"], softcap=c["softcap"])
     got = out.float().cpu().numpy()
     err_max, err_mean = pa.error_stats(got, c["expected"])
-    print(f"{path.stem}: max_abs={err_max:.3e} mean_abs={err_mean:.3e}")
+    print(f"{path.stem} [{layout}]: max_abs={err_max:.3e} mean_abs={err_mean:.3e}")
     assert err_max <= 2e-3 and err_mean <= 2e-4

@@ -14,7 +14,8 @@ import pytest
 import torch
 
 from instinct_amd.batches import DecodeBatch, pack_tables
-from instinct_amd.paged_kv import KVCache, KVGroup, PagePool
+from instinct_amd.paged_kv import (LAYOUTS, KVCache, KVGroup, PagePool, pages_to_rows,
+                                  rows_to_pages)
 
 
 def test_lowest_free_page_first_keeps_the_arena_compact():
@@ -90,10 +91,11 @@ def test_block_arithmetic(tokens, pages):
     assert len(table) == pages
 
 
-def small_cache():
+def small_cache(layout="rows"):
     groups = [KVGroup("full", (0,), kv_heads=2, head_dim=8),
               KVGroup("local", (1,), kv_heads=2, head_dim=8, window=6)]
-    return KVCache(groups, page_size=4, capacities={"full": 8, "local": 8}, device="cpu")
+    return KVCache(groups, page_size=4, capacities={"full": 8, "local": 8}, device="cpu",
+                   layout=layout)
 
 
 def test_rows_map_positions_through_the_table():
@@ -106,8 +108,9 @@ def test_rows_map_positions_through_the_table():
     np.testing.assert_array_equal(cache.rows(np.array([-1, 2]), 4, 6), [8, 9])
 
 
-def test_write_gather_and_copy_page():
-    cache = small_cache()
+@pytest.mark.parametrize("layout", LAYOUTS)
+def test_write_gather_and_copy_page(layout):
+    cache = small_cache(layout)
     rows = torch.tensor([3, 9, 17])
     k = torch.arange(3 * 2 * 8, dtype=torch.float32).view(3, 2, 8)
     v = -k
@@ -116,8 +119,22 @@ def test_write_gather_and_copy_page():
     assert torch.equal(gk, k.half()) and torch.equal(gv, v.half())
     assert cache.keys[0].abs().sum() == k.abs().sum()
     cache.copy_page(cache.groups["full"], source=2, target=6, count=2)  # rows 8,9 -> 24,25
-    assert torch.equal(cache.keys[0][25], k[1].half())
+    assert torch.equal(cache.gather(0, torch.tensor([25]))[0][0], k[1].half())
+    assert torch.equal(cache.gather(0, torch.tensor([26]))[1][0], torch.zeros(2, 8).half())
     assert cache.device_bytes == 4 * 32 * 2 * 8 * 2
+    # Both layouts hold the same rows: converting one gives the other.
+    arena = cache.keys[0]
+    as_rows = arena if layout == "rows" else pages_to_rows(arena)
+    assert torch.equal(as_rows[9], k[1].half())
+    if layout == "pages":
+        assert tuple(arena.shape) == (8, 2, 4, 8)
+        assert torch.equal(arena[2, :, 1], k[1].half())  # row 9 = page 2, slot 1
+        assert torch.equal(pages_to_rows(rows_to_pages(as_rows, 4)), as_rows)
+
+
+def test_unknown_layout_is_rejected():
+    with pytest.raises(ValueError, match="layout"):
+        small_cache("columns")
 
 
 def test_decode_batch_packs_tables_and_lengths():
