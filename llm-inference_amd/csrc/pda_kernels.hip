@@ -24,7 +24,11 @@
 //    that wave (as _SINGLE_WRITE); a unit cut by a range boundary leaves
 //    unnormalised partials (as _SPLIT_WRITE) in one of the wave's two slots,
 //    which the merge kernel combines (as _DECODE_MERGE). The first wave of
-//    each pair records the meeting point for the merge.
+//    each pair records the meeting point for the merge. (Merging in the
+//    split kernel was measured slower: agent-scope fences at every cut unit
+//    write back the L2 and more than doubled the kernel on config 3, and a
+//    fence-free variant, device-coherent stores plus a per-unit counter,
+//    left one wave to read all pieces of a unit at the very end.)
 //  * Inside a wave, R lanes share one key row (R = head_dim / EPL, EPL = 8 or
 //    16 fp16 per lane, i.e. one or two 16-byte loads per lane per row), so a
 //    wave covers 64 / R keys per step. Every step reads K and V rows once and
@@ -126,6 +130,12 @@ struct Geom {
   static constexpr int SLICES = D / EPL;
   static constexpr int R = next_pow2(SLICES);                     // lanes per key
   static constexpr int KPS = 64 / R;                              // keys per step
+  // p.v on v_dot2 over key pairs (head dims with 2R lanes x 8 elements):
+  // lane (kp, r2), kp = lane / 2R, r2 = lane % 2R, holds elements
+  // [r2 * 8, r2 * 8 + 8) of the step's keys 2 kp and 2 kp + 1.
+  static constexpr bool PV2 = EPL == 16 && D == 2 * R * 8;
+  static constexpr int OPL = PV2 ? 8 : EPL;                       // outputs per lane
+  static constexpr int NPAIR = KPS / 2;                           // key pairs per step
   static_assert(D % EPL == 0 && DC % 8 == 0, "head_dim must be a multiple of 8");
   static_assert(R <= 32, "head_dim too large");
 };
@@ -159,6 +169,32 @@ __device__ __forceinline__ float subset_sum(float x) {
   return x;
 }
 
+// Sum over the key pairs of the p.v layout (lanes r2, r2 + 2R, ...).
+template <int R>
+__device__ __forceinline__ float pair_sum(float x) {
+  if constexpr (2 * R <= 16) x += __shfl_xor(x, 16);
+  if constexpr (2 * R <= 32) x += __shfl_xor(x, 32);
+  return x;
+}
+
+// The value of lane ^ R (the other key of this lane's pair).
+template <int R>
+__device__ __forceinline__ float pair_swap(float x) {
+  if constexpr (R == 8)  // row_ror:8 == lane ^ 8, every lane valid: no old value
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x128, 0xF, 0xF, true));
+  else
+    return __shfl_xor(x, R);
+}
+
+// a.x * b.x + a.y * b.y in fp32: the 3-operand v_dot2 with an inline zero
+// (the compiler would otherwise zero a register to use the accumulating form).
+__device__ __forceinline__ float dot2_first(f16x2 a, f16x2 b) {
+  float d;
+  asm("v_dot2_f32_f16 %0, %1, %2, 0" : "=v"(d) : "v"(a), "v"(b));
+  return d;
+}
+
 __device__ __forceinline__ float wave_max(float x) {
   x = fmaxf(x, dpp<0xB1>(x));
   x = fmaxf(x, dpp<0x4E>(x));
@@ -171,6 +207,21 @@ __device__ __forceinline__ float wave_max(float x) {
 }
 
 __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+// Log-sum-exp combination of pieces (metal_kernels.py:103-124): a running
+// maximum, pieces whose max is -inf (no visible key) weigh 0.
+template <int NC>
+__device__ __forceinline__ void lse_add(float& top, float& sum, float (&acc)[NC], float2 ml,
+                                        const float (&part)[NC]) {
+  if (ml.x == -INFINITY) return;
+  const float mn = fmaxf(top, ml.x);
+  const float fo = __builtin_amdgcn_exp2f(top - mn);  // 0 while top = -inf
+  const float fn = __builtin_amdgcn_exp2f(ml.x - mn);
+  top = mn;
+  sum = sum * fo + ml.y * fn;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) acc[c] = acc[c] * fo + part[c] * fn;
+}
 
 // s_waitcnt on the vector memory counter alone: at most N loads outstanding
 // (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]).
@@ -266,6 +317,8 @@ __global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(2
 void paged_decode_kernel(const Params p) {
   using Gm = Geom<D>;
   constexpr int EPL = Gm::EPL, NV = Gm::NV, DC = Gm::DC, R = Gm::R, KPS = Gm::KPS;
+  constexpr bool PV2 = Gm::PV2;
+  constexpr int OPL = Gm::OPL;
   extern __shared__ int s_dyn[];
   __shared__ int s_ticket[kPairs];
   const int B = p.batch;
@@ -279,6 +332,14 @@ void paged_decode_kernel(const Params p) {
   const int r = lane % R;   // slice of the head this lane holds
   const bool active = r < Gm::SLICES;
   const int d0 = active ? r * 8 : 0;  // first element of chunk 0
+  const int r2 = lane % (2 * R);      // p.v layout: element group and key pair
+  const int kp = lane / (2 * R);
+  const bool hi = kk & 1;             // this lane's key is the second of its pair
+  // v_perm selectors that pair V elements as (this lane's key, the other),
+  // the order of the probability pair below: bytes 0-3 of the source pair
+  // are the second key's dword, 4-7 the first key's.
+  const uint32_t sel_lo = hi ? 0x05040100u : 0x01000504u;
+  const uint32_t sel_hi = hi ? 0x07060302u : 0x03020706u;
   const int P = p.page_size;
   const int spp = P / KPS;  // steps per page
   const int nkvg = p.hkv * p.nhg;
@@ -287,6 +348,14 @@ void paged_decode_kernel(const Params p) {
   build_prefix<kSplitThreads>(p, s_prefix, s_len);  // ends with a barrier
   if (blockIdx.x == 0)
     for (int i = tid; i <= B; i += kSplitThreads) p.prefix[i] = s_prefix[i];
+  // Sequences with no visible key get zeros (metal_kernels.py:88-90 with a
+  // zero sum); workgroup j takes sequences j, j + grid, ...
+  for (int bz = blockIdx.x; bz < B; bz += gridDim.x) {
+    if (s_prefix[bz + 1] != s_prefix[bz]) continue;
+    f16* const dz = p.out + (int64_t)bz * p.hq * D;
+    for (int i = tid * 8; i < p.hq * D; i += kSplitThreads * 8)
+      *reinterpret_cast<f16x8*>(dz + i) = f16x8{};
+  }
   const int64_t total = (int64_t)s_prefix[B] * nkvg;
   const int npairs = stream_pairs(total, p);
   const int pl = w % kPairs;
@@ -331,8 +400,9 @@ void paged_decode_kernel(const Params p) {
 
   const char* const kbase = reinterpret_cast<const char*>(p.k);
   const char* const vbase = reinterpret_cast<const char*>(p.v);
-  int taken = 0;               // pages this wave processed
+
   bool first_unit = true;
+  int taken = 0;               // pages this wave processed
   bool pending = granted(take_ticket());  // the next page along the wave's way is ours
 
   while (pending) {
@@ -357,7 +427,7 @@ void paged_decode_kernel(const Params p) {
       }
     }
 
-    float o[G][EPL];
+    float o[G][OPL];
     float l[G];
     float m[G];
 #pragma unroll
@@ -365,12 +435,15 @@ void paged_decode_kernel(const Params p) {
       l[g] = 0.0f;
       m[g] = -INFINITY;
 #pragma unroll
-      for (int i = 0; i < EPL; ++i) o[g][i] = 0.0f;
+      for (int i = 0; i < OPL; ++i) o[g][i] = 0.0f;
     }
 
     // Addressing: a wave-uniform byte offset per step (page and first key of
-    // the step) plus a 32-bit per-lane offset (its key, kv head and chunk).
+    // the step) plus 32-bit per-lane offsets: K by (key, kv head, chunk), V
+    // by (key pair, kv head, element group) on the p.v path, else as K.
     const uint32_t lane_off = (uint32_t)(kk * p.row_bytes + kvh * p.head_bytes + d0 * 2);
+    const uint32_t v_off =
+        PV2 ? (uint32_t)(2 * kp * p.row_bytes + kvh * p.head_bytes + r2 * 16) : lane_off;
 
     // Page-table window: lane i holds the physical id of unit page
     // win + dir * i (lanes past the unit's ends hold an end entry and are
@@ -445,12 +518,12 @@ void paged_decode_kernel(const Params p) {
       }
       // Once the unit is done the ring keeps reloading the last step (cache
       // hits, never used), so every slot always has one load in flight.
-      const char* kp = kbase + last_off + lane_off;
-      const char* vp = vbase + last_off + lane_off;
+      const char* kq = kbase + last_off + lane_off;
+      const char* vq = vbase + last_off + v_off;
 #pragma unroll
       for (int v = 0; v < NV; ++v) {
-        kb[u][v] = *reinterpret_cast<const f16x8*>(kp + 2 * DC * v);
-        vb[u][v] = *reinterpret_cast<const f16x8*>(vp + 2 * DC * v);
+        kb[u][v] = *reinterpret_cast<const f16x8*>(kq + 2 * DC * v);
+        vb[u][v] = *reinterpret_cast<const f16x8*>(vq + (PV2 ? v * p.row_bytes : 2 * DC * v));
       }
     };
 
@@ -464,30 +537,31 @@ void paged_decode_kernel(const Params p) {
       float s[G];
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        float acc = 0.0f;
+        float acc = dot2_first(q[g][0], f16x2{kd[0][0], kd[0][1]});
 #pragma unroll
         for (int v = 0; v < NV; ++v) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const f16x2 kp = f16x2{kd[v][2 * i], kd[v][2 * i + 1]};
-            acc = __builtin_amdgcn_fdot2(q[g][4 * v + i], kp, acc, false);
+          for (int i = v == 0 ? 1 : 0; i < 4; ++i) {
+            const f16x2 kv2 = f16x2{kd[v][2 * i], kd[v][2 * i + 1]};
+            acc = __builtin_amdgcn_fdot2(q[g][4 * v + i], kv2, acc, false);
           }
         }
         s[g] = acc;
       }
 #pragma unroll
       for (int g = 0; g < G; ++g) s[g] = group_sum<R>(s[g]);
-      // Scores in log2 units; softcap c * tanh(x / c) (metal_kernels.py:53)
-      // as c * (1 - 2 / (e^(2x/c) + 1)).
+      // x = score - running max, in log2 units; softcap c * tanh(x / c)
+      // (metal_kernels.py:53) as c * (1 - 2 / (e^(2x/c) + 1)).
+      float x[G];
       if (p.softcap > 0.0f) {
 #pragma unroll
         for (int g = 0; g < G; ++g) {
           const float e = __builtin_amdgcn_exp2f(s[g] * p.cap_in);
-          s[g] = (1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f)) * p.cap_out;
+          x[g] = (1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f)) * p.cap_out - m[g];
         }
       } else {
 #pragma unroll
-        for (int g = 0; g < G; ++g) s[g] *= p.scale_log2;
+        for (int g = 0; g < G; ++g) x[g] = __builtin_fmaf(s[g], p.scale_log2, -m[g]);
       }
       if (!(t0 >= first && t0 + KPS <= len)) {
         // Boundary step. A step with no visible key is skipped: before the
@@ -498,33 +572,77 @@ void paged_decode_kernel(const Params p) {
         const bool valid = t >= first && t < len;
         if (!__any(valid)) return;
 #pragma unroll
-        for (int g = 0; g < G; ++g) s[g] = valid ? s[g] : -INFINITY;
+        for (int g = 0; g < G; ++g) x[g] = valid ? x[g] : -INFINITY;
+        if constexpr (PV2) {
+          const int ta = t0 + 2 * kp;
 #pragma unroll
-        for (int v = 0; v < NV; ++v) vd[v] = zero_unless(vd[v], valid);
+          for (int v = 0; v < NV; ++v) vd[v] = zero_unless(vd[v], ta + v >= first && ta + v < len);
+        } else {
+#pragma unroll
+          for (int v = 0; v < NV; ++v) vd[v] = zero_unless(vd[v], valid);
+        }
       }
       bool grow = false;
 #pragma unroll
-      for (int g = 0; g < G; ++g) grow |= s[g] > m[g] + kSlack;
+      for (int g = 0; g < G; ++g) grow |= x[g] > kSlack;
       if (__any(grow)) {
+        // Rare: a score passed the running max by 2^8 (always so for the
+        // first visible key, while the max is -inf). Raise the max to the
+        // wave's largest score and rescale what was summed so far. The
+        // scores are recomputed from s: x + m would be inf - inf there.
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-          const float mn = fmaxf(m[g], wave_max(s[g]));
+          float sc;
+          if (p.softcap > 0.0f) {
+            const float e = __builtin_amdgcn_exp2f(s[g] * p.cap_in);
+            sc = (1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f)) * p.cap_out;
+          } else {
+            sc = s[g] * p.scale_log2;
+          }
+          sc = x[g] == -INFINITY ? -INFINITY : sc;  // masked keys stay out
+          const float mn = fmaxf(m[g], wave_max(sc));
           const float f = __builtin_amdgcn_exp2f(m[g] - mn);
+          x[g] = sc - mn;
           m[g] = mn;
           l[g] *= f;
 #pragma unroll
-          for (int i = 0; i < EPL; ++i) o[g][i] *= f;
+          for (int i = 0; i < OPL; ++i) o[g][i] *= f;
         }
       }
+      if constexpr (PV2) {
+        // V element pairs (this lane's key, the other key of its pair),
+        // shared by all heads.
+        f16x2 vv[8];
+        const i32x4 va = __builtin_bit_cast(i32x4, vd[0]);  // key 2 kp
+        const i32x4 vb = __builtin_bit_cast(i32x4, vd[1]);  // key 2 kp + 1
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float pr = __builtin_amdgcn_exp2f(s[g] - m[g]);
-        l[g] += pr;
+        for (int j = 0; j < 4; ++j) {
+          vv[2 * j] = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(va[j], vb[j], sel_lo));
+          vv[2 * j + 1] = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(va[j], vb[j], sel_hi));
+        }
 #pragma unroll
-        for (int v = 0; v < NV; ++v) {
+        for (int g = 0; g < G; ++g) {
+          // Probabilities of the pair's two keys as fp16: this lane holds its
+          // own key's, lane ^ R the other's. The sum uses the same rounded
+          // values, so the weights stay a normalised combination.
+          const float pr = __builtin_amdgcn_exp2f(x[g]);
+          const float other = pair_swap<R>(pr);
+          const f16x2 pp = f16x2{(f16)pr, (f16)other};
+          l[g] = __builtin_amdgcn_fdot2(pp, f16x2{(f16)1.0f, (f16)1.0f}, l[g], false);
 #pragma unroll
-          for (int i = 0; i < 8; ++i)
-            o[g][8 * v + i] = __builtin_fmaf(pr, (float)vd[v][i], o[g][8 * v + i]);
+          for (int i = 0; i < 8; ++i) o[g][i] = __builtin_amdgcn_fdot2(pp, vv[i], o[g][i], false);
+        }
+      } else {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const float pr = __builtin_amdgcn_exp2f(x[g]);
+          l[g] += pr;
+#pragma unroll
+          for (int v = 0; v < NV; ++v) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+              o[g][8 * v + i] = __builtin_fmaf(pr, (float)vd[v][i], o[g][8 * v + i]);
+          }
         }
       }
     };
@@ -546,27 +664,40 @@ void paged_decode_kernel(const Params p) {
     // `pending` now tells whether the page after this unit is ours too.
 
     // Fold the wave's key subsets (metal_kernels.py:63-81); every lane then
-    // holds the totals of its slice. The lanes of key subset kk write the
-    // heads g with g % KPS == kk.
+    // holds the totals of its elements. On the p.v pair path the lanes of
+    // key pair kp write the heads g with g % NPAIR == kp, elements r2 * 8 ..;
+    // otherwise the lanes of key subset kk write the heads g with
+    // g % KPS == kk, in chunks.
+    constexpr int kWriters = PV2 ? Gm::NPAIR : KPS;
+    const int writer = PV2 ? kp : kk;
+    const bool writes = PV2 || active;
+    const int e0 = PV2 ? r2 * 8 : d0;      // first output element of this lane
+    const int estride = PV2 ? 8 : DC;     // between its chunks of 8
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      l[g] = subset_sum<R>(l[g]);
+      if constexpr (PV2) {
+        l[g] = pair_sum<R>(l[g]);
 #pragma unroll
-      for (int i = 0; i < EPL; ++i) o[g][i] = subset_sum<R>(o[g][i]);
+        for (int i = 0; i < OPL; ++i) o[g][i] = pair_sum<R>(o[g][i]);
+      } else {
+        l[g] = subset_sum<R>(l[g]);
+#pragma unroll
+        for (int i = 0; i < OPL; ++i) o[g][i] = subset_sum<R>(o[g][i]);
+      }
     }
     if (cnt == npg) {
       // The whole unit is here: normalise and write (metal_kernels.py:87-91).
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        if (g % KPS != kk || !active) continue;
+        if (g % kWriters != writer || !writes) continue;
         const float inv = l[g] > 0.0f ? 1.0f / l[g] : 0.0f;
-        f16* dst = p.out + ((int64_t)b * p.hq + h0 + g) * D + d0;
+        f16* dst = p.out + ((int64_t)b * p.hq + h0 + g) * D + e0;
 #pragma unroll
-        for (int v = 0; v < NV; ++v) {
+        for (int v = 0; v < OPL / 8; ++v) {
           f16x8 y;
 #pragma unroll
           for (int i = 0; i < 8; ++i) y[i] = (f16)(o[g][8 * v + i] * inv);
-          *reinterpret_cast<f16x8*>(dst + DC * v) = y;
+          *reinterpret_cast<f16x8*>(dst + estride * v) = y;
         }
       }
     } else {
@@ -577,13 +708,13 @@ void paged_decode_kernel(const Params p) {
       const int64_t slot = 2 * vw + (holds_start ? 0 : 1);
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        if (g % KPS != kk || !active) continue;
-        float* dst = p.part_o + (slot * G + g) * D + d0;
+        if (g % kWriters != writer || !writes) continue;
+        float* dst = p.part_o + (slot * G + g) * D + e0;
 #pragma unroll
-        for (int i = 0; i < EPL; i += 4)
-          *reinterpret_cast<float4*>(dst + DC * (i / 8) + i % 8) =
+        for (int i = 0; i < OPL; i += 4)
+          *reinterpret_cast<float4*>(dst + estride * (i / 8) + i % 8) =
               make_float4(o[g][i], o[g][i + 1], o[g][i + 2], o[g][i + 3]);
-        if (r == 0) p.part_ml[slot * G + g] = make_float2(m[g], l[g]);
+        if ((PV2 ? r2 : r) == 0) p.part_ml[slot * G + g] = make_float2(m[g], l[g]);
       }
     }
     first_unit = false;
@@ -617,17 +748,18 @@ void paged_decode_kernel(const Params p) {
 }
 
 // Merge kernel (metal_kernels.py:103-124): one workgroup of MW waves per
-// (sequence, kv head group, head of the group). A unit with no visible page
-// gets zeros. The unit's pages [s, e) of the stream lie in the ranges of pairs
-// qa..qb; pair q split its range [X, Xn) at M = X + meet[q] into the first
-// wave's [X, M) and the second wave's [M, Xn). Each of these ranges that meets
-// [s, e) holds one piece of the unit, in slot 0 of that wave if the range
-// starts inside the unit, else in slot 1. A unit with one piece was written by
-// the split kernel. The pieces are combined with log-sum-exp weights (pieces
-// whose max is -inf hold no visible key and weigh 0; a zero total gives 0,
-// :116,122): wave w takes every MW-th batch of pieces with a running maximum,
-// so the loads of a batch go out together, and the waves meet in LDS. The
-// piece list has a fixed order, so the result does not depend on timing.
+// (sequence, kv head group, head of the group). The unit's pages [s, e) of
+// the stream lie in the ranges of pairs qa..qb; pair q split its range
+// [X, Xn) at M = X + meet[q] into the first wave's [X, M) and the second
+// wave's [M, Xn). Each of these ranges that meets [s, e) holds one piece of
+// the unit, in slot 0 of that wave if the range starts inside the unit, else
+// in slot 1. A unit with one piece was written by the split kernel, one with
+// no visible page zeroed there. The pieces are combined with log-sum-exp
+// weights (pieces whose max is -inf hold no visible key and weigh 0; a zero
+// total gives 0, :116,122): wave w takes every MW-th batch of pieces with a
+// running maximum, so the loads of a batch go out together, and the waves
+// meet in LDS. The piece list has a fixed order, so the result does not
+// depend on timing.
 template <int D, int G>
 __global__ __launch_bounds__(kMergeMaxWaves * 64) void paged_decode_merge_kernel(const Params p) {
   constexpr int kChunks = (D + 63) / 64;  // elements l, l + 64, ... of lane l
@@ -650,10 +782,7 @@ __global__ __launch_bounds__(kMergeMaxWaves * 64) void paged_decode_merge_kernel
   const int nkvg = p.hkv * p.nhg;
   const int pb0 = p.prefix[b];
   const int npg = p.prefix[b + 1] - pb0;
-  if (npg == 0) {
-    for (int i = tid; i < D; i += blockDim.x) dst[i] = (f16)0.0f;
-    return;
-  }
+  if (npg == 0) return;  // zeroed by the split kernel
   const int64_t total = (int64_t)p.prefix[p.batch] * nkvg;
   const int pairs = stream_pairs(total, p);
   const int64_t s = (int64_t)pb0 * nkvg + (int64_t)kvg * npg;
@@ -699,16 +828,8 @@ __global__ __launch_bounds__(kMergeMaxWaves * 64) void paged_decode_merge_kernel
         }
       }
 #pragma unroll
-      for (int u = 0; u < kBatch; ++u) {
-        if (sl[u] < 0 || ml[u].x == -INFINITY) continue;
-        const float mn = fmaxf(top, ml[u].x);
-        const float fo = __builtin_amdgcn_exp2f(top - mn);  // 0 while top = -inf
-        const float fn = __builtin_amdgcn_exp2f(ml[u].x - mn);
-        top = mn;
-        sum = sum * fo + ml[u].y * fn;
-#pragma unroll
-        for (int c = 0; c < kChunks; ++c) acc[c] = acc[c] * fo + part[u][c] * fn;
-      }
+      for (int u = 0; u < kBatch; ++u)
+        if (sl[u] >= 0) lse_add<kChunks>(top, sum, acc, ml[u], part[u]);
     }
     __syncthreads();  // the piece list is rewritten by the next pass
   }
@@ -824,6 +945,7 @@ struct Plan {
   size_t off_meet = 0, off_ml = 0, off_o = 0, total = 0;
 };
 
+
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 int make_plan(int32_t batch, int32_t q_heads, int32_t kv_heads, int32_t head_dim,
@@ -870,7 +992,8 @@ int make_plan(int32_t batch, int32_t q_heads, int32_t kv_heads, int32_t head_dim
   pl.min_pages = split_pages > 0 ? split_pages : kMinPagesPerWave;
   // Workspace: the per-sequence page prefix, the meeting points of the wave
   // pairs, the (max, sum) pairs and the unnormalised partial outputs of the
-  // cut units (two slots per wave).
+  // cut units (two slots per wave). Nothing in it outlives a call, so calls
+  // of any shape share one workspace without initialisation.
   pl.off_meet = align256((size_t)(batch + 1) * sizeof(int32_t));
   pl.off_ml = pl.off_meet + align256((size_t)kMaxPairs * sizeof(int32_t));
   pl.off_o = pl.off_ml + align256((size_t)kSlots * pl.G * sizeof(float2));
@@ -916,7 +1039,7 @@ int merge_waves(const Plan& pl, int head_dim, int grid_pairs) {
 
 extern "C" {
 
-int pda_version(void) { return (0 << 16) | 4; }
+int pda_version(void) { return (0 << 16) | 5; }
 
 const char* pda_last_error(void) { return g_error; }
 
