@@ -754,19 +754,18 @@ void paged_decode_kernel(const Params p) {
 // wave's [M, Xn). Each of these ranges that meets [s, e) holds one piece of
 // the unit, in slot 0 of that wave if the range starts inside the unit, else
 // in slot 1. A unit with one piece was written by the split kernel, one with
-// no visible page zeroed there. The pieces are combined with log-sum-exp
-// weights (pieces whose max is -inf hold no visible key and weigh 0; a zero
-// total gives 0, :116,122): wave w takes every MW-th batch of pieces with a
-// running maximum, so the loads of a batch go out together, and the waves
-// meet in LDS. The piece list has a fixed order, so the result does not
-// depend on timing.
+// no visible page zeroed there. Candidate pieces are numbered 2 (q - qa) +
+// (second wave); wave w takes the batches of kBatch candidates w, w + MW, ...:
+// one lane per candidate reads its pair's meeting point, then the loads of
+// all pieces of the batch go out together and the batch is combined at once
+// against its own maximum with log-sum-exp weights (pieces whose max is -inf
+// hold no visible key and weigh 0; a zero total gives 0, :116,122). Batches
+// and waves are folded in a fixed order, so the result does not depend on
+// timing.
 template <int D, int G>
 __global__ __launch_bounds__(kMergeMaxWaves * 64) void paged_decode_merge_kernel(const Params p) {
   constexpr int kChunks = (D + 63) / 64;  // elements l, l + 64, ... of lane l
-  constexpr int kBatch = 32 / kChunks;    // pieces whose loads go out together
-  constexpr int kListPairs = 1024;        // pairs whose pieces are listed per pass
-  __shared__ int s_slot[2 * kListPairs];  // piece slots, -1 = none
-  __shared__ int s_count;
+  constexpr int kBatch = 32 / kChunks;    // candidates whose loads go out together
   __shared__ float s_top[kMergeMaxWaves], s_sum[kMergeMaxWaves];
   __shared__ float s_acc[kMergeMaxWaves][kChunks * 64];
   const int tid = threadIdx.x;
@@ -789,49 +788,60 @@ __global__ __launch_bounds__(kMergeMaxWaves * 64) void paged_decode_merge_kernel
   const int64_t e = s + npg;
   const int qa = pair_of(s, total, pairs);
   const int qb = pair_of(e - 1, total, pairs);
+  const int cand = 2 * (qb - qa + 1);
+
+  // Slot of candidate j, or -1 when that wave's range misses the unit.
+  auto piece_slot = [&](int j) -> int {
+    const int q = qa + (j >> 1);
+    const int64_t X = range_start(q, total, pairs);
+    const int64_t Xn = range_start(q + 1, total, pairs);
+    const int64_t M = X + p.meet[q];
+    if ((j & 1) == 0)
+      return X < M && X < e && M > s ? 2 * (2 * q) + (X >= s ? 0 : 1) : -1;
+    return M < Xn && M < e && Xn > s ? 2 * (2 * q + 1) + (M >= s ? 0 : 1) : -1;
+  };
+  if (cand == 2) {
+    // Inside one pair's range: a single piece means one wave held the whole
+    // unit and wrote it.
+    const int sl = lane < 2 ? piece_slot(lane) : -1;
+    if (__popcll(__ballot(sl >= 0)) <= 1) return;
+  }
 
   float top = -INFINITY, sum = 0.0f, acc[kChunks];
 #pragma unroll
   for (int c = 0; c < kChunks; ++c) acc[c] = 0.0f;
-  for (int q0 = qa; q0 <= qb; q0 += kListPairs) {
-    // List the pieces of pairs q0 .. q1 in LDS: entries 2 (q - q0) and
-    // 2 (q - q0) + 1 hold the first and second wave's piece of pair q, or -1.
-    const int q1 = min(qb, q0 + kListPairs - 1);
-    const int count = 2 * (q1 - q0 + 1);
-    if (tid == 0) s_count = 0;
-    __syncthreads();
-    for (int q = q0 + tid; q <= q1; q += blockDim.x) {
-      const int64_t X = range_start(q, total, pairs);
-      const int64_t Xn = range_start(q + 1, total, pairs);
-      const int64_t M = X + p.meet[q];
-      const bool front = X < M && X < e && M > s;
-      const bool rear = M < Xn && M < e && Xn > s;
-      s_slot[2 * (q - q0)] = front ? 2 * (2 * q) + (X >= s ? 0 : 1) : -1;
-      s_slot[2 * (q - q0) + 1] = rear ? 2 * (2 * q + 1) + (M >= s ? 0 : 1) : -1;
-      if (front || rear) atomicAdd(&s_count, (int)front + (int)rear);
-    }
-    __syncthreads();
-    if (qa == qb && s_count <= 1) return;  // inside one wave's range: written whole
-    for (int i0 = w * kBatch; i0 < count; i0 += mw * kBatch) {
-      int sl[kBatch];
-      float2 ml[kBatch];
-      float part[kBatch][kChunks];
+  for (int base = w * kBatch; base < cand; base += mw * kBatch) {
+    const int mine = lane < kBatch && base + lane < cand ? piece_slot(base + lane) : -1;
+    int sl[kBatch];
+    float2 ml[kBatch];
+    float part[kBatch][kChunks];
 #pragma unroll
-      for (int u = 0; u < kBatch; ++u) {
-        sl[u] = i0 + u < count ? s_slot[i0 + u] : -1;
-        const int64_t slot = sl[u] < 0 ? 0 : sl[u];
-        ml[u] = p.part_ml[slot * G + g];
+    for (int u = 0; u < kBatch; ++u) {
+      sl[u] = __builtin_amdgcn_readlane(mine, u);
+      const int64_t at = sl[u] < 0 ? 0 : sl[u];
+      ml[u] = p.part_ml[at * G + g];
 #pragma unroll
-        for (int c = 0; c < kChunks; ++c) {
-          const int d = c * 64 + lane;
-          part[u][c] = d < D ? p.part_o[(slot * G + g) * D + d] : 0.0f;
-        }
+      for (int c = 0; c < kChunks; ++c) {
+        const int d = c * 64 + lane;
+        part[u][c] = d < D ? p.part_o[(at * G + g) * D + d] : 0.0f;
       }
-#pragma unroll
-      for (int u = 0; u < kBatch; ++u)
-        if (sl[u] >= 0) lse_add<kChunks>(top, sum, acc, ml[u], part[u]);
     }
-    __syncthreads();  // the piece list is rewritten by the next pass
+    float bt = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u)
+      if (sl[u] >= 0) bt = fmaxf(bt, ml[u].x);
+    if (bt == -INFINITY) continue;  // no visible key in this batch
+    float bs = 0.0f, ba[kChunks];
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c) ba[c] = 0.0f;
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const float wt = sl[u] >= 0 ? __builtin_amdgcn_exp2f(ml[u].x - bt) : 0.0f;
+      bs = __builtin_fmaf(wt, ml[u].y, bs);
+#pragma unroll
+      for (int c = 0; c < kChunks; ++c) ba[c] = __builtin_fmaf(wt, part[u][c], ba[c]);
+    }
+    lse_add<kChunks>(top, sum, acc, make_float2(bt, bs), ba);
   }
   if (mw > 1) {
     // Combine the waves: each publishes its maximum, rescales to the common
