@@ -34,7 +34,9 @@
 //    wave covers 64 / R keys per step. Every step reads K and V rows once and
 //    serves all G query heads of the GQA group from registers.
 //  * q.k uses v_dot2 (fp16 pairs, fp32 accumulate) and a DPP butterfly over
-//    the R lanes; p.v uses mixed-precision FMA (fp32 += fp32 * fp16).
+//    the R lanes. p.v uses v_dot2 over key pairs where the head dim allows it
+//    (128, 256, 512: fp16 probabilities of two keys times their fp16 values),
+//    else mixed-precision FMA (fp32 += fp32 * fp16).
 //  * Online softmax in the log2 domain with a lazy running max: the
 //    accumulators are rescaled only when a score exceeds the running max by
 //    more than 2^8, so steady-state steps do no rescaling.
