@@ -147,6 +147,37 @@ int pda_decode_merge(const void* queries, const void* keys, const void* values,
                      int32_t split_pages,
                      void* workspace, size_t workspace_bytes, void* stream);
 
+/* K/V append with rotary position embedding, one launch for n tokens.
+ * Replaces, per attention layer and step, the reference's
+ *   q = batch.rope(q, rope_dims, ...); k = batch.rope(k, rope_dims, ...)
+ *   (batches.py:195-201 -> portable.py:88-132, non-traditional RoPE) and
+ *   cache.write(layer, rows, k, v) (batches.py:203-207, paged_kv.py:278-283);
+ * the CUDA engine's rope_cache_kernel (cuda/kernels.cu:123-170) fuses the same.
+ *   q, q_out      [n, q_heads, head_dim] fp16; q_out may equal q (in place);
+ *                 both NULL: no queries
+ *   k, v          [n, kv_heads, head_dim] fp16, the new keys and values
+ *   k_arena, v_arena  one layer's arenas (arena_rows rows, `layout` as for the
+ *                 decode call); k, v, both arenas and rows all NULL: no write
+ *   positions     [n] int32, token positions (the angle offsets)
+ *   rows          [n] int32, arena row of each token (table[pos / P] * P +
+ *                 pos % P, batches.py:175-178); rows outside [0, arena_rows)
+ *                 are not written
+ *   inv_freq      [rope_dims / 2] float32 device array: angle of pair i =
+ *                 float(position) * inv_freq[i] in float32, i.e.
+ *                 base^(-2i / rope_dims) or 1 / freqs[i] (portable.py:117-121)
+ * Element i < rope_dims / 2 of a head pairs with i + rope_dims / 2:
+ *   out[i] = x[i] cos - x[i + h] sin, out[i + h] = x[i + h] cos + x[i] sin,
+ * in float32, rounded to fp16; elements from rope_dims on are copied, and the
+ * values are copied unchanged. rope_dims = 0 writes K/V without rotation
+ * (KVCache.write alone). Requires rope_dims even, <= head_dim <= 512. No
+ * workspace; enqueued on `stream`. */
+int pda_rope_append(const void* q, void* q_out, const void* k, const void* v,
+                    void* k_arena, void* v_arena, const int32_t* positions,
+                    const int32_t* rows, int32_t n, int32_t q_heads,
+                    int32_t kv_heads, int32_t head_dim, int32_t page_size,
+                    int64_t arena_rows, int32_t layout, int32_t rope_dims,
+                    const float* inv_freq, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,196 @@
+// K/V append with rotary position embedding for MI355X (gfx950), C-ABI in
+// pda.h (pda_rope_append).
+//
+// Reference steps fused here, per attention layer and decode step:
+//   q = batch.rope(q, dims, base | freqs); k = batch.rope(k, ...)
+//       (python/instinct/batches.py:195-201 -> backends/portable.py:88-132,
+//       the non-traditional "split-half" rotation: element i pairs with
+//       i + dims / 2, angle = position * inv_freq[i], computed in float32)
+//   cache.write(layer, rows, k, v)
+//       (batches.py:203-207 -> paged_kv.py:278-283: scatter the rotated key
+//       and the value of each token into arena row rows[t])
+// The CUDA engine fuses the same steps (cuda/kernels.cu:123-170).
+//
+// MI355X design: one workgroup per (token, chunk of heads), so a decode batch
+// of 64 tokens still spreads over a few hundred workgroups. The angles of the
+// token are computed once per workgroup into LDS (sincosf with full range
+// reduction: positions reach 10^5 and more); lanes then walk the rotation
+// pairs of consecutive elements, so every wave instruction touches one
+// contiguous run of a head. The arena write goes to either K/V layout (rows or
+// page tiles) by the same strides as the decode kernel. The rotation uses
+// separately rounded float32 products and sums (no contraction), the order of
+// the reference's float32 expression, and rounds to fp16 to nearest even.
+
+#include <hip/hip_runtime.h>
+
+#include <stdint.h>
+
+#include "pda.h"
+#include "pda_internal.h"
+
+namespace {
+
+typedef _Float16 f16;
+
+constexpr int kAppendThreads = 256;
+constexpr int kHeadsPerGroup = 4;  // heads of one token per workgroup
+constexpr int kMaxHalf = 256;      // rope_dims / 2 for head_dim <= 512
+constexpr int kMaxHeadDim = 2 * kMaxHalf;
+
+struct AppendParams {
+  const f16* q;
+  f16* q_out;
+  const f16* k;
+  const f16* v;
+  f16* k_arena;
+  f16* v_arena;
+  const int32_t* positions;
+  const int32_t* rows;
+  const float* inv_freq;
+  int64_t arena_rows;
+  int32_t hq;        // query heads rotated (0 when q is null)
+  int32_t hkv;       // kv heads written (0 when k is null)
+  int32_t d;         // head_dim
+  int32_t half;      // rope_dims / 2
+  int32_t page_size;
+  int32_t layout;
+};
+
+// Element e of kv head h in arena row `row`, in either layout.
+__device__ __forceinline__ int64_t arena_index(const AppendParams& p, int64_t row, int h,
+                                               int e) {
+  if (p.layout == PDA_LAYOUT_ROWS) return (row * p.hkv + h) * p.d + e;
+  const int64_t page = row / p.page_size;
+  const int64_t slot = row - page * p.page_size;
+  return ((page * p.hkv + h) * p.page_size + slot) * p.d + e;
+}
+
+// Rotates one head: pairs (j, j + half) for j < half, the elements from
+// 2 * half on are copied. `tid0`/`step` spread the work over the threads.
+__device__ __forceinline__ void rotate_head(const f16* src, f16* dst, const float* s_cos,
+                                            const float* s_sin, int half, int d, int tid0,
+                                            int step) {
+  for (int j = tid0; j < half; j += step) {
+    const float x1 = (float)src[j];
+    const float x2 = (float)src[j + half];
+    const float c = s_cos[j], s = s_sin[j];
+    dst[j] = (f16)__fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, s));
+    dst[j + half] = (f16)__fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, s));
+  }
+  for (int e = 2 * half + tid0; e < d; e += step) dst[e] = src[e];
+}
+
+__global__ __launch_bounds__(kAppendThreads) void rope_append_kernel(const AppendParams p) {
+  __shared__ float s_cos[kMaxHalf], s_sin[kMaxHalf];
+  const int t = blockIdx.x;
+  const int tid = threadIdx.x;
+  if (p.half > 0) {
+    const float pos = (float)p.positions[t];
+    for (int j = tid; j < p.half; j += kAppendThreads) {
+      float s, c;
+      sincosf(__fmul_rn(pos, p.inv_freq[j]), &s, &c);
+      s_cos[j] = c;
+      s_sin[j] = s;
+    }
+    __syncthreads();
+  }
+  // Heads of this workgroup: query heads [0, hq), then kv heads.
+  const int h0 = blockIdx.y * kHeadsPerGroup;
+  const int h1 = min(h0 + kHeadsPerGroup, p.hq + p.hkv);
+  const int64_t row = p.hkv > 0 ? (int64_t)p.rows[t] : -1;
+  const bool write = row >= 0 && row < p.arena_rows;  // other rows are skipped
+  // Threads of one head: kAppendThreads / kHeadsPerGroup consecutive lanes.
+  constexpr int kPerHead = kAppendThreads / kHeadsPerGroup;
+  const int h = h0 + tid / kPerHead;
+  const int tid0 = tid % kPerHead;
+  if (h >= h1) return;
+  if (h < p.hq) {
+    const int64_t base = ((int64_t)t * p.hq + h) * p.d;
+    rotate_head(p.q + base, p.q_out + base, s_cos, s_sin, p.half, p.d, tid0, kPerHead);
+    return;
+  }
+  if (!write) return;
+  const int kh = h - p.hq;
+  const int64_t base = ((int64_t)t * p.hkv + kh) * p.d;
+  f16* const kdst = p.k_arena + arena_index(p, row, kh, 0);
+  f16* const vdst = p.v_arena + arena_index(p, row, kh, 0);
+  rotate_head(p.k + base, kdst, s_cos, s_sin, p.half, p.d, tid0, kPerHead);
+  for (int e = tid0; e < p.d; e += kPerHead) vdst[e] = p.v[base + e];
+}
+
+using pda_internal::fail;
+using pda_internal::ok;
+
+}  // namespace
+
+extern "C" {
+
+int pda_rope_append(const void* q, void* q_out, const void* k, const void* v,
+                    void* k_arena, void* v_arena, const int32_t* positions,
+                    const int32_t* rows, int32_t n, int32_t q_heads, int32_t kv_heads,
+                    int32_t head_dim, int32_t page_size, int64_t arena_rows,
+                    int32_t layout, int32_t rope_dims, const float* inv_freq,
+                    void* stream) {
+  if (n < 0 || head_dim <= 0 || head_dim > kMaxHeadDim)
+    return fail(PDA_ERR_INVALID_ARGUMENT, "n=%d head_dim=%d (need n >= 0, 0 < head_dim <= %d)",
+                n, head_dim, kMaxHeadDim);
+  if (n == 0) return ok();  // nothing is read or written (buffers may be NULL)
+  if (rope_dims < 0 || rope_dims > head_dim || rope_dims % 2)
+    return fail(PDA_ERR_INVALID_ARGUMENT,
+                "rope_dims %d must be even and within [0, head_dim %d]", rope_dims, head_dim);
+  const bool rotate_q = q != nullptr || q_out != nullptr;
+  if (rotate_q && (!q || !q_out || q_heads <= 0))
+    return fail(PDA_ERR_INVALID_ARGUMENT, "queries need q, q_out and q_heads > 0");
+  const bool append = k || v || k_arena || v_arena || rows;
+  if (append) {
+    if (!k || !v || !k_arena || !v_arena || !rows || kv_heads <= 0)
+      return fail(PDA_ERR_INVALID_ARGUMENT,
+                  "the K/V write needs k, v, both arenas, rows and kv_heads > 0");
+    if (layout != PDA_LAYOUT_ROWS && layout != PDA_LAYOUT_PAGES)
+      return fail(PDA_ERR_INVALID_ARGUMENT, "unknown K/V layout %d", layout);
+    if (arena_rows <= 0 || (layout == PDA_LAYOUT_PAGES && (page_size <= 0 || arena_rows % page_size)))
+      return fail(PDA_ERR_INVALID_ARGUMENT,
+                  "arena_rows %lld must be positive (a multiple of page_size %d for page tiles)",
+                  (long long)arena_rows, page_size);
+  }
+  if (rope_dims > 0 && (!positions || !inv_freq))
+    return fail(PDA_ERR_INVALID_ARGUMENT, "rotation needs positions and inv_freq");
+  const uintptr_t mis = (uintptr_t)q | (uintptr_t)q_out | (uintptr_t)k | (uintptr_t)v |
+                        (uintptr_t)k_arena | (uintptr_t)v_arena;
+  if (mis & 1) return fail(PDA_ERR_ALIGNMENT, "fp16 buffers must be 2-byte aligned");
+  if ((uintptr_t)positions & 3 || (uintptr_t)rows & 3 || (uintptr_t)inv_freq & 3)
+    return fail(PDA_ERR_ALIGNMENT, "int32/float32 buffers must be 4-byte aligned");
+  const int hq = rotate_q ? q_heads : 0;
+  const int hkv = append ? kv_heads : 0;
+  if (hq + hkv == 0) return ok();
+  if ((int64_t)hq + hkv > 65535LL * kHeadsPerGroup)
+    return fail(PDA_ERR_INVALID_ARGUMENT, "too many heads (%d)", hq + hkv);
+
+  AppendParams prm;
+  prm.q = static_cast<const f16*>(q);
+  prm.q_out = static_cast<f16*>(q_out);
+  prm.k = static_cast<const f16*>(k);
+  prm.v = static_cast<const f16*>(v);
+  prm.k_arena = static_cast<f16*>(k_arena);
+  prm.v_arena = static_cast<f16*>(v_arena);
+  prm.positions = positions;
+  prm.rows = rows;
+  prm.inv_freq = inv_freq;
+  prm.arena_rows = arena_rows;
+  prm.hq = hq;
+  prm.hkv = hkv;
+  prm.d = head_dim;
+  prm.half = rope_dims / 2;
+  prm.page_size = page_size;
+  prm.layout = layout;
+  void* args[] = {&prm};
+  const dim3 grid(n, (hq + hkv + kHeadsPerGroup - 1) / kHeadsPerGroup);
+  const hipError_t err =
+      hipLaunchKernel(reinterpret_cast<const void*>(rope_append_kernel), grid,
+                      dim3(kAppendThreads), args, 0, static_cast<hipStream_t>(stream));
+  if (err != hipSuccess)
+    return fail(PDA_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(err));
+  return ok();
+}
+
+}  // extern "C"

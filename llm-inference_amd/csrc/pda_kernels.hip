@@ -59,6 +59,30 @@
 #include <utility>
 
 #include "pda.h"
+#include "pda_internal.h"
+
+namespace pda_internal {
+
+namespace {
+thread_local char g_error[512] = "";
+}  // namespace
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_error, sizeof(g_error), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int ok() {
+  g_error[0] = '\0';
+  return PDA_OK;
+}
+
+const char* last_error() { return g_error; }
+
+}  // namespace pda_internal
 
 namespace {
 
@@ -876,20 +900,8 @@ __global__ __launch_bounds__(kMergeMaxWaves * 64) void paged_decode_merge_kernel
 // ---------------------------------------------------------------------------
 // Host side: validation, planning, dispatch.
 
-thread_local char g_error[512] = "";
-
-int fail(int code, const char* fmt, ...) {
-  va_list ap;
-  va_start(ap, fmt);
-  vsnprintf(g_error, sizeof(g_error), fmt, ap);
-  va_end(ap);
-  return code;
-}
-
-int ok() {
-  g_error[0] = '\0';
-  return PDA_OK;
-}
+using pda_internal::fail;
+using pda_internal::ok;
 
 using KernelFn = void (*)(Params);
 
@@ -1053,7 +1065,7 @@ extern "C" {
 
 int pda_version(void) { return (0 << 16) | 5; }
 
-const char* pda_last_error(void) { return g_error; }
+const char* pda_last_error(void) { return pda_internal::last_error(); }
 
 int pda_workspace_bytes(int32_t batch, int32_t q_heads, int32_t kv_heads,
                         int32_t head_dim, int32_t page_size,

@@ -4,9 +4,12 @@ Counterpart of ``DecodeBatch`` (python/instinct/batches.py:142-253) for the
 MI355X kernel: one new token per sequence, page tables packed to
 ``[batch, width]`` int32 with zero padding (:170-179), ``lengths =
 positions + 1`` (:162-164), write rows ``table[pos // P] * P + pos % P``
-(:175-178), and :meth:`DecodeBatch.attend`, which writes the new K/V first
-and then attends over ``[first, length)`` (:203-226), returning
-``[batch, q_heads * head_dim]``.
+(:175-178), :meth:`DecodeBatch.rope` (:195-201) and
+:meth:`DecodeBatch.attend`, which writes the new K/V first and then attends
+over ``[first, length)`` (:203-226), returning ``[batch, q_heads *
+head_dim]``. :meth:`DecodeBatch.rope_attend` does the model's two ``rope``
+calls, the write and the attention with the rotation and the write fused into
+one launch.
 
 The packed tables, lengths and write rows are uploaded once per step and
 shared by every layer of a group, as in the reference.
@@ -14,10 +17,12 @@ shared by every layer of a group, as in the reference.
 
 from __future__ import annotations
 
+from typing import Any
+
 import numpy as np
 import torch
 
-from .hip_kernels import paged_decode_attention
+from .hip_kernels import paged_decode_attention, rope, rope_append
 from .paged_kv import KVCache
 
 
@@ -63,6 +68,27 @@ class DecodeBatch:
     def positions(self) -> torch.Tensor:
         return self.offsets
 
+    def rope(self, x: torch.Tensor, dims: int, *, base: float | None = None,
+             freqs: Any = None) -> torch.Tensor:
+        """Rotary embedding of ``[batch, heads, head_dim]`` at each
+        sequence's position (batches.py:195-201, portable.py:88-132)."""
+        return rope(x.to(torch.float16).contiguous(), self.offsets, dims, base=base,
+                    freqs=freqs)
+
+    def rope_attend(self, layer: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
+                    dims: int, scale: float, base: float | None = None, freqs: Any = None,
+                    softcap: float = 0.0) -> torch.Tensor:
+        """``attend(layer, rope(q), rope(k), v)`` with the rotation of q and k
+        and the K/V write in one launch (the model calls of
+        backends/dense.py:99-102 and DecodeBatch.attend, batches.py:203-226)."""
+        group = self.cache.layer_group[layer]
+        cache = self.cache
+        q_rot = rope_append(q.to(torch.float16).contiguous(), k.to(torch.float16).contiguous(),
+                            v.to(torch.float16).contiguous(), cache.keys[layer],
+                            cache.values[layer], self.offsets, self._write[group.name],
+                            page_size=cache.page_size, dims=dims, base=base, freqs=freqs)
+        return self._attend_written(layer, q_rot, scale=scale, softcap=softcap)
+
     def attend(self, layer: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
                scale: float, softcap: float = 0.0) -> torch.Tensor:
         """Write this step's K/V, then paged decode attention
@@ -70,6 +96,11 @@ class DecodeBatch:
         ``v`` are ``[batch, kv_heads, head_dim]``."""
         group = self.cache.layer_group[layer]
         self.cache.write(layer, self._write[group.name], k, v)
+        return self._attend_written(layer, q, scale=scale, softcap=softcap)
+
+    def _attend_written(self, layer: int, q: torch.Tensor, *, scale: float,
+                        softcap: float) -> torch.Tensor:
+        group = self.cache.layer_group[layer]
         out = paged_decode_attention(
             q.to(torch.float16).contiguous(),
             self.cache.keys[layer],

@@ -1,4 +1,5 @@
-"""Paged decode attention on MI355X, behind the reference's operator API.
+"""Paged decode attention and the K/V append on MI355X, behind the
+reference's operator API.
 
 :func:`paged_decode_attention` keeps the signature and meaning of the
 reference's ``paged_decode_attention`` (python/instinct/backends/
@@ -11,10 +12,16 @@ head_dim]`` (3-D) or the page-tile layout ``[pages, kv_heads, page_size,
 head_dim]`` (4-D, see :mod:`instinct_amd.paged_kv`), which the kernel reads
 as whole contiguous tiles.
 
+The step before it, the rotary embedding of the new queries and keys
+(``DecodeBatch.rope``, python/instinct/batches.py:195-201 ->
+backends/portable.py:88-132) and the write of the new keys and values into
+the arena (``KVCache.write``, paged_kv.py:278-283), is :func:`rope_append`
+(one launch), with :func:`rope` and :func:`kv_write` as its two halves.
+
 The work happens in hand-written HIP kernels (libpda.so, see
-``csrc/pda_kernels.hip``) called through the C-ABI of ``include/pda.h``; this
-module only validates, allocates the output and the split workspace, and
-passes device pointers and the current stream.
+``csrc/pda_kernels.hip`` and ``csrc/pda_append.hip``) called through the
+C-ABI of ``include/pda.h``; this module only validates, allocates outputs and
+the split workspace, and passes device pointers and the current stream.
 """
 
 from __future__ import annotations
@@ -22,6 +29,7 @@ from __future__ import annotations
 import ctypes
 from typing import Any
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -118,3 +126,162 @@ def paged_decode_attention(
         ws.numel(), ctypes.c_void_p(stream))
     _lib.check(rc)
     return out
+
+
+# ---------------------------------------------------------------------------
+# Rotary embedding and K/V append.
+
+_inv_freq_cache: dict[tuple, torch.Tensor] = {}
+
+
+def rope_inv_freq(dims: int, *, base: float | None = None, freqs: Any = None,
+                  device: torch.device | str = "cuda") -> torch.Tensor:
+    """float32 ``[dims // 2]`` inverse frequencies on ``device``, as
+    ``portable._rope_plain`` forms them (portable.py:117-121):
+    ``base ** (-arange(0, dims // 2) * 2 / dims)`` in float32, or
+    ``1 / freqs`` (an infinite frequency leaves its pair unrotated). The
+    kernel's angle is float32(position) * inv_freq[i]."""
+    if dims <= 0 or dims % 2:
+        raise ValueError("rope dims must be a positive even number")
+    half = dims // 2
+    f32 = np.float32
+    if freqs is None:
+        if base is None:
+            raise ValueError("rope needs base or freqs")
+        key = ("base", dims, float(base))
+    else:
+        freqs = np.asarray(freqs.cpu() if isinstance(freqs, torch.Tensor) else freqs,
+                           dtype=f32)
+        if freqs.shape[0] < half:
+            raise ValueError("freqs must hold dims // 2 entries")
+        key = ("freqs", dims, freqs[:half].tobytes())
+    device = torch.device(device)
+    key = key + (str(device),)
+    table = _inv_freq_cache.get(key)
+    if table is None:
+        if freqs is None:
+            exponent = (-np.arange(0, half, dtype=f32) * f32(2)) / f32(dims)
+            host = np.power(f32(base), exponent, dtype=f32)
+        else:
+            with np.errstate(divide="ignore"):
+                host = (f32(1) / freqs[:half]).astype(f32)
+        table = torch.as_tensor(host, device=device)
+        _inv_freq_cache[key] = table
+    return table
+
+
+def _check_f16(name: str, t: torch.Tensor, dims: int) -> None:
+    if t.dtype != torch.float16:
+        raise TypeError(f"{name} must be float16, got {t.dtype}")
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be on a GPU")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if t.dim() != dims:
+        raise ValueError(f"{name} must have {dims} dimensions")
+
+
+def _arena_geometry(keys: torch.Tensor, page_size: int) -> tuple[int, int, int, int]:
+    """(layout, arena_rows, kv_heads, head_dim) of a K/V arena."""
+    if keys.dim() == 3:
+        return _lib.PDA_LAYOUT_ROWS, int(keys.shape[0]), int(keys.shape[1]), int(keys.shape[2])
+    if keys.dim() == 4:
+        if int(keys.shape[2]) != page_size:
+            raise ValueError("page-tile arena must be [pages, kv_heads, page_size, head_dim]")
+        return (_lib.PDA_LAYOUT_PAGES, int(keys.shape[0]) * page_size, int(keys.shape[1]),
+                int(keys.shape[3]))
+    raise ValueError("arena must be [rows, kv_heads, head_dim] or "
+                     "[pages, kv_heads, page_size, head_dim]")
+
+
+def _launch_rope_append(q, q_out, k, v, keys, values, positions, rows, *, n, q_heads,
+                        kv_heads, head_dim, page_size, arena_rows, layout, dims, table,
+                        device) -> None:
+    stream = torch.cuda.current_stream(device).cuda_stream
+    ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+    rc = _lib.library().pda_rope_append(
+        ptr(q), ptr(q_out), ptr(k), ptr(v), ptr(keys), ptr(values), ptr(positions),
+        ptr(rows), int(n), int(q_heads), int(kv_heads), int(head_dim), int(page_size),
+        int(arena_rows), int(layout), int(dims), ptr(table), ctypes.c_void_p(stream))
+    _lib.check(rc)
+
+
+def _int32_vector(name: str, t: torch.Tensor, n: int) -> torch.Tensor:
+    if t.dtype != torch.int32 or t.shape != (n,):
+        raise ValueError(f"{name} must be int32 [{n}]")
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be on a GPU")
+    return t.contiguous()
+
+
+def rope_append(q: torch.Tensor | None, k: torch.Tensor, v: torch.Tensor,
+                keys: torch.Tensor, values: torch.Tensor, positions: torch.Tensor,
+                rows: torch.Tensor, *, page_size: int, dims: int, base: float | None = None,
+                freqs: Any = None, q_out: torch.Tensor | None = None) -> torch.Tensor | None:
+    """Rotate this step's queries and keys and write the rotated keys and the
+    values into the arena, in one launch: the reference's
+    ``q = batch.rope(q, dims, ...)``, ``k = batch.rope(k, dims, ...)``
+    (batches.py:195-201) then ``cache.write(layer, rows, k, v)``
+    (batches.py:203-207, paged_kv.py:278-283).
+
+    ``q`` ``[n, q_heads, D]`` (or None), ``k``, ``v`` ``[n, kv_heads, D]``
+    fp16; ``keys``/``values`` one layer's arena in either layout;
+    ``positions`` and ``rows`` int32 ``[n]`` (rows outside the arena are not
+    written). ``dims`` = 0 writes without rotation. Returns the rotated
+    queries (``q_out``, new unless given; ``q_out`` may be ``q``)."""
+    n, kv_heads, head_dim = (int(x) for x in k.shape)
+    layout, arena_rows, a_heads, a_dim = _arena_geometry(keys, page_size)
+    for name, t, d in (("k", k, 3), ("v", v, 3), ("keys", keys, keys.dim()),
+                       ("values", values, keys.dim())):
+        _check_f16(name, t, d)
+    if tuple(v.shape) != tuple(k.shape) or tuple(values.shape) != tuple(keys.shape):
+        raise ValueError("k/v and keys/values must have matching shapes")
+    if (a_heads, a_dim) != (kv_heads, head_dim):
+        raise ValueError("k does not match the arena's kv_heads and head_dim")
+    q_heads = 0
+    if q is not None:
+        _check_f16("q", q, 3)
+        if int(q.shape[0]) != n or int(q.shape[2]) != head_dim:
+            raise ValueError("q must be [n, q_heads, head_dim]")
+        q_heads = int(q.shape[1])
+        if q_out is None:
+            q_out = torch.empty_like(q)
+        _check_f16("q_out", q_out, 3)
+        if q_out.shape != q.shape:
+            raise ValueError("q_out must have q's shape")
+    rows = _int32_vector("rows", rows, n)
+    if n == 0:
+        return q_out
+    table = None
+    if dims:
+        positions = _int32_vector("positions", positions, n)
+        table = rope_inv_freq(dims, base=base, freqs=freqs, device=k.device)
+    _launch_rope_append(q, q_out if q is not None else None, k, v, keys, values,
+                        positions if dims else None, rows, n=n, q_heads=q_heads,
+                        kv_heads=kv_heads, head_dim=head_dim, page_size=page_size,
+                        arena_rows=arena_rows, layout=layout, dims=dims, table=table,
+                        device=k.device)
+    return q_out
+
+
+def rope(x: torch.Tensor, positions: torch.Tensor, dims: int, *, base: float | None = None,
+         freqs: Any = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``DecodeBatch.rope`` (batches.py:195-201): rotate ``[n, heads, D]`` by
+    one position per token (non-traditional RoPE, portable.py:88-132)."""
+    _check_f16("x", x, 3)
+    n, heads, head_dim = (int(s) for s in x.shape)
+    if out is None:
+        out = torch.empty_like(x)
+    positions = _int32_vector("positions", positions, n)
+    table = rope_inv_freq(dims, base=base, freqs=freqs, device=x.device)
+    _launch_rope_append(x, out, None, None, None, None, positions, None, n=n, q_heads=heads,
+                        kv_heads=0, head_dim=head_dim, page_size=0, arena_rows=0,
+                        layout=0, dims=dims, table=table, device=x.device)
+    return out
+
+
+def kv_write(keys: torch.Tensor, values: torch.Tensor, rows: torch.Tensor, k: torch.Tensor,
+             v: torch.Tensor, *, page_size: int) -> None:
+    """``KVCache.write`` (paged_kv.py:278-283): scatter ``k``, ``v``
+    ``[n, kv_heads, D]`` into arena rows ``rows`` in place, either layout."""
+    rope_append(None, k, v, keys, values, rows, rows, page_size=page_size, dims=0)

@@ -204,14 +204,16 @@ class KVCache:
     def write(self, layer: int, rows: torch.Tensor, keys: torch.Tensor,
               values: torch.Tensor) -> None:
         """Scatter new rows ``[n, kv_heads, head_dim]`` into the layer arena
-        in place (paged_kv.py:278-283)."""
-        if self.layout == "rows":
-            self.keys[layer].index_copy_(0, rows.long(), keys.to(self.dtype))
-            self.values[layer].index_copy_(0, rows.long(), values.to(self.dtype))
-            return
-        page, slot = self._split(rows)
-        self.keys[layer][page, :, slot] = keys.to(self.dtype)
-        self.values[layer][page, :, slot] = values.to(self.dtype)
+        in place (paged_kv.py:278-283), with the HIP append kernel; rows
+        outside the arena are not written."""
+        from .hip_kernels import kv_write
+
+        arena = self.keys[layer]
+        if not arena.is_cuda:
+            raise ValueError("KVCache.write runs on the GPU; the arenas are on the CPU")
+        kv_write(arena, self.values[layer], rows.to(device=arena.device, dtype=torch.int32),
+                 keys.to(self.dtype).contiguous(), values.to(self.dtype).contiguous(),
+                 page_size=self.page_size)
 
     def gather(self, layer: int, rows: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
         """Rows of the arena, ``[n, kv_heads, head_dim]`` (paged_kv.py:285-292)."""

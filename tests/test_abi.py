@@ -116,3 +116,49 @@ def test_page_count_limit():
     with pytest.raises(_lib.PdaError) as err:
         _lib.plan(4096, 64, 8, 128, 16, 1 << 24, 1 << 28, 0)
     assert err.value.code == _lib.PDA_ERR_TOO_LONG
+
+
+def append(**overrides):
+    args = dict(q=FAKE, q_out=FAKE, k=FAKE, v=FAKE, k_arena=FAKE, v_arena=FAKE,
+                positions=FAKE, rows=FAKE, n=64, q_heads=28, kv_heads=4, head_dim=128,
+                page_size=16, arena_rows=4096, layout=_lib.PDA_LAYOUT_PAGES, rope_dims=128,
+                inv_freq=FAKE, stream=None)
+    args.update(overrides)
+    return _lib.library().pda_rope_append(*args.values())
+
+
+@pytest.mark.parametrize("overrides", [
+    dict(n=-1),
+    dict(head_dim=0),
+    dict(n=0, head_dim=0),
+    dict(head_dim=1024, rope_dims=0),
+    dict(rope_dims=7),
+    dict(rope_dims=130),
+    dict(rope_dims=-2),
+    dict(q_out=None),                   # q without q_out
+    dict(q_heads=0),
+    dict(v=None),                       # a partial K/V write
+    dict(rows=None),
+    dict(kv_heads=0),
+    dict(layout=2),
+    dict(arena_rows=0),
+    dict(arena_rows=4100),              # not a whole number of page tiles
+    dict(page_size=0),
+    dict(positions=None),               # rotation without positions
+    dict(inv_freq=None),
+])
+def test_append_validation_rejects_bad_arguments(overrides):
+    assert append(**overrides) == _lib.PDA_ERR_INVALID_ARGUMENT
+    assert _lib.library().pda_last_error()
+
+
+def test_append_alignment_and_empty_calls():
+    assert append(k=FAKE + 1) == _lib.PDA_ERR_ALIGNMENT
+    assert append(rows=FAKE + 2) == _lib.PDA_ERR_ALIGNMENT
+    # Nothing to do: no launch, no error.
+    assert append(n=0) == _lib.PDA_OK
+    assert append(q=None, q_out=None, k=None, v=None, k_arena=None, v_arena=None,
+                  rows=None) == _lib.PDA_OK
+    # Rows layout needs no page size; rope_dims 0 needs no positions or table.
+    assert append(n=0, layout=_lib.PDA_LAYOUT_ROWS, page_size=0) == _lib.PDA_OK
+    assert append(n=0, rope_dims=0, positions=None, inv_freq=None) == _lib.PDA_OK

@@ -108,13 +108,28 @@ def test_rows_map_positions_through_the_table():
     np.testing.assert_array_equal(cache.rows(np.array([-1, 2]), 4, 6), [8, 9])
 
 
+def put_rows(cache, layer, rows, k, v):
+    """Test-side scatter (the GPU kernel's write is tested in test_gpu_append)."""
+    for arena, data in ((cache.keys[layer], k), (cache.values[layer], v)):
+        if cache.layout == "rows":
+            arena[rows] = data.half()
+        else:
+            arena[rows // cache.page_size, :, rows % cache.page_size] = data.half()
+
+
+def test_write_runs_on_the_gpu_only():
+    cache = small_cache()
+    with pytest.raises(ValueError, match="GPU"):
+        cache.write(0, torch.tensor([1]), torch.zeros(1, 2, 8), torch.zeros(1, 2, 8))
+
+
 @pytest.mark.parametrize("layout", LAYOUTS)
-def test_write_gather_and_copy_page(layout):
+def test_gather_and_copy_page(layout):
     cache = small_cache(layout)
     rows = torch.tensor([3, 9, 17])
     k = torch.arange(3 * 2 * 8, dtype=torch.float32).view(3, 2, 8)
     v = -k
-    cache.write(0, rows, k, v)
+    put_rows(cache, 0, rows, k, v)
     gk, gv = cache.gather(0, rows)
     assert torch.equal(gk, k.half()) and torch.equal(gv, v.half())
     assert cache.keys[0].abs().sum() == k.abs().sum()
