@@ -14,6 +14,9 @@ the flush is reported as "warm".
 value = algorithmic K/V bytes / median call time (GB/s). The CPU baseline is
 the oracle's threaded C++ restatement of the reference's split-K algorithm,
 timed on a bounded sample of the same workload on this host's cores.
+Also reported: the step before the call, RoPE of the new queries and keys
+plus the K/V append into the arena (one launch, "append"), and one layer's
+decode attention step (append then call, "layer_step_us"), both flushed.
 
 Prints ONE JSON line. Only --gpus 1 is supported (a one-GPU build).
 """
@@ -83,6 +86,25 @@ def time_calls(passes, steps, flush=None):
     wall = time.perf_counter() - t0
     per_pass = [[e[j].elapsed_time(e[j + 1]) for e in ev] for j in range(n)]
     return per_pass, wall
+
+
+def append_inputs(w):
+    """This step's new queries, keys and values for every sequence of the
+    workload, at position length - 1, and the arena rows they go to
+    (table[pos // P] * P + pos % P, batches.py:175-178)."""
+    import torch
+
+    dev = w.q.device
+    gen = torch.Generator(device=dev).manual_seed(7)
+    q = torch.randn(w.q.shape, generator=gen, device=dev).half()
+    k = torch.randn((w.batch, w.kv_heads, w.head_dim), generator=gen, device=dev).half()
+    v = torch.randn((w.batch, w.kv_heads, w.head_dim), generator=gen, device=dev).half()
+    positions = (w.lengths - 1).clamp(min=0).to(torch.int32)
+    pages = w.tables.long().gather(1, (positions.long() // w.page_size)[:, None])[:, 0]
+    rows = (pages * w.page_size + positions.long() % w.page_size).to(torch.int32)
+    q_out = torch.empty_like(q)
+    bytes_moved = 2 * q.numel() * 2 + 2 * (k.numel() + v.numel()) * 2
+    return q, k, v, positions, rows, q_out, bytes_moved
 
 
 def cpu_baseline(w, budget_s):
@@ -246,6 +268,35 @@ def main():
     line["wall_s_timed_loop"] = round(wall, 3)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
+
+    # The step before the attention call: RoPE of the new queries and keys and
+    # the K/V append (one launch), timed alone and followed by the call (one
+    # layer's decode attention step). Runs last: it writes into the arena.
+    from instinct_amd.hip_kernels import rope_append
+
+    aq, ak, av, apos, arows, aq_out, abytes = append_inputs(w)
+
+    def append():
+        rope_append(aq, ak, av, w.keys, w.values, apos, arows, page_size=w.page_size,
+                    dims=w.head_dim, base=1e6, q_out=aq_out)
+
+    def append_and_call():
+        append()
+        call()
+
+    for _ in range(args.warmup):
+        append_and_call()
+    (app_ms,), _ = time_calls([append], args.steps, flushing)
+    (step_ms,), _ = time_calls([append_and_call], args.steps, flushing)
+    app_med = statistics.median(app_ms)
+    line["append"] = {
+        "kernel": "rope_append_kernel (pda_rope_append: RoPE of q and k, K/V write)",
+        "tokens": w.batch,
+        "us_median": round(app_med * 1e3, 2),
+        "bytes": abytes,
+        "GB_per_s": round(abytes / (app_med * 1e-3) / 1e9, 2),
+    }
+    line["layer_step_us"] = round(statistics.median(step_ms) * 1e3, 2)
     print(json.dumps(line), flush=True)
 
 

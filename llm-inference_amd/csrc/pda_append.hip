@@ -11,12 +11,12 @@
 //       and the value of each token into arena row rows[t])
 // The CUDA engine fuses the same steps (cuda/kernels.cu:123-170).
 //
-// MI355X design: one workgroup per (token, chunk of heads), so a decode batch
-// of 64 tokens still spreads over a few hundred workgroups. The angles of the
-// token are computed once per workgroup into LDS (sincosf with full range
-// reduction: positions reach 10^5 and more); lanes then walk the rotation
-// pairs of consecutive elements, so every wave instruction touches one
-// contiguous run of a head. The arena write goes to either K/V layout (rows or
+// MI355X design: one wave per (token, head), four per workgroup, so a decode
+// batch of 64 tokens still spreads over a few hundred workgroups. Lanes walk
+// the rotation pairs of consecutive elements, so every wave instruction
+// touches one contiguous run of a head, and each lane computes its own angles
+// (sincosf with full range reduction: positions reach 10^5 and more) while
+// its source elements load. The arena write goes to either K/V layout (rows or
 // page tiles) by the same strides as the decode kernel. The rotation uses
 // separately rounded float32 products and sums (no contraction), the order of
 // the reference's float32 expression, and rounds to fp16 to nearest even.
@@ -32,8 +32,8 @@ namespace {
 
 typedef _Float16 f16;
 
-constexpr int kAppendThreads = 256;
-constexpr int kHeadsPerGroup = 4;  // heads of one token per workgroup
+constexpr int kHeadsPerGroup = 4;  // heads of one token per workgroup, one wave each
+constexpr int kAppendThreads = 64 * kHeadsPerGroup;
 constexpr int kMaxHalf = 256;      // rope_dims / 2 for head_dim <= 512
 constexpr int kMaxHeadDim = 2 * kMaxHalf;
 
@@ -66,56 +66,45 @@ __device__ __forceinline__ int64_t arena_index(const AppendParams& p, int64_t ro
 }
 
 // Rotates one head: pairs (j, j + half) for j < half, the elements from
-// 2 * half on are copied. `tid0`/`step` spread the work over the threads.
-__device__ __forceinline__ void rotate_head(const f16* src, f16* dst, const float* s_cos,
-                                            const float* s_sin, int half, int d, int tid0,
-                                            int step) {
-  for (int j = tid0; j < half; j += step) {
+// 2 * half on are copied. Lane `lane` of the head's wave takes j = lane,
+// lane + 64, ...; the source elements are loaded before the angles are
+// computed, so their latency overlaps the position and frequency loads.
+__device__ __forceinline__ void rotate_head(const f16* src, f16* dst, float pos,
+                                            const float* inv_freq, int half, int d,
+                                            int lane) {
+  for (int j = lane; j < half; j += 64) {
     const float x1 = (float)src[j];
     const float x2 = (float)src[j + half];
-    const float c = s_cos[j], s = s_sin[j];
+    float s, c;
+    sincosf(__fmul_rn(pos, inv_freq[j]), &s, &c);
     dst[j] = (f16)__fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, s));
     dst[j + half] = (f16)__fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, s));
   }
-  for (int e = 2 * half + tid0; e < d; e += step) dst[e] = src[e];
+  for (int e = 2 * half + lane; e < d; e += 64) dst[e] = src[e];
 }
 
+// One wave per head: workgroup (t, y) takes heads 4y .. 4y + 3 of token t,
+// query heads first, then kv heads. No LDS and no barrier: every wave
+// computes the angles it uses (sincosf with full range reduction).
 __global__ __launch_bounds__(kAppendThreads) void rope_append_kernel(const AppendParams p) {
-  __shared__ float s_cos[kMaxHalf], s_sin[kMaxHalf];
   const int t = blockIdx.x;
-  const int tid = threadIdx.x;
-  if (p.half > 0) {
-    const float pos = (float)p.positions[t];
-    for (int j = tid; j < p.half; j += kAppendThreads) {
-      float s, c;
-      sincosf(__fmul_rn(pos, p.inv_freq[j]), &s, &c);
-      s_cos[j] = c;
-      s_sin[j] = s;
-    }
-    __syncthreads();
-  }
-  // Heads of this workgroup: query heads [0, hq), then kv heads.
-  const int h0 = blockIdx.y * kHeadsPerGroup;
-  const int h1 = min(h0 + kHeadsPerGroup, p.hq + p.hkv);
-  const int64_t row = p.hkv > 0 ? (int64_t)p.rows[t] : -1;
-  const bool write = row >= 0 && row < p.arena_rows;  // other rows are skipped
-  // Threads of one head: kAppendThreads / kHeadsPerGroup consecutive lanes.
-  constexpr int kPerHead = kAppendThreads / kHeadsPerGroup;
-  const int h = h0 + tid / kPerHead;
-  const int tid0 = tid % kPerHead;
-  if (h >= h1) return;
+  const int lane = threadIdx.x & 63;
+  const int h = blockIdx.y * kHeadsPerGroup + (threadIdx.x >> 6);
+  if (h >= p.hq + p.hkv) return;
+  const float pos = p.half > 0 ? (float)p.positions[t] : 0.0f;
   if (h < p.hq) {
     const int64_t base = ((int64_t)t * p.hq + h) * p.d;
-    rotate_head(p.q + base, p.q_out + base, s_cos, s_sin, p.half, p.d, tid0, kPerHead);
+    rotate_head(p.q + base, p.q_out + base, pos, p.inv_freq, p.half, p.d, lane);
     return;
   }
-  if (!write) return;
+  const int64_t row = p.rows[t];
+  if (row < 0 || row >= p.arena_rows) return;  // rows outside the arena are skipped
   const int kh = h - p.hq;
   const int64_t base = ((int64_t)t * p.hkv + kh) * p.d;
-  f16* const kdst = p.k_arena + arena_index(p, row, kh, 0);
+  rotate_head(p.k + base, p.k_arena + arena_index(p, row, kh, 0), pos, p.inv_freq, p.half,
+              p.d, lane);
   f16* const vdst = p.v_arena + arena_index(p, row, kh, 0);
-  rotate_head(p.k + base, kdst, s_cos, s_sin, p.half, p.d, tid0, kPerHead);
-  for (int e = tid0; e < p.d; e += kPerHead) vdst[e] = p.v[base + e];
+  for (int e = lane; e < p.d; e += 64) vdst[e] = p.v[base + e];
 }
 
 using pda_internal::fail;
