@@ -147,6 +147,54 @@ int pda_decode_merge(const void* queries, const void* keys, const void* values,
                      int32_t split_pages,
                      void* workspace, size_t workspace_bytes, void* stream);
 
+/* 8-bit K/V: pda_paged_decode_attention over int8 arenas with one fp16 scale
+ * per (row, kv head) of keys and of values. Replaces the reference's
+ * quantized path, paged_decode_attention(..., scales=(key_scales,
+ * value_scales)) (metal_kernels.py:134-141,164-248 with KVCache bits=8,
+ * paged_kv.py:50-55,176-181): the score is multiplied by the key's scale and
+ * the probability that weights a value row by the value's scale, i.e.
+ * attention over int8 * scale.
+ *   keys, values  int8, [arena_rows, kv_heads, head_dim] (PDA_LAYOUT_ROWS) or
+ *                 [arena_rows / page_size, kv_heads, page_size, head_dim]
+ *                 (PDA_LAYOUT_PAGES), 16-byte aligned
+ *   key_scales, value_scales  fp16, [arena_rows, kv_heads] beside a row
+ *                 arena, [arena_rows / page_size, kv_heads, page_size] beside
+ *                 a page-tile arena
+ * head_dim in {64, 128, 256, 512}; every other argument as for the fp16
+ * call, which shares the workspace sizing (pda_workspace_bytes). The split
+ * and merge passes exist as for fp16; merge with the _q8 entry after a _q8
+ * split. */
+int pda_paged_decode_attention_q8(const void* queries, const void* keys,
+                                  const void* values, const void* key_scales,
+                                  const void* value_scales,
+                                  const int32_t* tables, const int32_t* lengths,
+                                  void* out, int32_t batch, int32_t q_heads,
+                                  int32_t kv_heads, int32_t head_dim,
+                                  int32_t page_size, int32_t table_stride,
+                                  int64_t arena_rows, int32_t layout,
+                                  int32_t longest, float scale, int32_t window,
+                                  float softcap, int32_t split_pages,
+                                  void* workspace, size_t workspace_bytes,
+                                  void* stream);
+int pda_decode_split_q8(const void* queries, const void* keys, const void* values,
+                        const void* key_scales, const void* value_scales,
+                        const int32_t* tables, const int32_t* lengths, void* out,
+                        int32_t batch, int32_t q_heads, int32_t kv_heads,
+                        int32_t head_dim, int32_t page_size, int32_t table_stride,
+                        int64_t arena_rows, int32_t layout, int32_t longest,
+                        float scale, int32_t window, float softcap,
+                        int32_t split_pages, void* workspace,
+                        size_t workspace_bytes, void* stream);
+int pda_decode_merge_q8(const void* queries, const void* keys, const void* values,
+                        const void* key_scales, const void* value_scales,
+                        const int32_t* tables, const int32_t* lengths, void* out,
+                        int32_t batch, int32_t q_heads, int32_t kv_heads,
+                        int32_t head_dim, int32_t page_size, int32_t table_stride,
+                        int64_t arena_rows, int32_t layout, int32_t longest,
+                        float scale, int32_t window, float softcap,
+                        int32_t split_pages, void* workspace,
+                        size_t workspace_bytes, void* stream);
+
 /* K/V append with rotary position embedding, one launch for n tokens.
  * Replaces, per attention layer and step, the reference's
  *   q = batch.rope(q, rope_dims, ...); k = batch.rope(k, rope_dims, ...)

@@ -118,6 +118,11 @@ struct Params {
   int32_t* meet;      // [pairs] pages the first wave of each pair took (workspace)
   float2* part_ml;    // [kSlots][G] (running max, sum) of cut units
   float* part_o;      // [kSlots][G][D] unnormalised outputs of cut units
+  const f16* kscale;  // 8-bit K/V: fp16 scale per (row, kv head) of keys,
+  const f16* vscale;  //   of values (null for fp16 K/V)
+  int64_t scale_page; // scale elements between pages,
+  int32_t scale_head; //   between kv heads of one page,
+  int32_t scale_row;  //   between rows of one page and kv head
   int64_t arena_pages;
   int64_t page_bytes; // K/V arena: bytes between pages,
   int32_t head_bytes; //   between kv heads of one page,
@@ -148,10 +153,14 @@ constexpr int next_pow2(int x) {
 // EPL elements of it as NV chunks of 8 (one 16-byte load each). Chunk c of
 // lane r covers elements [c * DC + r * 8, c * DC + r * 8 + 8), DC = D / NV, so
 // one load instruction of the wave reads whole 128-byte lines of KPS rows.
-template <int D>
+//
+// 8-bit K/V (Q8): a lane holds 16 consecutive int8 elements [r * 16, r * 16 +
+// 16) of its key, one 16-byte load; R = D / 16, and p.v always runs on key
+// pairs, the values of one pair loaded as two 8-byte pieces.
+template <int D, bool Q8 = false>
 struct Geom {
-  static constexpr int EPL = (D >= 80 && D % 16 == 0) ? 16 : 8;  // fp16 per lane
-  static constexpr int NV = EPL / 8;                              // 16-byte loads
+  static constexpr int EPL = Q8 ? 16 : ((D >= 80 && D % 16 == 0) ? 16 : 8);  // per lane
+  static constexpr int NV = Q8 ? 1 : EPL / 8;                     // 16-byte K loads
   static constexpr int DC = D / NV;                               // chunk stride
   static constexpr int SLICES = D / EPL;
   static constexpr int R = next_pow2(SLICES);                     // lanes per key
@@ -162,7 +171,11 @@ struct Geom {
   static constexpr bool PV2 = EPL == 16 && D == 2 * R * 8;
   static constexpr int OPL = PV2 ? 8 : EPL;                       // outputs per lane
   static constexpr int NPAIR = KPS / 2;                           // key pairs per step
+  // Vector memory loads per step: K and V (fp16); K, the two V pieces and the
+  // key scale and the pair's two value scales (8-bit).
+  static constexpr int LOADS = Q8 ? 6 : 2 * NV;
   static_assert(D % EPL == 0 && DC % 8 == 0, "head_dim must be a multiple of 8");
+  static_assert(!Q8 || PV2, "8-bit K/V needs the key-pair p.v layout");
   static_assert(R <= 32, "head_dim too large");
 };
 
@@ -198,6 +211,7 @@ __device__ __forceinline__ float subset_sum(float x) {
 // Sum over the key pairs of the p.v layout (lanes r2, r2 + 2R, ...).
 template <int R>
 __device__ __forceinline__ float pair_sum(float x) {
+  if constexpr (2 * R <= 8) x += dpp<0x128>(x);  // row_ror:8 == lane ^ 8
   if constexpr (2 * R <= 16) x += __shfl_xor(x, 16);
   if constexpr (2 * R <= 32) x += __shfl_xor(x, 32);
   return x;
@@ -264,6 +278,15 @@ __device__ __forceinline__ f16x8 zero_unless(f16x8 x, bool keep) {
   bits.z = keep ? bits.z : 0;
   bits.w = keep ? bits.w : 0;
   return __builtin_bit_cast(f16x8, bits);
+}
+
+// Four int8 values (one dword) as two fp16 pairs, exactly: each byte b is
+// moved, with its sign bit flipped (b + 128), under the fp16 exponent byte
+// 0x64, which reads as 1024 + b + 128; subtracting 1152 leaves b. `sel_a` /
+// `sel_b` choose which bytes (and in which order) form the two pairs.
+__device__ __forceinline__ f16x2 bytes_to_f16x2(uint32_t flipped, uint32_t sel) {
+  const f16x2 biased = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, flipped, sel));
+  return biased - f16x2{(f16)1152.0f, (f16)1152.0f};
 }
 
 struct SeqGeometry {
@@ -338,10 +361,10 @@ __device__ void build_prefix(const Params& p, int* s_prefix, int* s_len) {
 // Split kernel: a persistent grid of wave pairs (see the file comment).
 // At least two waves per SIMD (<= 256 registers): with G = 7 or 8 heads the
 // few values that do not fit live outside the main loop.
-template <int D, int G>
+template <int D, int G, bool Q8>
 __global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void paged_decode_kernel(const Params p) {
-  using Gm = Geom<D>;
+  using Gm = Geom<D, Q8>;
   constexpr int EPL = Gm::EPL, NV = Gm::NV, DC = Gm::DC, R = Gm::R, KPS = Gm::KPS;
   constexpr bool PV2 = Gm::PV2;
   constexpr int OPL = Gm::OPL;
@@ -366,6 +389,10 @@ void paged_decode_kernel(const Params p) {
   // are the second key's dword, 4-7 the first key's.
   const uint32_t sel_lo = hi ? 0x05040100u : 0x01000504u;
   const uint32_t sel_hi = hi ? 0x07060302u : 0x03020706u;
+  // 8-bit: bytes (this lane's key, the other) of two elements, from the
+  // first key's dword (source bytes 4-7) and the second's (0-3).
+  const uint32_t sel8_lo = hi ? 0x05010400u : 0x01050004u;
+  const uint32_t sel8_hi = hi ? 0x07030602u : 0x03070206u;
   const int P = p.page_size;
   const int spp = P / KPS;  // steps per page
   const int nkvg = p.hkv * p.nhg;
@@ -444,12 +471,23 @@ void paged_decode_kernel(const Params p) {
     f16x2 q[G][EPL / 2];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const f16* qp = p.q + ((int64_t)b * p.hq + h0 + g) * D + d0;
+      if constexpr (Q8) {
+        // Elements [r * 16, r * 16 + 16), the slice of the int8 key row.
+        const f16* qp = p.q + ((int64_t)b * p.hq + h0 + g) * D + r * 16;
 #pragma unroll
-      for (int v = 0; v < NV; ++v) {
-        f16x8 xq = zero_unless(*reinterpret_cast<const f16x8*>(qp + DC * v), active);
+        for (int v = 0; v < 2; ++v) {
+          const f16x8 xq = *reinterpret_cast<const f16x8*>(qp + 8 * v);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) q[g][4 * v + i] = f16x2{xq[2 * i], xq[2 * i + 1]};
+          for (int i = 0; i < 4; ++i) q[g][4 * v + i] = f16x2{xq[2 * i], xq[2 * i + 1]};
+        }
+      } else {
+        const f16* qp = p.q + ((int64_t)b * p.hq + h0 + g) * D + d0;
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+          f16x8 xq = zero_unless(*reinterpret_cast<const f16x8*>(qp + DC * v), active);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) q[g][4 * v + i] = f16x2{xq[2 * i], xq[2 * i + 1]};
+        }
       }
     }
 
@@ -467,9 +505,18 @@ void paged_decode_kernel(const Params p) {
     // Addressing: a wave-uniform byte offset per step (page and first key of
     // the step) plus 32-bit per-lane offsets: K by (key, kv head, chunk), V
     // by (key pair, kv head, element group) on the p.v path, else as K.
-    const uint32_t lane_off = (uint32_t)(kk * p.row_bytes + kvh * p.head_bytes + d0 * 2);
+    const uint32_t lane_off =
+        Q8 ? (uint32_t)(kk * p.row_bytes + kvh * p.head_bytes + r * 16)
+           : (uint32_t)(kk * p.row_bytes + kvh * p.head_bytes + d0 * 2);
     const uint32_t v_off =
-        PV2 ? (uint32_t)(2 * kp * p.row_bytes + kvh * p.head_bytes + r2 * 16) : lane_off;
+        Q8    ? (uint32_t)(2 * kp * p.row_bytes + kvh * p.head_bytes + r2 * 8)
+        : PV2 ? (uint32_t)(2 * kp * p.row_bytes + kvh * p.head_bytes + r2 * 16)
+              : lane_off;
+    // 8-bit scales, in elements from the step's first key: this lane's key,
+    // and its pair's keys with this lane's own key first.
+    const uint32_t ks_off = (uint32_t)(kvh * p.scale_head + kk * p.scale_row);
+    const uint32_t vs_own = (uint32_t)(kvh * p.scale_head + (2 * kp + (hi ? 1 : 0)) * p.scale_row);
+    const uint32_t vs_other = (uint32_t)(kvh * p.scale_head + (2 * kp + (hi ? 0 : 1)) * p.scale_row);
 
     // Page-table window: lane i holds the physical id of unit page
     // win + dir * i (lanes past the unit's ends hold an end entry and are
@@ -496,8 +543,11 @@ void paged_decode_kernel(const Params p) {
     int s_t0[kNbuf];
     bool s_ok[kNbuf];
     int64_t last_off = 0;
+    int64_t last_soff = 0;  // 8-bit: scale element of the step's first key
 
     f16x8 kb[kNbuf][NV], vb[kNbuf][NV];
+    f16 ksb[kNbuf];       // 8-bit: this lane's key scale
+    f16x2 vsb[kNbuf];     // 8-bit: value scales of (own key, other key)
 
     auto load_step = [&](int u) {
       if (loading && start_page) {
@@ -527,6 +577,7 @@ void paged_decode_kernel(const Params p) {
         const bool ok = lpid >= 0 && lpid < p.arena_pages;
         const int pid = ok ? lpid : 0;
         last_off = (int64_t)pid * p.page_bytes + lsub * KPS * p.row_bytes;
+        if constexpr (Q8) last_soff = (int64_t)pid * p.scale_page + lsub * KPS * p.scale_row;
         s_real[u] = true;
         s_t0[u] = (first_page + lpa) * P + lsub * KPS;
         s_ok[u] = ok;
@@ -546,10 +597,21 @@ void paged_decode_kernel(const Params p) {
       // hits, never used), so every slot always has one load in flight.
       const char* kq = kbase + last_off + lane_off;
       const char* vq = vbase + last_off + v_off;
+      if constexpr (Q8) {
+        kb[u][0] = *reinterpret_cast<const f16x8*>(kq);
+        const uint2 va = *reinterpret_cast<const uint2*>(vq);
+        const uint2 vc = *reinterpret_cast<const uint2*>(vq + p.row_bytes);
+        vb[u][0] = __builtin_bit_cast(f16x8, i32x4{(int)va.x, (int)va.y, (int)vc.x, (int)vc.y});
+        const f16* ks = p.kscale + last_soff;
+        const f16* vs = p.vscale + last_soff;
+        ksb[u] = ks[ks_off];
+        vsb[u] = f16x2{vs[vs_own], vs[vs_other]};
+      } else {
 #pragma unroll
-      for (int v = 0; v < NV; ++v) {
-        kb[u][v] = *reinterpret_cast<const f16x8*>(kq + 2 * DC * v);
-        vb[u][v] = *reinterpret_cast<const f16x8*>(vq + (PV2 ? v * p.row_bytes : 2 * DC * v));
+        for (int v = 0; v < NV; ++v) {
+          kb[u][v] = *reinterpret_cast<const f16x8*>(kq + 2 * DC * v);
+          vb[u][v] = *reinterpret_cast<const f16x8*>(vq + (PV2 ? v * p.row_bytes : 2 * DC * v));
+        }
       }
     };
 
@@ -560,22 +622,43 @@ void paged_decode_kernel(const Params p) {
       f16x8(&vd)[NV] = vb[u];
       // q.k for every head of the group: v_dot2 over this lane's slice,
       // then the butterfly over the R lanes of the key.
+      // This lane's key elements as fp16 pairs (8-bit: converted exactly).
+      f16x2 kp2[EPL / 2];
+      if constexpr (Q8) {
+        const i32x4 raw = __builtin_bit_cast(i32x4, kd[0]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t flipped = (uint32_t)raw[j] ^ 0x80808080u;
+          kp2[2 * j] = bytes_to_f16x2(flipped, 0x04010400u);
+          kp2[2 * j + 1] = bytes_to_f16x2(flipped, 0x04030402u);
+        }
+      } else {
+#pragma unroll
+        for (int v = 0; v < NV; ++v)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) kp2[4 * v + i] = f16x2{kd[v][2 * i], kd[v][2 * i + 1]};
+      }
       float s[G];
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        float acc = dot2_first(q[g][0], f16x2{kd[0][0], kd[0][1]});
+        float acc = dot2_first(q[g][0], kp2[0]);
 #pragma unroll
-        for (int v = 0; v < NV; ++v) {
-#pragma unroll
-          for (int i = v == 0 ? 1 : 0; i < 4; ++i) {
-            const f16x2 kv2 = f16x2{kd[v][2 * i], kd[v][2 * i + 1]};
-            acc = __builtin_amdgcn_fdot2(q[g][4 * v + i], kv2, acc, false);
-          }
-        }
+        for (int i = 1; i < EPL / 2; ++i) acc = __builtin_amdgcn_fdot2(q[g][i], kp2[i], acc, false);
         s[g] = acc;
       }
 #pragma unroll
       for (int g = 0; g < G; ++g) s[g] = group_sum<R>(s[g]);
+      // Scores in log2 units per unit of s (8-bit: times this key's scale,
+      // metal_kernels.py:52 KEY_SCALE).
+      float sl2 = p.scale_log2;
+      if constexpr (Q8) {
+        const float ksf = (float)ksb[u];
+        sl2 *= ksf;
+        if (p.softcap > 0.0f) {
+#pragma unroll
+          for (int g = 0; g < G; ++g) s[g] *= ksf;
+        }
+      }
       // x = score - running max, in log2 units; softcap c * tanh(x / c)
       // (metal_kernels.py:53) as c * (1 - 2 / (e^(2x/c) + 1)).
       float x[G];
@@ -587,7 +670,7 @@ void paged_decode_kernel(const Params p) {
         }
       } else {
 #pragma unroll
-        for (int g = 0; g < G; ++g) x[g] = __builtin_fmaf(s[g], p.scale_log2, -m[g]);
+        for (int g = 0; g < G; ++g) x[g] = __builtin_fmaf(s[g], sl2, -m[g]);
       }
       if (!(t0 >= first && t0 + KPS <= len)) {
         // Boundary step. A step with no visible key is skipped: before the
@@ -599,7 +682,20 @@ void paged_decode_kernel(const Params p) {
         if (!__any(valid)) return;
 #pragma unroll
         for (int g = 0; g < G; ++g) x[g] = valid ? x[g] : -INFINITY;
-        if constexpr (PV2) {
+        if constexpr (Q8) {
+          // Zero bytes are zero values; the scales of masked keys may hold
+          // anything, so they are zeroed too.
+          const int ta = t0 + 2 * kp;
+          const bool v0 = ta >= first && ta < len, v1 = ta + 1 >= first && ta + 1 < len;
+          i32x4 bits = __builtin_bit_cast(i32x4, vd[0]);
+          bits.x = v0 ? bits.x : 0;
+          bits.y = v0 ? bits.y : 0;
+          bits.z = v1 ? bits.z : 0;
+          bits.w = v1 ? bits.w : 0;
+          vd[0] = __builtin_bit_cast(f16x8, bits);
+          const bool own_ok = hi ? v1 : v0, other_ok = hi ? v0 : v1;
+          vsb[u] = f16x2{own_ok ? vsb[u][0] : (f16)0.0f, other_ok ? vsb[u][1] : (f16)0.0f};
+        } else if constexpr (PV2) {
           const int ta = t0 + 2 * kp;
 #pragma unroll
           for (int v = 0; v < NV; ++v) vd[v] = zero_unless(vd[v], ta + v >= first && ta + v < len);
@@ -623,7 +719,7 @@ void paged_decode_kernel(const Params p) {
             const float e = __builtin_amdgcn_exp2f(s[g] * p.cap_in);
             sc = (1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f)) * p.cap_out;
           } else {
-            sc = s[g] * p.scale_log2;
+            sc = s[g] * sl2;
           }
           sc = x[g] == -INFINITY ? -INFINITY : sc;  // masked keys stay out
           const float mn = fmaxf(m[g], wave_max(sc));
@@ -639,12 +735,31 @@ void paged_decode_kernel(const Params p) {
         // V element pairs (this lane's key, the other key of its pair),
         // shared by all heads.
         f16x2 vv[8];
-        const i32x4 va = __builtin_bit_cast(i32x4, vd[0]);  // key 2 kp
-        const i32x4 vb = __builtin_bit_cast(i32x4, vd[1]);  // key 2 kp + 1
+        if constexpr (Q8) {
+          // Bytes of keys 2 kp (dwords x, y) and 2 kp + 1 (z, w), elements
+          // r2 * 8 .. r2 * 8 + 7: interleave them (this lane's key first),
+          // convert exactly, then weight by the keys' value scales
+          // (metal_kernels.py:58 VALUE_SCALE).
+          const i32x4 raw = __builtin_bit_cast(i32x4, vd[0]);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          vv[2 * j] = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(va[j], vb[j], sel_lo));
-          vv[2 * j + 1] = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(va[j], vb[j], sel_hi));
+          for (int j = 0; j < 2; ++j) {
+            const uint32_t a = (uint32_t)raw[j] ^ 0x80808080u;
+            const uint32_t c = (uint32_t)raw[2 + j] ^ 0x80808080u;
+            const uint32_t lo = __builtin_amdgcn_perm(a, c, sel8_lo);  // elements 4j, 4j + 1
+            const uint32_t hi2 = __builtin_amdgcn_perm(a, c, sel8_hi); // elements 4j + 2, 4j + 3
+            vv[4 * j] = bytes_to_f16x2(lo, 0x04010400u) * vsb[u];
+            vv[4 * j + 1] = bytes_to_f16x2(lo, 0x04030402u) * vsb[u];
+            vv[4 * j + 2] = bytes_to_f16x2(hi2, 0x04010400u) * vsb[u];
+            vv[4 * j + 3] = bytes_to_f16x2(hi2, 0x04030402u) * vsb[u];
+          }
+        } else {
+          const i32x4 va = __builtin_bit_cast(i32x4, vd[0]);  // key 2 kp
+          const i32x4 vb = __builtin_bit_cast(i32x4, vd[1]);  // key 2 kp + 1
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            vv[2 * j] = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(va[j], vb[j], sel_lo));
+            vv[2 * j + 1] = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(va[j], vb[j], sel_hi));
+          }
         }
 #pragma unroll
         for (int g = 0; g < G; ++g) {
@@ -682,7 +797,7 @@ void paged_decode_kernel(const Params p) {
     do {
 #pragma unroll
       for (int u = 0; u < kNbuf; ++u) {
-        wait_vmem<(kNbuf - 1) * 2 * NV>();
+        wait_vmem<(kNbuf - 1) * Gm::LOADS>();
         if (s_real[u]) compute_step(u);
         load_step(u);
       }
@@ -910,39 +1025,59 @@ struct KernelPair {
   KernelFn merge = nullptr;
 };
 
-template <int D, int G>
+template <int D, int G, bool Q8>
 KernelPair pair() {
-  return {paged_decode_kernel<D, G>, paged_decode_merge_kernel<D, G>};
+  return {paged_decode_kernel<D, G, Q8>, paged_decode_merge_kernel<D, G>};
 }
 
-template <int D>
+template <int D, bool Q8>
 KernelPair kernels_for_g(int g) {
   switch (g) {
-    case 1: return pair<D, 1>();
-    case 2: return pair<D, 2>();
-    case 3: return pair<D, 3>();
-    case 4: return pair<D, 4>();
-    case 5: return pair<D, 5>();
-    case 6: return pair<D, 6>();
-    case 7: return pair<D, 7>();
-    case 8: return pair<D, 8>();
+    case 1: return pair<D, 1, Q8>();
+    case 2: return pair<D, 2, Q8>();
+    case 3: return pair<D, 3, Q8>();
+    case 4: return pair<D, 4, Q8>();
+    case 5: return pair<D, 5, Q8>();
+    case 6: return pair<D, 6, Q8>();
+    case 7: return pair<D, 7, Q8>();
+    case 8: return pair<D, 8, Q8>();
   }
   return {};
 }
 
-KernelPair kernels_for(int d, int g) {
+// Compiled head dims: fp16 K/V 64, 80, 96, 128, 256, 512; 8-bit K/V the
+// dims whose p.v runs on key pairs (64, 128, 256, 512).
+KernelPair kernels_for(int d, int g, bool q8) {
+  if (q8) {
+    switch (d) {
+      case 64: return kernels_for_g<64, true>(g);
+      case 128: return kernels_for_g<128, true>(g);
+      case 256: return kernels_for_g<256, true>(g);
+      case 512: return kernels_for_g<512, true>(g);
+    }
+    return {};
+  }
   switch (d) {
-    case 64: return kernels_for_g<64>(g);
-    case 80: return kernels_for_g<80>(g);
-    case 96: return kernels_for_g<96>(g);
-    case 128: return kernels_for_g<128>(g);
-    case 256: return kernels_for_g<256>(g);
-    case 512: return kernels_for_g<512>(g);
+    case 64: return kernels_for_g<64, false>(g);
+    case 80: return kernels_for_g<80, false>(g);
+    case 96: return kernels_for_g<96, false>(g);
+    case 128: return kernels_for_g<128, false>(g);
+    case 256: return kernels_for_g<256, false>(g);
+    case 512: return kernels_for_g<512, false>(g);
   }
   return {};
 }
 
-int keys_per_step(int d) {
+int keys_per_step(int d, bool q8) {
+  if (q8) {
+    switch (d) {
+      case 64: return Geom<64, true>::KPS;
+      case 128: return Geom<128, true>::KPS;
+      case 256: return Geom<256, true>::KPS;
+      case 512: return Geom<512, true>::KPS;
+    }
+    return 0;
+  }
   switch (d) {
     case 64: return Geom<64>::KPS;
     case 80: return Geom<80>::KPS;
@@ -974,7 +1109,7 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 int make_plan(int32_t batch, int32_t q_heads, int32_t kv_heads, int32_t head_dim,
               int32_t page_size, int32_t table_stride, int32_t longest,
-              int32_t window, int32_t split_pages, Plan* out) {
+              int32_t window, int32_t split_pages, Plan* out, bool q8 = false) {
   if (batch < 0 || q_heads <= 0 || kv_heads <= 0 || head_dim <= 0 ||
       page_size <= 0 || table_stride <= 0 || window < 0 || split_pages < 0)
     return fail(PDA_ERR_INVALID_ARGUMENT,
@@ -984,11 +1119,10 @@ int make_plan(int32_t batch, int32_t q_heads, int32_t kv_heads, int32_t head_dim
                 window, split_pages);
   if (q_heads % kv_heads)
     return fail(PDA_ERR_HEAD_RATIO, "query heads must be a multiple of kv heads");
-  if (!kernels_for(head_dim, 1).split)
-    return fail(PDA_ERR_HEAD_DIM,
-                "head_dim %d has no kernel (supported: 64, 80, 96, 128, 256, 512)",
-                head_dim);
-  const int kps = keys_per_step(head_dim);
+  if (!kernels_for(head_dim, 1, q8).split)
+    return fail(PDA_ERR_HEAD_DIM, "head_dim %d has no %s kernel (supported: %s)", head_dim,
+                q8 ? "8-bit" : "fp16", q8 ? "64, 128, 256, 512" : "64, 80, 96, 128, 256, 512");
+  const int kps = keys_per_step(head_dim, q8);
   if (page_size % kps)
     return fail(PDA_ERR_PAGE_SIZE,
                 "page_size %d must be a multiple of %d for head_dim %d",
@@ -1106,25 +1240,30 @@ constexpr int kPassSplit = 1;
 constexpr int kPassMerge = 2;
 
 // Validates, plans and launches the split pass, the merge pass or both.
+// key_scales / value_scales non-null: 8-bit K/V (int8 arenas).
 int decode(int passes, const void* queries, const void* keys, const void* values,
+           const void* key_scales, const void* value_scales,
            const int32_t* tables, const int32_t* lengths, void* out, int32_t batch,
            int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t page_size,
            int32_t table_stride, int64_t arena_rows, int32_t layout, int32_t longest,
            float scale, int32_t window, float softcap, int32_t split_pages, void* workspace,
            size_t workspace_bytes, void* stream) {
+  const bool q8 = key_scales || value_scales;
   Plan pl;
   int rc = make_plan(batch, q_heads, kv_heads, head_dim, page_size, table_stride,
-                     longest, window, split_pages, &pl);
+                     longest, window, split_pages, &pl, q8);
   if (rc) return rc;
   if (batch == 0) return ok();
-  if (!queries || !keys || !values || !tables || !lengths || !out)
+  if (!queries || !keys || !values || !tables || !lengths || !out ||
+      (q8 && (!key_scales || !value_scales)))
     return fail(PDA_ERR_INVALID_ARGUMENT, "null buffer pointer");
   if (arena_rows < page_size)
     return fail(PDA_ERR_INVALID_ARGUMENT, "arena_rows %lld holds no whole page",
                 (long long)arena_rows);
   if (layout != PDA_LAYOUT_ROWS && layout != PDA_LAYOUT_PAGES)
     return fail(PDA_ERR_INVALID_ARGUMENT, "unknown K/V layout %d", layout);
-  const int64_t page_bytes = (int64_t)page_size * kv_heads * head_dim * 2;
+  const int elem = q8 ? 1 : 2;  // bytes per K/V element
+  const int64_t page_bytes = (int64_t)page_size * kv_heads * head_dim * elem;
   if (page_bytes > INT32_MAX)
     return fail(PDA_ERR_TOO_LONG, "one page of the arena exceeds 2^31 bytes");
   if (!(scale == scale) || isinf(scale) || !(softcap >= 0.0f) || isinf(softcap))
@@ -1132,7 +1271,9 @@ int decode(int passes, const void* queries, const void* keys, const void* values
   const uintptr_t mis = (uintptr_t)queries | (uintptr_t)keys | (uintptr_t)values |
                         (uintptr_t)out;
   if (mis & 15)
-    return fail(PDA_ERR_ALIGNMENT, "fp16 buffers must be 16-byte aligned");
+    return fail(PDA_ERR_ALIGNMENT, "query, K/V and output buffers must be 16-byte aligned");
+  if (((uintptr_t)key_scales | (uintptr_t)value_scales) & 1)
+    return fail(PDA_ERR_ALIGNMENT, "fp16 scale buffers must be 2-byte aligned");
   if ((uintptr_t)tables & 3 || (uintptr_t)lengths & 3)
     return fail(PDA_ERR_ALIGNMENT, "int32 buffers must be 4-byte aligned");
   if (!workspace || workspace_bytes < pl.total)
@@ -1141,7 +1282,7 @@ int decode(int passes, const void* queries, const void* keys, const void* values
   if ((uintptr_t)workspace & 255)
     return fail(PDA_ERR_ALIGNMENT, "workspace must be 256-byte aligned");
 
-  const KernelPair kp = kernels_for(head_dim, pl.G);
+  const KernelPair kp = kernels_for(head_dim, pl.G, q8);
   const size_t lds = (size_t)(2 * batch + 1) * sizeof(int32_t);
   const int groups = resident_groups(kp.split, lds);
   if (groups < 0) return fail(PDA_ERR_HIP, "device query failed");
@@ -1160,12 +1301,19 @@ int decode(int passes, const void* queries, const void* keys, const void* values
   prm.part_o = reinterpret_cast<float*>(ws + pl.off_o);
   prm.arena_pages = arena_rows / page_size;
   prm.page_bytes = page_bytes;
-  if (layout == PDA_LAYOUT_ROWS) {  // [rows, kv_heads, head_dim]
-    prm.row_bytes = kv_heads * head_dim * 2;
-    prm.head_bytes = head_dim * 2;
-  } else {  // [pages, kv_heads, page_size, head_dim]
-    prm.row_bytes = head_dim * 2;
-    prm.head_bytes = page_size * head_dim * 2;
+  prm.kscale = static_cast<const f16*>(key_scales);
+  prm.vscale = static_cast<const f16*>(value_scales);
+  prm.scale_page = (int64_t)page_size * kv_heads;
+  if (layout == PDA_LAYOUT_ROWS) {  // [rows, kv_heads, head_dim], scales [rows, kv_heads]
+    prm.row_bytes = kv_heads * head_dim * elem;
+    prm.head_bytes = head_dim * elem;
+    prm.scale_row = kv_heads;
+    prm.scale_head = 1;
+  } else {  // [pages, kv_heads, page_size, head_dim], scales [pages, kv_heads, page_size]
+    prm.row_bytes = head_dim * elem;
+    prm.head_bytes = page_size * head_dim * elem;
+    prm.scale_row = 1;
+    prm.scale_head = page_size;
   }
   prm.batch = batch;
   prm.table_stride = table_stride;
@@ -1211,9 +1359,24 @@ extern "C" {
       int32_t split_pages, void *workspace, size_t workspace_bytes,            \
       void *stream
 #define PDA_DECODE_ARGS                                                        \
-  queries, keys, values, tables, lengths, out, batch, q_heads, kv_heads,       \
-      head_dim, page_size, table_stride, arena_rows, layout, longest, scale,   \
-      window, softcap, split_pages, workspace, workspace_bytes, stream
+  queries, keys, values, nullptr, nullptr, tables, lengths, out, batch,        \
+      q_heads, kv_heads, head_dim, page_size, table_stride, arena_rows,        \
+      layout, longest, scale, window, softcap, split_pages, workspace,         \
+      workspace_bytes, stream
+#define PDA_DECODE_PARAMS_Q8                                                   \
+  const void *queries, const void *keys, const void *values,                   \
+      const void *key_scales, const void *value_scales,                        \
+      const int32_t *tables, const int32_t *lengths, void *out, int32_t batch, \
+      int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t page_size,  \
+      int32_t table_stride, int64_t arena_rows, int32_t layout,                \
+      int32_t longest, float scale, int32_t window, float softcap,             \
+      int32_t split_pages, void *workspace, size_t workspace_bytes,            \
+      void *stream
+#define PDA_DECODE_ARGS_Q8                                                     \
+  queries, keys, values, key_scales, value_scales, tables, lengths, out,       \
+      batch, q_heads, kv_heads, head_dim, page_size, table_stride, arena_rows, \
+      layout, longest, scale, window, softcap, split_pages, workspace,         \
+      workspace_bytes, stream
 
 int pda_paged_decode_attention(PDA_DECODE_PARAMS) {
   return decode(kPassSplit | kPassMerge, PDA_DECODE_ARGS);
@@ -1222,5 +1385,23 @@ int pda_paged_decode_attention(PDA_DECODE_PARAMS) {
 int pda_decode_split(PDA_DECODE_PARAMS) { return decode(kPassSplit, PDA_DECODE_ARGS); }
 
 int pda_decode_merge(PDA_DECODE_PARAMS) { return decode(kPassMerge, PDA_DECODE_ARGS); }
+
+int pda_paged_decode_attention_q8(PDA_DECODE_PARAMS_Q8) {
+  if (!key_scales || !value_scales)
+    return fail(PDA_ERR_INVALID_ARGUMENT, "8-bit K/V needs key and value scales");
+  return decode(kPassSplit | kPassMerge, PDA_DECODE_ARGS_Q8);
+}
+
+int pda_decode_split_q8(PDA_DECODE_PARAMS_Q8) {
+  if (!key_scales || !value_scales)
+    return fail(PDA_ERR_INVALID_ARGUMENT, "8-bit K/V needs key and value scales");
+  return decode(kPassSplit, PDA_DECODE_ARGS_Q8);
+}
+
+int pda_decode_merge_q8(PDA_DECODE_PARAMS_Q8) {
+  if (!key_scales || !value_scales)
+    return fail(PDA_ERR_INVALID_ARGUMENT, "8-bit K/V needs key and value scales");
+  return decode(kPassMerge, PDA_DECODE_ARGS_Q8);
+}
 
 }  // extern "C"

@@ -74,9 +74,13 @@ def paged_decode_attention(
     (metal_kernels.py:164-186). ``split_pages`` is the fewest pages a wave
     reads before the batch is spread over fewer waves (0 = default); the
     result does not depend on it. ``passes`` = "split" or "merge" launches
-    one of the two kernels only (the output is complete after the merge)."""
-    if scales is not None:
-        raise NotImplementedError("8-bit K/V (scales) has no MI355X kernel yet")
+    one of the two kernels only (the output is complete after the merge).
+
+    ``scales`` = (key_scales, value_scales) selects 8-bit K/V
+    (metal_kernels.py:134-141): ``keys``/``values`` are int8 arenas and the
+    scales fp16, one per (row, kv head): ``[rows, kv_heads]`` beside a row
+    arena, ``[pages, kv_heads, page_size]`` beside a page-tile arena."""
+    q8 = scales is not None
     batch, q_heads, head_dim = (int(n) for n in queries.shape)
     kv_heads = int(keys.shape[1])
     if keys.dim() == 3:
@@ -91,13 +95,23 @@ def paged_decode_attention(
                          "[pages, kv_heads, page_size, head_dim]")
     if q_heads % kv_heads:
         raise ValueError("query heads must be a multiple of kv heads")
-    for name, t in (("queries", queries), ("keys", keys), ("values", values)):
-        if t.dtype != torch.float16:
-            raise TypeError(f"{name} must be float16, got {t.dtype}")
+    kv_dtype = torch.int8 if q8 else torch.float16
+    for name, t, dtype in (("queries", queries, torch.float16), ("keys", keys, kv_dtype),
+                           ("values", values, kv_dtype)):
+        if t.dtype != dtype:
+            raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
         if not t.is_cuda:
             raise ValueError(f"{name} must be on a GPU")
         if not t.is_contiguous():
             raise ValueError(f"{name} must be contiguous")
+    if q8:
+        scale_shape = ((int(keys.shape[0]), kv_heads) if keys.dim() == 3
+                       else (int(keys.shape[0]), kv_heads, page_size))
+        for name, t in zip(("key_scales", "value_scales"), scales):
+            if t.dtype != torch.float16 or tuple(t.shape) != scale_shape:
+                raise ValueError(f"{name} must be float16 {list(scale_shape)}")
+            if not t.is_cuda or not t.is_contiguous():
+                raise ValueError(f"{name} must be a contiguous GPU tensor")
     if tuple(keys.shape) != tuple(values.shape) or width != head_dim:
         raise ValueError("keys and values must have the same shape and head_dim")
     if tables.dtype != torch.int32 or lengths.dtype != torch.int32:
@@ -117,9 +131,10 @@ def paged_decode_attention(
     ws = workspace(device, need)
     stream = torch.cuda.current_stream(device).cuda_stream
     entry = {"both": "pda_paged_decode_attention", "split": "pda_decode_split",
-             "merge": "pda_decode_merge"}[passes]
+             "merge": "pda_decode_merge"}[passes] + ("_q8" if q8 else "")
+    extra = (scales[0].data_ptr(), scales[1].data_ptr()) if q8 else ()
     rc = getattr(_lib.library(), entry)(
-        queries.data_ptr(), keys.data_ptr(), values.data_ptr(), tables.data_ptr(),
+        queries.data_ptr(), keys.data_ptr(), values.data_ptr(), *extra, tables.data_ptr(),
         lengths.data_ptr(), out.data_ptr(), batch, q_heads, kv_heads, head_dim,
         int(page_size), stride, arena_rows, layout, int(longest), float(scale),
         int(window), float(softcap), int(split_pages), ws.data_ptr(),

@@ -16,7 +16,7 @@ FAKE = 0x10000  # an aligned, never-dereferenced address
 
 def declared_functions():
     text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
-    return sorted(set(re.findall(r"\b(pda_[a-z_]+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(pda_[a-z0-9_]+)\s*\(", text)))
 
 
 def test_header_declares_the_expected_entry_points():
