@@ -51,6 +51,8 @@ def parse():
     ap.add_argument("--split-pages", type=int, default=0)
     ap.add_argument("--layout", choices=["pages", "rows"], default="pages",
                     help="K/V arena layout: page tiles (MI355X) or the reference's rows")
+    ap.add_argument("--kv-bits", type=int, choices=[16, 8], default=16,
+                    help="K/V storage: fp16, or int8 with a scale per (row, kv head)")
     ap.add_argument("--no-flush", action="store_true", help="skip the flushed pass")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="approximate CPU time budget of the CPU-baseline sample")
@@ -179,13 +181,30 @@ def main():
     torch.cuda.set_device(device)
     w = workloads.CONFIGS[args.config](device=device).to_layout(args.layout)
     kv_bytes = w.kv_bytes()
+    fp16_bytes = kv_bytes
+    scales = None
+    if args.kv_bits == 8:
+        # The same rows quantized as KVCache(bits=8) stores them (absmax / 127
+        # per row and kv head); the bytes read are int8 rows plus fp16 scales.
+        scales = []
+        for name in ("keys", "values"):
+            x = getattr(w, name)
+            s8 = (x.abs().amax(-1).float().clamp(min=1e-4) / 127.0).half()
+            q8 = (x.float() / s8.float()[..., None]).round().clamp(-127, 127).to(torch.int8)
+            setattr(w, name, q8)
+            scales.append(s8)
+            del x
+        scales = tuple(scales)
+        kv_bytes = int(w.spans().sum()) * w.kv_heads * (w.head_dim + 2) * 2
+        torch.cuda.empty_cache()
     out = torch.empty_like(w.q)
 
     def call(passes="both"):
         paged_decode_attention(w.q, w.keys, w.values, w.tables, w.lengths,
                                page_size=w.page_size, longest=w.longest, scale=w.scale,
                                window=w.window, softcap=w.softcap,
-                               split_pages=args.split_pages, out=out, passes=passes)
+                               split_pages=args.split_pages, out=out, passes=passes,
+                               scales=scales)
 
     def split():
         call("split")
@@ -221,7 +240,7 @@ def main():
     waves, _ = _lib.plan(w.batch, w.q_heads, w.kv_heads, w.head_dim, w.page_size,
                          int(w.tables.shape[1]), w.longest, w.window, args.split_pages)
     traffic = None
-    if TRAFFIC_FILE.exists() and args.config == 2:
+    if TRAFFIC_FILE.exists() and args.config == 2 and args.kv_bits == 16:
         traffic = json.loads(TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
     line = {
         "metric": METRIC,
@@ -234,13 +253,13 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16",
+        "dtype": "f16" if args.kv_bits == 16 else "i8 K/V, f16 math",
         "data": "synthetic (seeded N(0,1) K/V/Q, random page permutation)",
         "config": {
             "workload": w.name,
             "batch": w.batch, "q_heads": w.q_heads, "kv_heads": w.kv_heads,
             "head_dim": w.head_dim, "page_size": w.page_size, "window": w.window,
-            "layout": w.layout,
+            "layout": w.layout, "kv_bits": args.kv_bits,
             "longest": w.longest, "kv_bytes": kv_bytes,
             "split_pages": args.split_pages, "stream_waves_max": waves,
             "cache": "warm (no flush)" if args.no_flush else "flushed (1 GiB write + 1 GiB read between calls)",
@@ -257,16 +276,19 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "kernel": f"paged_decode_kernel<{w.head_dim},{min(8, w.q_heads // w.kv_heads)}> "
-                      "(split pass; events around it alone)",
+            "kernel": f"paged_decode_kernel<{w.head_dim},{min(8, w.q_heads // w.kv_heads)},"
+                      f"{str(args.kv_bits == 8).lower()}> (split pass; events around it alone)",
             "us_mean": round(split_mean * 1e3, 2),
             "call_us_mean": round(statistics.fmean(ms) * 1e3, 2),
         },
     }
     if w.meta.get("sharers") is not None:
         line["config"]["unique_kv_bytes"] = w.unique_kv_bytes()
+    if args.kv_bits == 8:
+        # Keys per second in fp16 terms: the fp16 bytes of the same rows / time.
+        line["fp16_equivalent_GB_per_s"] = round(fp16_bytes / (med * 1e-3) / 1e9, 2)
     line["wall_s_timed_loop"] = round(wall, 3)
-    if not args.no_cpu:
+    if not args.no_cpu and args.kv_bits == 16:
         line["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
 
     # The step before the attention call: RoPE of the new queries and keys and
@@ -278,7 +300,7 @@ def main():
 
     def append():
         rope_append(aq, ak, av, w.keys, w.values, apos, arows, page_size=w.page_size,
-                    dims=w.head_dim, base=1e6, q_out=aq_out)
+                    dims=w.head_dim, base=1e6, q_out=aq_out, scales=scales)
 
     def append_and_call():
         append()
@@ -290,7 +312,9 @@ def main():
     (step_ms,), _ = time_calls([append_and_call], args.steps, flushing)
     app_med = statistics.median(app_ms)
     line["append"] = {
-        "kernel": "rope_append_kernel (pda_rope_append: RoPE of q and k, K/V write)",
+        "kernel": ("rope_append_kernel (pda_rope_append: RoPE of q and k, K/V write)"
+                   if args.kv_bits == 16 else
+                   "rope_append_q8_kernel (pda_rope_append_q8: RoPE, quantized K/V write)"),
         "tokens": w.batch,
         "us_median": round(app_med * 1e3, 2),
         "bytes": abytes,

@@ -226,6 +226,22 @@ int pda_rope_append(const void* q, void* q_out, const void* k, const void* v,
                     int64_t arena_rows, int32_t layout, int32_t rope_dims,
                     const float* inv_freq, void* stream);
 
+/* 8-bit K/V: pda_rope_append into int8 arenas. The rotated keys (rounded to
+ * fp16 as the fp16 call writes them) and the values are quantized per (row,
+ * kv head) as the reference's KVCache.write does for bits=8
+ * (paged_kv.py:50-55,278-283): scale = fp16(max(absmax, 1e-4) / 127),
+ * int8 = clip(rint(x / scale), -127, 127); the scales go to key_scales /
+ * value_scales ([arena_rows, kv_heads] beside a row arena, [arena_rows /
+ * page_size, kv_heads, page_size] beside a page-tile arena). Queries stay
+ * fp16. Other arguments as pda_rope_append. */
+int pda_rope_append_q8(const void* q, void* q_out, const void* k, const void* v,
+                       void* k_arena, void* v_arena, void* key_scales,
+                       void* value_scales, const int32_t* positions,
+                       const int32_t* rows, int32_t n, int32_t q_heads,
+                       int32_t kv_heads, int32_t head_dim, int32_t page_size,
+                       int64_t arena_rows, int32_t layout, int32_t rope_dims,
+                       const float* inv_freq, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

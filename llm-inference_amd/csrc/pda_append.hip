@@ -42,8 +42,10 @@ struct AppendParams {
   f16* q_out;
   const f16* k;
   const f16* v;
-  f16* k_arena;
-  f16* v_arena;
+  void* k_arena;      // fp16, or int8 with scale arenas (8-bit K/V)
+  void* v_arena;
+  f16* k_scale;       // 8-bit: fp16 scale per (row, kv head)
+  f16* v_scale;
   const int32_t* positions;
   const int32_t* rows;
   const float* inv_freq;
@@ -55,6 +57,14 @@ struct AppendParams {
   int32_t page_size;
   int32_t layout;
 };
+
+// Scale of kv head h in arena row `row`: [rows, kv_heads] beside a row arena,
+// [pages, kv_heads, page_size] beside a page-tile arena.
+__device__ __forceinline__ int64_t scale_index(const AppendParams& p, int64_t row, int h) {
+  if (p.layout == PDA_LAYOUT_ROWS) return row * p.hkv + h;
+  const int64_t page = row / p.page_size;
+  return (page * p.hkv + h) * p.page_size + (row - page * p.page_size);
+}
 
 // Element e of kv head h in arena row `row`, in either layout.
 __device__ __forceinline__ int64_t arena_index(const AppendParams& p, int64_t row, int h,
@@ -101,25 +111,90 @@ __global__ __launch_bounds__(kAppendThreads) void rope_append_kernel(const Appen
   if (row < 0 || row >= p.arena_rows) return;  // rows outside the arena are skipped
   const int kh = h - p.hq;
   const int64_t base = ((int64_t)t * p.hkv + kh) * p.d;
-  rotate_head(p.k + base, p.k_arena + arena_index(p, row, kh, 0), pos, p.inv_freq, p.half,
-              p.d, lane);
-  f16* const vdst = p.v_arena + arena_index(p, row, kh, 0);
+  rotate_head(p.k + base, static_cast<f16*>(p.k_arena) + arena_index(p, row, kh, 0), pos,
+              p.inv_freq, p.half, p.d, lane);
+  f16* const vdst = static_cast<f16*>(p.v_arena) + arena_index(p, row, kh, 0);
   for (int e = lane; e < p.d; e += 64) vdst[e] = p.v[base + e];
+}
+
+constexpr int kMaxPerLane = kMaxHeadDim / 64;  // elements of a row per lane
+
+// The rotated value of element e of a row (fp16, as rotate_head writes it),
+// reading the element and its rotation partner.
+__device__ __forceinline__ f16 rotated(const f16* src, int e, float pos, const float* inv_freq,
+                                       int half) {
+  if (e >= 2 * half) return src[e];
+  const int j = e < half ? e : e - half;
+  const float x1 = (float)src[j];
+  const float x2 = (float)src[j + half];
+  float s, c;
+  sincosf(__fmul_rn(pos, inv_freq[j]), &s, &c);
+  return e < half ? (f16)__fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, s))
+                  : (f16)__fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, s));
+}
+
+// One row of one wave, lane-owned elements e = lane + 64 i, quantized as
+// paged_kv.quantize (paged_kv.py:50-55): scale = fp16(max(absmax, 1e-4) /
+// 127), q = clip(rint(x / scale), -127, 127).
+__device__ __forceinline__ void quantize_row(const f16 (&x)[kMaxPerLane], int d, int lane,
+                                             int8_t* dst, f16* scale_dst) {
+  float top = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kMaxPerLane; ++i)
+    if (lane + 64 * i < d) top = fmaxf(top, fabsf((float)x[i]));
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) top = fmaxf(top, __shfl_xor(top, off));
+  const f16 scale = (f16)(fmaxf(top, 1e-4f) / 127.0f);
+  const float sf = (float)scale;
+#pragma unroll
+  for (int i = 0; i < kMaxPerLane; ++i) {
+    const int e = lane + 64 * i;
+    if (e < d) {
+      const float q = fminf(fmaxf(rintf((float)x[i] / sf), -127.0f), 127.0f);
+      dst[e] = (int8_t)q;
+    }
+  }
+  if (lane == 0) *scale_dst = scale;
+}
+
+// 8-bit K/V: as rope_append_kernel, with the rotated keys and the values
+// quantized per (row, kv head) into int8 arenas and fp16 scale arenas.
+__global__ __launch_bounds__(kAppendThreads) void rope_append_q8_kernel(const AppendParams p) {
+  const int t = blockIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int h = blockIdx.y * kHeadsPerGroup + (threadIdx.x >> 6);
+  if (h >= p.hq + p.hkv) return;
+  const float pos = p.half > 0 ? (float)p.positions[t] : 0.0f;
+  if (h < p.hq) {
+    const int64_t base = ((int64_t)t * p.hq + h) * p.d;
+    rotate_head(p.q + base, p.q_out + base, pos, p.inv_freq, p.half, p.d, lane);
+    return;
+  }
+  const int64_t row = p.rows[t];
+  if (row < 0 || row >= p.arena_rows) return;  // rows outside the arena are skipped
+  const int kh = h - p.hq;
+  const int64_t base = ((int64_t)t * p.hkv + kh) * p.d;
+  f16 xk[kMaxPerLane], xv[kMaxPerLane];
+#pragma unroll
+  for (int i = 0; i < kMaxPerLane; ++i) {
+    const int e = lane + 64 * i;
+    xk[i] = e < p.d ? rotated(p.k + base, e, pos, p.inv_freq, p.half) : (f16)0.0f;
+    xv[i] = e < p.d ? p.v[base + e] : (f16)0.0f;
+  }
+  const int64_t at = arena_index(p, row, kh, 0);
+  const int64_t sat = scale_index(p, row, kh);
+  quantize_row(xk, p.d, lane, static_cast<int8_t*>(p.k_arena) + at, p.k_scale + sat);
+  quantize_row(xv, p.d, lane, static_cast<int8_t*>(p.v_arena) + at, p.v_scale + sat);
 }
 
 using pda_internal::fail;
 using pda_internal::ok;
 
-}  // namespace
-
-extern "C" {
-
-int pda_rope_append(const void* q, void* q_out, const void* k, const void* v,
-                    void* k_arena, void* v_arena, const int32_t* positions,
-                    const int32_t* rows, int32_t n, int32_t q_heads, int32_t kv_heads,
-                    int32_t head_dim, int32_t page_size, int64_t arena_rows,
-                    int32_t layout, int32_t rope_dims, const float* inv_freq,
-                    void* stream) {
+int rope_append(const void* q, void* q_out, const void* k, const void* v, void* k_arena,
+                void* v_arena, void* k_scale, void* v_scale, bool q8,
+                const int32_t* positions, const int32_t* rows, int32_t n, int32_t q_heads,
+                int32_t kv_heads, int32_t head_dim, int32_t page_size, int64_t arena_rows,
+                int32_t layout, int32_t rope_dims, const float* inv_freq, void* stream) {
   if (n < 0 || head_dim <= 0 || head_dim > kMaxHeadDim)
     return fail(PDA_ERR_INVALID_ARGUMENT, "n=%d head_dim=%d (need n >= 0, 0 < head_dim <= %d)",
                 n, head_dim, kMaxHeadDim);
@@ -130,11 +205,12 @@ int pda_rope_append(const void* q, void* q_out, const void* k, const void* v,
   const bool rotate_q = q != nullptr || q_out != nullptr;
   if (rotate_q && (!q || !q_out || q_heads <= 0))
     return fail(PDA_ERR_INVALID_ARGUMENT, "queries need q, q_out and q_heads > 0");
-  const bool append = k || v || k_arena || v_arena || rows;
+  const bool append = k || v || k_arena || v_arena || rows || (q8 && (k_scale || v_scale));
   if (append) {
-    if (!k || !v || !k_arena || !v_arena || !rows || kv_heads <= 0)
-      return fail(PDA_ERR_INVALID_ARGUMENT,
-                  "the K/V write needs k, v, both arenas, rows and kv_heads > 0");
+    if (!k || !v || !k_arena || !v_arena || !rows || kv_heads <= 0 ||
+        (q8 && (!k_scale || !v_scale)))
+      return fail(PDA_ERR_INVALID_ARGUMENT, "the K/V write needs k, v, both arenas%s, rows "
+                  "and kv_heads > 0", q8 ? ", both scale arenas" : "");
     if (layout != PDA_LAYOUT_ROWS && layout != PDA_LAYOUT_PAGES)
       return fail(PDA_ERR_INVALID_ARGUMENT, "unknown K/V layout %d", layout);
     if (arena_rows <= 0 || (layout == PDA_LAYOUT_PAGES && (page_size <= 0 || arena_rows % page_size)))
@@ -145,7 +221,8 @@ int pda_rope_append(const void* q, void* q_out, const void* k, const void* v,
   if (rope_dims > 0 && (!positions || !inv_freq))
     return fail(PDA_ERR_INVALID_ARGUMENT, "rotation needs positions and inv_freq");
   const uintptr_t mis = (uintptr_t)q | (uintptr_t)q_out | (uintptr_t)k | (uintptr_t)v |
-                        (uintptr_t)k_arena | (uintptr_t)v_arena;
+                        (q8 ? (uintptr_t)k_scale | (uintptr_t)v_scale
+                            : (uintptr_t)k_arena | (uintptr_t)v_arena);
   if (mis & 1) return fail(PDA_ERR_ALIGNMENT, "fp16 buffers must be 2-byte aligned");
   if ((uintptr_t)positions & 3 || (uintptr_t)rows & 3 || (uintptr_t)inv_freq & 3)
     return fail(PDA_ERR_ALIGNMENT, "int32/float32 buffers must be 4-byte aligned");
@@ -160,8 +237,10 @@ int pda_rope_append(const void* q, void* q_out, const void* k, const void* v,
   prm.q_out = static_cast<f16*>(q_out);
   prm.k = static_cast<const f16*>(k);
   prm.v = static_cast<const f16*>(v);
-  prm.k_arena = static_cast<f16*>(k_arena);
-  prm.v_arena = static_cast<f16*>(v_arena);
+  prm.k_arena = k_arena;
+  prm.v_arena = v_arena;
+  prm.k_scale = static_cast<f16*>(k_scale);
+  prm.v_scale = static_cast<f16*>(v_scale);
   prm.positions = positions;
   prm.rows = rows;
   prm.inv_freq = inv_freq;
@@ -174,12 +253,39 @@ int pda_rope_append(const void* q, void* q_out, const void* k, const void* v,
   prm.layout = layout;
   void* args[] = {&prm};
   const dim3 grid(n, (hq + hkv + kHeadsPerGroup - 1) / kHeadsPerGroup);
-  const hipError_t err =
-      hipLaunchKernel(reinterpret_cast<const void*>(rope_append_kernel), grid,
-                      dim3(kAppendThreads), args, 0, static_cast<hipStream_t>(stream));
+  const void* fn = q8 ? reinterpret_cast<const void*>(rope_append_q8_kernel)
+                     : reinterpret_cast<const void*>(rope_append_kernel);
+  const hipError_t err = hipLaunchKernel(fn, grid, dim3(kAppendThreads), args, 0,
+                                         static_cast<hipStream_t>(stream));
   if (err != hipSuccess)
     return fail(PDA_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(err));
   return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+int pda_rope_append(const void* q, void* q_out, const void* k, const void* v,
+                    void* k_arena, void* v_arena, const int32_t* positions,
+                    const int32_t* rows, int32_t n, int32_t q_heads, int32_t kv_heads,
+                    int32_t head_dim, int32_t page_size, int64_t arena_rows,
+                    int32_t layout, int32_t rope_dims, const float* inv_freq,
+                    void* stream) {
+  return rope_append(q, q_out, k, v, k_arena, v_arena, nullptr, nullptr, false, positions,
+                     rows, n, q_heads, kv_heads, head_dim, page_size, arena_rows, layout,
+                     rope_dims, inv_freq, stream);
+}
+
+int pda_rope_append_q8(const void* q, void* q_out, const void* k, const void* v,
+                       void* k_arena, void* v_arena, void* key_scales, void* value_scales,
+                       const int32_t* positions, const int32_t* rows, int32_t n,
+                       int32_t q_heads, int32_t kv_heads, int32_t head_dim,
+                       int32_t page_size, int64_t arena_rows, int32_t layout,
+                       int32_t rope_dims, const float* inv_freq, void* stream) {
+  return rope_append(q, q_out, k, v, k_arena, v_arena, key_scales, value_scales, true,
+                     positions, rows, n, q_heads, kv_heads, head_dim, page_size, arena_rows,
+                     layout, rope_dims, inv_freq, stream);
 }
 
 }  // extern "C"

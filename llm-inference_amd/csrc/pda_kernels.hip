@@ -546,8 +546,10 @@ void paged_decode_kernel(const Params p) {
     int64_t last_soff = 0;  // 8-bit: scale element of the step's first key
 
     f16x8 kb[kNbuf][NV], vb[kNbuf][NV];
-    f16 ksb[kNbuf];       // 8-bit: this lane's key scale
-    f16x2 vsb[kNbuf];     // 8-bit: value scales of (own key, other key)
+    // 8-bit: this lane's key scale and the value scales of its pair's keys
+    // (own, other), kept apart until the step is computed so that no
+    // instruction waits on them at load time.
+    f16 ksb[kNbuf], vs_own_b[kNbuf], vs_other_b[kNbuf];
 
     auto load_step = [&](int u) {
       if (loading && start_page) {
@@ -605,7 +607,8 @@ void paged_decode_kernel(const Params p) {
         const f16* ks = p.kscale + last_soff;
         const f16* vs = p.vscale + last_soff;
         ksb[u] = ks[ks_off];
-        vsb[u] = f16x2{vs[vs_own], vs[vs_other]};
+        vs_own_b[u] = vs[vs_own];
+        vs_other_b[u] = vs[vs_other];
       } else {
 #pragma unroll
         for (int v = 0; v < NV; ++v) {
@@ -694,7 +697,8 @@ void paged_decode_kernel(const Params p) {
           bits.w = v1 ? bits.w : 0;
           vd[0] = __builtin_bit_cast(f16x8, bits);
           const bool own_ok = hi ? v1 : v0, other_ok = hi ? v0 : v1;
-          vsb[u] = f16x2{own_ok ? vsb[u][0] : (f16)0.0f, other_ok ? vsb[u][1] : (f16)0.0f};
+          vs_own_b[u] = own_ok ? vs_own_b[u] : (f16)0.0f;
+          vs_other_b[u] = other_ok ? vs_other_b[u] : (f16)0.0f;
         } else if constexpr (PV2) {
           const int ta = t0 + 2 * kp;
 #pragma unroll
@@ -741,16 +745,17 @@ void paged_decode_kernel(const Params p) {
           // convert exactly, then weight by the keys' value scales
           // (metal_kernels.py:58 VALUE_SCALE).
           const i32x4 raw = __builtin_bit_cast(i32x4, vd[0]);
+          const f16x2 vsp = f16x2{vs_own_b[u], vs_other_b[u]};
 #pragma unroll
           for (int j = 0; j < 2; ++j) {
             const uint32_t a = (uint32_t)raw[j] ^ 0x80808080u;
             const uint32_t c = (uint32_t)raw[2 + j] ^ 0x80808080u;
             const uint32_t lo = __builtin_amdgcn_perm(a, c, sel8_lo);  // elements 4j, 4j + 1
             const uint32_t hi2 = __builtin_amdgcn_perm(a, c, sel8_hi); // elements 4j + 2, 4j + 3
-            vv[4 * j] = bytes_to_f16x2(lo, 0x04010400u) * vsb[u];
-            vv[4 * j + 1] = bytes_to_f16x2(lo, 0x04030402u) * vsb[u];
-            vv[4 * j + 2] = bytes_to_f16x2(hi2, 0x04010400u) * vsb[u];
-            vv[4 * j + 3] = bytes_to_f16x2(hi2, 0x04030402u) * vsb[u];
+            vv[4 * j] = bytes_to_f16x2(lo, 0x04010400u) * vsp;
+            vv[4 * j + 1] = bytes_to_f16x2(lo, 0x04030402u) * vsp;
+            vv[4 * j + 2] = bytes_to_f16x2(hi2, 0x04010400u) * vsp;
+            vv[4 * j + 3] = bytes_to_f16x2(hi2, 0x04030402u) * vsp;
           }
         } else {
           const i32x4 va = __builtin_bit_cast(i32x4, vd[0]);  // key 2 kp

@@ -86,7 +86,8 @@ class DecodeBatch:
         q_rot = rope_append(q.to(torch.float16).contiguous(), k.to(torch.float16).contiguous(),
                             v.to(torch.float16).contiguous(), cache.keys[layer],
                             cache.values[layer], self.offsets, self._write[group.name],
-                            page_size=cache.page_size, dims=dims, base=base, freqs=freqs)
+                            page_size=cache.page_size, dims=dims, base=base, freqs=freqs,
+                            scales=cache.scales(layer))
         return self._attend_written(layer, q_rot, scale=scale, softcap=softcap)
 
     def attend(self, layer: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
@@ -112,5 +113,6 @@ class DecodeBatch:
             scale=scale,
             window=group.window,
             softcap=softcap,
+            scales=self.cache.scales(layer),
         )
         return out.reshape(self.count, -1)

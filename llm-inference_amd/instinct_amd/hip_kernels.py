@@ -211,13 +211,18 @@ def _arena_geometry(keys: torch.Tensor, page_size: int) -> tuple[int, int, int, 
 
 def _launch_rope_append(q, q_out, k, v, keys, values, positions, rows, *, n, q_heads,
                         kv_heads, head_dim, page_size, arena_rows, layout, dims, table,
-                        device) -> None:
+                        device, scales=None) -> None:
     stream = torch.cuda.current_stream(device).cuda_stream
     ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
-    rc = _lib.library().pda_rope_append(
-        ptr(q), ptr(q_out), ptr(k), ptr(v), ptr(keys), ptr(values), ptr(positions),
-        ptr(rows), int(n), int(q_heads), int(kv_heads), int(head_dim), int(page_size),
-        int(arena_rows), int(layout), int(dims), ptr(table), ctypes.c_void_p(stream))
+    lib = _lib.library()
+    head = (ptr(q), ptr(q_out), ptr(k), ptr(v), ptr(keys), ptr(values))
+    tail = (ptr(positions), ptr(rows), int(n), int(q_heads), int(kv_heads), int(head_dim),
+            int(page_size), int(arena_rows), int(layout), int(dims), ptr(table),
+            ctypes.c_void_p(stream))
+    if scales is None:
+        rc = lib.pda_rope_append(*head, *tail)
+    else:
+        rc = lib.pda_rope_append_q8(*head, ptr(scales[0]), ptr(scales[1]), *tail)
     _lib.check(rc)
 
 
@@ -232,7 +237,9 @@ def _int32_vector(name: str, t: torch.Tensor, n: int) -> torch.Tensor:
 def rope_append(q: torch.Tensor | None, k: torch.Tensor, v: torch.Tensor,
                 keys: torch.Tensor, values: torch.Tensor, positions: torch.Tensor,
                 rows: torch.Tensor, *, page_size: int, dims: int, base: float | None = None,
-                freqs: Any = None, q_out: torch.Tensor | None = None) -> torch.Tensor | None:
+                freqs: Any = None, q_out: torch.Tensor | None = None,
+                scales: tuple[torch.Tensor, torch.Tensor] | None = None
+                ) -> torch.Tensor | None:
     """Rotate this step's queries and keys and write the rotated keys and the
     values into the arena, in one launch: the reference's
     ``q = batch.rope(q, dims, ...)``, ``k = batch.rope(k, dims, ...)``
@@ -243,12 +250,29 @@ def rope_append(q: torch.Tensor | None, k: torch.Tensor, v: torch.Tensor,
     fp16; ``keys``/``values`` one layer's arena in either layout;
     ``positions`` and ``rows`` int32 ``[n]`` (rows outside the arena are not
     written). ``dims`` = 0 writes without rotation. Returns the rotated
-    queries (``q_out``, new unless given; ``q_out`` may be ``q``)."""
+    queries (``q_out``, new unless given; ``q_out`` may be ``q``).
+
+    ``scales`` = (key_scales, value_scales) writes 8-bit K/V: ``keys`` and
+    ``values`` are int8 arenas, the rotated keys and the values are quantized
+    per (row, kv head) as ``paged_kv.quantize`` does (paged_kv.py:50-55)."""
     n, kv_heads, head_dim = (int(x) for x in k.shape)
     layout, arena_rows, a_heads, a_dim = _arena_geometry(keys, page_size)
-    for name, t, d in (("k", k, 3), ("v", v, 3), ("keys", keys, keys.dim()),
-                       ("values", values, keys.dim())):
+    for name, t, d in (("k", k, 3), ("v", v, 3)):
         _check_f16(name, t, d)
+    if scales is None:
+        for name, t in (("keys", keys), ("values", values)):
+            _check_f16(name, t, keys.dim())
+    else:
+        scale_shape = ((arena_rows, kv_heads) if layout == _lib.PDA_LAYOUT_ROWS
+                       else (arena_rows // page_size, kv_heads, page_size))
+        for name, t in (("keys", keys), ("values", values)):
+            if t.dtype != torch.int8 or not t.is_cuda or not t.is_contiguous():
+                raise ValueError(f"{name} must be a contiguous int8 GPU tensor")
+        for name, t in zip(("key_scales", "value_scales"), scales):
+            if (t.dtype != torch.float16 or tuple(t.shape) != scale_shape or not t.is_cuda
+                    or not t.is_contiguous()):
+                raise ValueError(f"{name} must be a contiguous float16 GPU tensor "
+                                 f"{list(scale_shape)}")
     if tuple(v.shape) != tuple(k.shape) or tuple(values.shape) != tuple(keys.shape):
         raise ValueError("k/v and keys/values must have matching shapes")
     if (a_heads, a_dim) != (kv_heads, head_dim):
@@ -275,7 +299,7 @@ def rope_append(q: torch.Tensor | None, k: torch.Tensor, v: torch.Tensor,
                         positions if dims else None, rows, n=n, q_heads=q_heads,
                         kv_heads=kv_heads, head_dim=head_dim, page_size=page_size,
                         arena_rows=arena_rows, layout=layout, dims=dims, table=table,
-                        device=k.device)
+                        device=k.device, scales=scales)
     return q_out
 
 
@@ -296,7 +320,10 @@ def rope(x: torch.Tensor, positions: torch.Tensor, dims: int, *, base: float | N
 
 
 def kv_write(keys: torch.Tensor, values: torch.Tensor, rows: torch.Tensor, k: torch.Tensor,
-             v: torch.Tensor, *, page_size: int) -> None:
+             v: torch.Tensor, *, page_size: int,
+             scales: tuple[torch.Tensor, torch.Tensor] | None = None) -> None:
     """``KVCache.write`` (paged_kv.py:278-283): scatter ``k``, ``v``
-    ``[n, kv_heads, D]`` into arena rows ``rows`` in place, either layout."""
-    rope_append(None, k, v, keys, values, rows, rows, page_size=page_size, dims=0)
+    ``[n, kv_heads, D]`` into arena rows ``rows`` in place, either layout
+    (quantized into int8 arenas and their scales when ``scales`` is given)."""
+    rope_append(None, k, v, keys, values, rows, rows, page_size=page_size, dims=0,
+                scales=scales)

@@ -137,9 +137,12 @@ class PagePool:
 
 
 class KVCache:
-    """Per-layer fp16 K/V arenas in device memory plus one page pool per
-    group (paged_kv.py:156-292, 16-bit K/V), in the ``"pages"`` tile layout
-    by default or the reference's ``"rows"`` layout."""
+    """Per-layer K/V arenas in device memory plus one page pool per group
+    (paged_kv.py:156-292), in the ``"pages"`` tile layout by default or the
+    reference's ``"rows"`` layout. ``bits`` = 16 stores fp16 rows; ``bits`` =
+    8 stores int8 rows with one fp16 scale per (row, kv head) (absmax / 127,
+    paged_kv.py:50-55,176-181), the scales ``[rows, kv_heads]`` beside a row
+    arena and ``[pages, kv_heads, page_size]`` beside a page-tile arena."""
 
     def __init__(
         self,
@@ -150,10 +153,15 @@ class KVCache:
         device: torch.device | str = "cuda",
         dtype: torch.dtype = torch.float16,
         layout: str = "pages",
+        bits: int = 16,
     ) -> None:
         if layout not in LAYOUTS:
             raise ValueError(f"layout must be one of {LAYOUTS}")
+        if bits not in (8, 16):
+            raise ValueError("K/V is stored in 16 or 8 bits")
         self.layout = layout
+        self.bits = bits
+        self.storage = torch.int8 if bits == 8 else dtype
         self.page_size = page_size
         self.dtype = dtype
         self.device = torch.device(device)
@@ -162,6 +170,8 @@ class KVCache:
         self.pools = {group.name: PagePool(capacities[group.name]) for group in groups}
         self.keys: dict[int, torch.Tensor] = {}
         self.values: dict[int, torch.Tensor] = {}
+        self.key_scales: dict[int, torch.Tensor] = {}
+        self.value_scales: dict[int, torch.Tensor] = {}
         for group in groups:
             pages = capacities[group.name]
             if layout == "rows":
@@ -169,13 +179,28 @@ class KVCache:
             else:
                 shape = (pages, group.kv_heads, page_size, group.head_dim)
             for layer in group.layers:
-                self.keys[layer] = torch.zeros(shape, dtype=dtype, device=self.device)
-                self.values[layer] = torch.zeros(shape, dtype=dtype, device=self.device)
+                self.keys[layer] = torch.zeros(shape, dtype=self.storage, device=self.device)
+                self.values[layer] = torch.zeros(shape, dtype=self.storage, device=self.device)
+                if bits == 8:
+                    for store in (self.key_scales, self.value_scales):
+                        store[layer] = torch.zeros(shape[:-1], dtype=torch.float16,
+                                                   device=self.device)
+
+    @property
+    def _stores(self) -> tuple[dict[int, torch.Tensor], ...]:
+        """Per-layer arrays indexed by row: K, V and, at 8 bits, their scales."""
+        if self.bits == 8:
+            return self.keys, self.values, self.key_scales, self.value_scales
+        return self.keys, self.values
+
+    def scales(self, layer: int) -> tuple[torch.Tensor, torch.Tensor] | None:
+        """(key_scales, value_scales) of an 8-bit layer, else None."""
+        return (self.key_scales[layer], self.value_scales[layer]) if self.bits == 8 else None
 
     @property
     def device_bytes(self) -> int:
         return sum(t.numel() * t.element_size()
-                   for store in (self.keys, self.values) for t in store.values())
+                   for store in self._stores for t in store.values())
 
     def rows(self, table: np.ndarray, start: int, end: int) -> np.ndarray:
         """Physical rows of logical positions ``[start, end)`` (paged_kv.py:259-265)."""
@@ -189,7 +214,8 @@ class KVCache:
         """Copy the first ``count`` rows of a page (copy-on-write of a shared
         tail, paged_kv.py:267-274)."""
         for layer in group.layers:
-            for arena in (self.keys[layer], self.values[layer]):
+            for store in self._stores:
+                arena = store[layer]
                 if self.layout == "rows":
                     src = slice(source * self.page_size, source * self.page_size + count)
                     dst = slice(target * self.page_size, target * self.page_size + count)
@@ -204,8 +230,8 @@ class KVCache:
     def write(self, layer: int, rows: torch.Tensor, keys: torch.Tensor,
               values: torch.Tensor) -> None:
         """Scatter new rows ``[n, kv_heads, head_dim]`` into the layer arena
-        in place (paged_kv.py:278-283), with the HIP append kernel; rows
-        outside the arena are not written."""
+        in place (paged_kv.py:278-283), quantized at 8 bits, with the HIP
+        append kernel; rows outside the arena are not written."""
         from .hip_kernels import kv_write
 
         arena = self.keys[layer]
@@ -213,12 +239,21 @@ class KVCache:
             raise ValueError("KVCache.write runs on the GPU; the arenas are on the CPU")
         kv_write(arena, self.values[layer], rows.to(device=arena.device, dtype=torch.int32),
                  keys.to(self.dtype).contiguous(), values.to(self.dtype).contiguous(),
-                 page_size=self.page_size)
+                 page_size=self.page_size, scales=self.scales(layer))
+
+    def _pick(self, store: torch.Tensor, rows: torch.Tensor) -> torch.Tensor:
+        if self.layout == "rows":
+            return store[rows.long()]
+        page, slot = self._split(rows)
+        return store[page, :, slot]
 
     def gather(self, layer: int, rows: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-        """Rows of the arena, ``[n, kv_heads, head_dim]`` (paged_kv.py:285-292)."""
-        if self.layout == "rows":
-            index = rows.long()
-            return self.keys[layer][index], self.values[layer][index]
-        page, slot = self._split(rows)
-        return self.keys[layer][page, :, slot], self.values[layer][page, :, slot]
+        """Rows of the arena, ``[n, kv_heads, head_dim]`` in the model dtype,
+        dequantized at 8 bits (paged_kv.py:285-292)."""
+        keys, values = self._pick(self.keys[layer], rows), self._pick(self.values[layer], rows)
+        if self.bits == 8:
+            ks = self._pick(self.key_scales[layer], rows)
+            vs = self._pick(self.value_scales[layer], rows)
+            keys = (keys.float() * ks.float()[..., None]).to(self.dtype)
+            values = (values.float() * vs.float()[..., None]).to(self.dtype)
+        return keys, values

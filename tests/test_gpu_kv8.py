@@ -127,3 +127,129 @@ def test_split_and_merge_passes_and_call_to_call(gpu):
     d = (out.float() - whole.float()).abs()
     assert d.max().item() <= MAX_ABS and d.mean().item() <= MEAN_ABS
     check(qw, "q8 split pages=4", split_pages=4)
+
+
+# ---------------------------------------------------------------------------
+# The 8-bit write: pda_rope_append_q8 (KVCache.write with bits=8).
+
+from instinct_amd import hip_kernels  # noqa: E402
+from instinct_amd.batches import DecodeBatch  # noqa: E402
+from instinct_amd.paged_kv import KVCache, KVGroup  # noqa: E402
+from oracle import rope_append as ra  # noqa: E402
+
+
+def scale_slot(scales, row, page_size, layout):
+    return scales[row] if layout == "rows" else scales[row // page_size, :, row % page_size]
+
+
+def arena_slot(arena, row, page_size, layout):
+    return arena[row] if layout == "rows" else arena[row // page_size, :, row % page_size]
+
+
+@pytest.mark.parametrize("layout", ["pages", "rows"])
+@pytest.mark.parametrize("d,dims", [(128, 128), (128, 0), (64, 64), (512, 256)])
+def test_quantizing_append(gpu, layout, d, dims):
+    rng = np.random.default_rng(d + dims)
+    n, hq, hkv, P, pages = 12, 7, 2, 16, 32
+    q = rng.standard_normal((n, hq, d)).astype(np.float16)
+    k = (rng.standard_normal((n, hkv, d)) * rng.uniform(0.01, 8, (n, hkv, 1))).astype(np.float16)
+    v = rng.standard_normal((n, hkv, d)).astype(np.float16)
+    v[3, 1] = 0  # an all-zero row takes the 1e-4 floor
+    positions = rng.integers(0, 70000, n).astype(np.int32)
+    rows = (rng.permutation(pages)[:n] * P + positions % P).astype(np.int32)
+    rows[5] = -1  # skipped
+    shape = (pages * P, hkv, d) if layout == "rows" else (pages, hkv, P, d)
+    t = lambda a: torch.as_tensor(a, device=gpu)  # noqa: E731
+    keys = torch.full(shape, 7, dtype=torch.int8, device=gpu)
+    values = torch.full(shape, -7, dtype=torch.int8, device=gpu)
+    ks = torch.full(shape[:-1], 3.0, dtype=torch.float16, device=gpu)
+    vs = torch.full(shape[:-1], 3.0, dtype=torch.float16, device=gpu)
+    q_out = hip_kernels.rope_append(t(q), t(k), t(v), keys, values, t(positions), t(rows),
+                                    page_size=P, dims=dims, base=1e6, scales=(ks, vs))
+    torch.cuda.synchronize()
+    inv = ra.inv_freq(dims, base=1e6) if dims else np.zeros(0, np.float32)
+    k_rot = ra.rope(k, positions, dims, inv) if dims else k
+    kq, kscale = kv8.quantize(k_rot)
+    vq, vscale = kv8.quantize(v)
+    keys, values, ks, vs = (x.cpu().numpy() for x in (keys, values, ks, vs))
+    written = set()
+    for i, row in enumerate(rows):
+        if row < 0:
+            continue
+        written.add(int(row))
+        gk, gv = arena_slot(keys, row, P, layout), arena_slot(values, row, P, layout)
+        gks, gvs = scale_slot(ks, row, P, layout), scale_slot(vs, row, P, layout)
+        # Values: bit-exact. Keys: the rotation may differ from NumPy's in the
+        # last bit of the sine/cosine, which can move a quantized value by one.
+        assert np.array_equal(gv, vq[i]) and np.array_equal(gvs, vscale[i]), (i, "values")
+        assert np.abs(gk.astype(np.int32) - kq[i].astype(np.int32)).max() <= 1, (i, "keys")
+        np.testing.assert_allclose(gks.astype(np.float32), kscale[i].astype(np.float32),
+                                   rtol=1e-3)
+    # Nothing else changed.
+    untouched = [r for r in range(pages * P) if r not in written]
+    for r in untouched[:: max(1, len(untouched) // 64)]:
+        assert (arena_slot(keys, r, P, layout) == 7).all()
+        assert (scale_slot(vs, r, P, layout) == 3.0).all()
+    if dims:
+        want = ra.rope(q, positions, dims, inv)
+        assert np.abs(q_out.cpu().numpy().astype(np.float32) - want.astype(np.float32)).max() <= 2e-3
+
+
+@pytest.mark.parametrize("layout", ["pages", "rows"])
+def test_decode_batch_at_8_bits(gpu, layout):
+    """KVCache(bits=8) and DecodeBatch: the write quantizes, the attention
+    reads int8 (batches.py:203-226 with scales, paged_kv.py:278-283), and
+    rope_attend equals rope, rope, attend."""
+    page = 16
+    groups = [KVGroup("full", (0, 1), kv_heads=4, head_dim=128)]
+    positions = np.array([0, 15, 16, 100, 333, 2047])
+    gen = torch.Generator(device=gpu).manual_seed(5)
+
+    def fresh():
+        cache = KVCache(groups, page_size=page, capacities={"full": 256}, device=gpu,
+                        layout=layout, bits=8)
+        pool = cache.pools["full"]
+        tables = {"full": [np.array([pool.allocate(reserved=False)
+                                     for _ in range(p // page + 1)]) for p in positions]}
+        # Rows as quantized N(0, 1) data: int8 ~ N(0, 36^2), scales ~ 1/36
+        # (absmax / 127 of a normal row), so the dequantized arena is ~N(0, 1).
+        g2 = torch.Generator(device=gpu).manual_seed(11)
+        for layer in (0, 1):
+            for store in (cache.keys, cache.values):
+                store[layer].copy_(torch.randn(store[layer].shape, generator=g2, device=gpu)
+                                   .mul(36).round().clamp(-127, 127).to(torch.int8))
+            for store in (cache.key_scales, cache.value_scales):
+                store[layer].copy_(torch.rand(store[layer].shape, generator=g2, device=gpu)
+                                   .mul(0.01).add(1 / 40).half())
+        return cache, DecodeBatch(cache, torch.zeros(6, device=gpu), positions=positions,
+                                  tables=tables)
+
+    q = torch.randn((6, 28, 128), generator=gen, device=gpu).half()
+    k = torch.randn((6, 4, 128), generator=gen, device=gpu).half()
+    v = torch.randn((6, 4, 128), generator=gen, device=gpu).half()
+    c1, b1 = fresh()
+    fused = b1.rope_attend(0, q, k, v, dims=128, base=1e6, scale=128 ** -0.5)
+    c2, b2 = fresh()
+    plain = b2.attend(0, b2.rope(q, 128, base=1e6), b2.rope(k, 128, base=1e6), v,
+                      scale=128 ** -0.5)
+    torch.cuda.synchronize()
+    for a, b in ((c1.keys[0], c2.keys[0]), (c1.values[0], c2.values[0]),
+                 (c1.key_scales[0], c2.key_scales[0]), (c1.value_scales[0], c2.value_scales[0])):
+        assert torch.equal(a, b)
+    d = (fused.float() - plain.float()).abs()
+    assert d.max().item() <= MAX_ABS and d.mean().item() <= MEAN_ABS
+    # Against the oracle on the dequantized arena (rows layout on the host).
+    keys, values = c1.keys[0], c1.values[0]
+    ks, vs = c1.key_scales[0], c1.value_scales[0]
+    if layout == "pages":
+        from instinct_amd.paged_kv import pages_to_rows
+        keys, values = pages_to_rows(keys), pages_to_rows(values)
+        ks, vs = ks.permute(0, 2, 1).reshape(-1, 4), vs.permute(0, 2, 1).reshape(-1, 4)
+    deq_k = kv8.dequantize(keys.cpu().numpy(), ks.cpu().numpy())
+    deq_v = kv8.dequantize(values.cpu().numpy(), vs.cpu().numpy())
+    q_rot = b1.rope(q, 128, base=1e6).cpu().numpy()
+    expected = pa.paged_decode_dense(q_rot, deq_k, deq_v, b1._tables["full"].cpu().numpy(),
+                                     positions + 1, page_size=page, scale=128 ** -0.5)
+    err_max, err_mean = pa.error_stats(fused.view(6, 28, 128).float().cpu().numpy(), expected)
+    print(f"DecodeBatch bits=8 {layout}: max_abs={err_max:.3e} mean_abs={err_mean:.3e}")
+    assert err_max <= MAX_ABS and err_mean <= MEAN_ABS
