@@ -242,6 +242,28 @@ int pda_rope_append_q8(const void* q, void* q_out, const void* k, const void* v,
                        int64_t arena_rows, int32_t layout, int32_t rope_dims,
                        const float* inv_freq, void* stream);
 
+/* Device-side packing of one decode step's page tables. Replaces the host
+ * packing of DecodeBatch.__init__ (batches.py:148-179: tables [B, width] int32
+ * with 0 padding, lengths = positions + 1, write rows table[pos / P] * P +
+ * pos % P) for an engine that keeps every request's page list resident on the
+ * device: seq_tables [num_slots, seq_stride] int32 holds request slot s's
+ * physical pages in row s. For each sequence b of the step (request slot
+ * slots[b], new token at positions[b]) it writes
+ *   tables[b][j]  = seq_tables[slots[b]][j] for j <= positions[b] / page_size,
+ *                   0 for the other j < width;
+ *   lengths[b]    = positions[b] + 1;
+ *   rows[b]       = tables[b][positions[b] / page_size] * page_size +
+ *                   positions[b] % page_size, or -1 when that page index is
+ *                   not below width and seq_stride.
+ * A slot outside [0, num_slots) or a negative position gives a zero row,
+ * length 0 and row -1. One launch on `stream`, no workspace; it can be
+ * captured in a HIP graph with the decode calls that read its outputs. */
+int pda_pack_decode_step(const int32_t* seq_tables, int32_t seq_stride,
+                         int32_t num_slots, const int32_t* slots,
+                         const int32_t* positions, int32_t batch, int32_t width,
+                         int32_t page_size, int32_t* tables, int32_t* lengths,
+                         int32_t* rows, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -56,6 +56,11 @@ SIGNATURES["pda_rope_append"] = (
     ctypes.c_int,
     [c_void_p] * 8 + [c_int32] * 5 + [c_int64, c_int32, c_int32, c_void_p, c_void_p],
 )
+SIGNATURES["pda_pack_decode_step"] = (
+    ctypes.c_int,
+    [c_void_p, c_int32, c_int32, c_void_p, c_void_p, c_int32, c_int32, c_int32,
+     c_void_p, c_void_p, c_void_p, c_void_p],
+)
 SIGNATURES["pda_rope_append_q8"] = (
     ctypes.c_int,
     [c_void_p] * 10 + [c_int32] * 5 + [c_int64, c_int32, c_int32, c_void_p, c_void_p],

@@ -327,3 +327,36 @@ def kv_write(keys: torch.Tensor, values: torch.Tensor, rows: torch.Tensor, k: to
     (quantized into int8 arenas and their scales when ``scales`` is given)."""
     rope_append(None, k, v, keys, values, rows, rows, page_size=page_size, dims=0,
                 scales=scales)
+
+
+def pack_decode_step(seq_tables: torch.Tensor, slots: torch.Tensor, positions: torch.Tensor, *,
+                     width: int, page_size: int, tables: torch.Tensor | None = None,
+                     lengths: torch.Tensor | None = None, rows: torch.Tensor | None = None
+                     ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """``DecodeBatch``'s per-step packing (batches.py:148-179) on the device:
+    from the resident per-slot page tables ``seq_tables [num_slots, stride]``
+    and the step's ``slots``/``positions`` (int32 ``[B]``), the packed tables
+    ``[B, width]`` (0 past the new token's page), ``lengths = positions + 1``
+    and the write rows. Outputs may be given (static buffers of a graph)."""
+    if seq_tables.dtype != torch.int32 or seq_tables.dim() != 2 or not seq_tables.is_cuda:
+        raise ValueError("seq_tables must be an int32 [num_slots, stride] GPU tensor")
+    seq_tables = seq_tables.contiguous()
+    batch = int(slots.shape[0])
+    slots = _int32_vector("slots", slots, batch)
+    positions = _int32_vector("positions", positions, batch)
+    dev = seq_tables.device
+    if tables is None:
+        tables = torch.empty((batch, width), dtype=torch.int32, device=dev)
+    if lengths is None:
+        lengths = torch.empty(batch, dtype=torch.int32, device=dev)
+    if rows is None:
+        rows = torch.empty(batch, dtype=torch.int32, device=dev)
+    if tuple(tables.shape) != (batch, width) or lengths.shape != (batch,) or rows.shape != (batch,):
+        raise ValueError("output shapes do not match the step")
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    rc = _lib.library().pda_pack_decode_step(
+        seq_tables.data_ptr(), int(seq_tables.shape[1]), int(seq_tables.shape[0]),
+        slots.data_ptr(), positions.data_ptr(), batch, int(width), int(page_size),
+        tables.data_ptr(), lengths.data_ptr(), rows.data_ptr(), ctypes.c_void_p(stream))
+    _lib.check(rc)
+    return tables, lengths, rows
