@@ -51,6 +51,9 @@ def parse():
     ap.add_argument("--split-pages", type=int, default=0)
     ap.add_argument("--layout", choices=["pages", "rows"], default="pages",
                     help="K/V arena layout: page tiles (MI355X) or the reference's rows")
+    ap.add_argument("--step-layers", type=int, default=28,
+                    help="layers of the whole-step timing (0 = skip): append + attention "
+                         "per layer, eager and as one captured HIP graph")
     ap.add_argument("--kv-bits", type=int, choices=[16, 8], default=16,
                     help="K/V storage: fp16, or int8 with a scale per (row, kv head)")
     ap.add_argument("--no-flush", action="store_true", help="skip the flushed pass")
@@ -107,6 +110,57 @@ def append_inputs(w):
     q_out = torch.empty_like(q)
     bytes_moved = 2 * q.numel() * 2 + 2 * (k.numel() + v.numel()) * 2
     return q, k, v, positions, rows, q_out, bytes_moved
+
+
+def decode_step(w, scales, layers, steps):
+    """One decode step's attention work for `layers` layers of this workload:
+    table packing on the device, then per layer the RoPE + K/V append and the
+    decode call, run eagerly (launched from Python) and replayed as one
+    captured HIP graph. The layers cycle over four copies of the arena (2.4
+    GB of K/V at config 2), so a layer's K/V are not in the caches."""
+    import torch
+
+    from instinct_amd.step import DecodeStepGraph
+
+    copies = 4
+    arenas = []
+    for i in range(min(copies, layers)):
+        extra = tuple(x.clone() for x in scales) if scales is not None else ()
+        arenas.append((w.keys.clone(), w.values.clone()) + extra)
+    per_layer = [arenas[i % len(arenas)] for i in range(layers)]
+    step = DecodeStepGraph(per_layer, w.tables, batch=w.batch, q_heads=w.q_heads,
+                           page_size=w.page_size, width=int(w.tables.shape[1]), scale=w.scale,
+                           longest=w.longest, dims=w.head_dim, base=1e6, window=w.window,
+                           softcap=w.softcap)
+    step.slots.copy_(torch.arange(w.batch, dtype=torch.int32, device=w.q.device))
+    step.positions.copy_((w.lengths - 1).clamp(min=0))
+    gen = torch.Generator(device=w.q.device).manual_seed(3)
+    for i in range(layers):
+        step.q[i].copy_(torch.randn(step.q[i].shape, generator=gen, device=w.q.device))
+        step.k[i].copy_(torch.randn(step.k[i].shape, generator=gen, device=w.q.device))
+        step.v[i].copy_(torch.randn(step.v[i].shape, generator=gen, device=w.q.device))
+    step.capture()
+
+    def timed(fn, n):
+        times = []
+        for _ in range(n):
+            torch.cuda._sleep(SPIN_CYCLES)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1) * 1e3)
+        return statistics.median(times)
+
+    n = max(5, min(steps, 20))
+    eager = timed(step.run, n)
+    graph = timed(step.replay, n)
+    del step, arenas, per_layer
+    torch.cuda.empty_cache()
+    return {"layers": layers, "launches_per_step": 1 + 3 * layers,
+            "eager_us": round(eager, 1), "graph_us": round(graph, 1),
+            "graph_us_per_layer": round(graph / layers, 2)}
 
 
 def cpu_baseline(w, budget_s):
@@ -321,6 +375,8 @@ def main():
         "GB_per_s": round(abytes / (app_med * 1e-3) / 1e9, 2),
     }
     line["layer_step_us"] = round(statistics.median(step_ms) * 1e3, 2)
+    if args.step_layers > 0:
+        line["decode_step"] = decode_step(w, scales, args.step_layers, args.steps)
     print(json.dumps(line), flush=True)
 
 

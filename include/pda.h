@@ -107,7 +107,7 @@ int pda_plan(int32_t batch, int32_t q_heads, int32_t kv_heads,
  * attention. `longest` is the host-side largest length, as in the reference
  * (a planning hint only: results never depend on it, and lengths above it
  * stay correct). `split_pages` is the fewest pages a wave reads before the
- * stream is spread over fewer waves (0 = 8; results do not depend on it).
+ * stream is spread over fewer waves (0 = 1; results do not depend on it).
  * `arena_rows` is the row count of the keys/values arenas (pages x
  * page_size) and `layout` is PDA_LAYOUT_ROWS or PDA_LAYOUT_PAGES (the reference
  * has one layout, rows); batch <= 8184.

@@ -103,7 +103,7 @@ constexpr int kMaxGroups = 512;                // resident split workgroups (256
 constexpr int kMaxWaves = kMaxGroups * kSplitWaves;
 constexpr int kMaxPairs = kMaxWaves / 2;
 constexpr int kSlots = 2 * kMaxWaves;          // partial slots: first and last unit of a wave
-constexpr int kMinPagesPerWave = 8;            // default: spread no thinner than this
+constexpr int kMinPagesPerWave = 1;            // default: spread no thinner than this
 constexpr int kMaxBatch = 8184;                // per-sequence tables in LDS: (2B + 1) ints
 constexpr int kMergeMaxWaves = 16;             // waves per merge workgroup, at most
 

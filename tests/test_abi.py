@@ -91,7 +91,8 @@ def test_workspace_and_plan_are_consistent():
     assert waves == 2048 and per_wave * waves >= 64 * 4 * 512
     # Few pages: the stream uses fewer wave pairs, each wave with about
     # split_pages pages (40 pages: 3 pairs of 7 pages a wave).
-    assert _lib.plan(1, 8, 8, 128, 16, 64, 64, 0) == (6, 7)
+    # 40 visible pages: one page per wave by default, two with split_pages=2.
+    assert _lib.plan(1, 8, 8, 128, 16, 64, 64, 0) == (40, 1)
     assert _lib.plan(1, 8, 8, 128, 16, 64, 64, 0, split_pages=2) == (20, 2)
     # A window bounds the visible pages whatever the table width.
     assert _lib.plan(32, 8, 4, 256, 16, 2048, 32768, 1024, split_pages=16)[0] == 32 * 4 * 65 // 16
