@@ -264,6 +264,28 @@ int pda_pack_decode_step(const int32_t* seq_tables, int32_t seq_stride,
                          int32_t page_size, int32_t* tables, int32_t* lengths,
                          int32_t* rows, void* stream);
 
+/* Paged prefill attention for a chunk of one sequence's prompt. Replaces
+ * PrefillBatch.attend's attention (batches.py:84-132; CUDA analogue
+ * cuda/kernels.cu:260-304) after the chunk's keys and values were written
+ * (pda_rope_append with n = count):
+ *   queries, out  [count, q_heads, head_dim] fp16, the chunk's tokens at
+ *                 positions start .. start + count - 1 (queries rotated)
+ *   keys, values  one layer's fp16 arena (layout as for the decode call)
+ *   table         [table_len] int32, the sequence's physical pages
+ * Query p attends keys [first(p), p]: first(p) = max(0, p - window + 1) with
+ * a window, else 0; keys on a page id that is negative, not below
+ * arena_rows / page_size or past table_len are masked (the reference raises
+ * on released pages in range). The score is scale * q.k, softcapped when
+ * softcap > 0. head_dim in {64, 128, 256}; no workspace; one launch on
+ * `stream`. */
+int pda_paged_prefill_attention(const void* queries, const void* keys,
+                                const void* values, const int32_t* table,
+                                int32_t table_len, int32_t start, int32_t count,
+                                void* out, int32_t q_heads, int32_t kv_heads,
+                                int32_t head_dim, int32_t page_size,
+                                int64_t arena_rows, int32_t layout, float scale,
+                                int32_t window, float softcap, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -22,7 +22,7 @@ from typing import Any
 import numpy as np
 import torch
 
-from .hip_kernels import paged_decode_attention, rope, rope_append
+from .hip_kernels import paged_decode_attention, paged_prefill_attention, rope, rope_append
 from .paged_kv import KVCache
 
 
@@ -115,4 +115,55 @@ class DecodeBatch:
             softcap=softcap,
             scales=self.cache.scales(layer),
         )
+        return out.reshape(self.count, -1)
+
+
+class PrefillBatch:
+    """A chunk of one sequence's prompt (batches.py:26-132 without image
+    tokens): positions ``start .. start + count - 1``, the chunk's K/V written
+    to the cache first, then causal attention over the sequence's pages on
+    the GPU (``pda_paged_prefill_attention``), ``[count, q_heads * head_dim]``
+    out."""
+
+    prefill = True
+
+    def __init__(self, cache: KVCache, tokens: torch.Tensor, *, start: int,
+                 tables: dict[str, np.ndarray]) -> None:
+        device = cache.device
+        self.cache = cache
+        self.tokens = tokens
+        self.count = int(tokens.shape[0])
+        self.start = int(start)
+        end = self.start + self.count
+        self.offsets = torch.arange(self.start, end, dtype=torch.int32, device=device)
+        self._write: dict[str, torch.Tensor] = {}
+        self._tables: dict[str, torch.Tensor] = {}
+        for name in cache.groups:
+            table = np.asarray(tables[name])
+            self._write[name] = torch.as_tensor(cache.rows(table, self.start, end),
+                                                device=device)
+            self._tables[name] = torch.as_tensor(table.astype(np.int32), device=device)
+
+    @property
+    def positions(self) -> torch.Tensor:
+        return self.offsets
+
+    def rope(self, x: torch.Tensor, dims: int, *, base: float | None = None,
+             freqs: Any = None) -> torch.Tensor:
+        """Rotate ``[tokens, heads, head_dim]`` at the chunk's positions
+        (batches.py:70-81)."""
+        return rope(x.to(torch.float16).contiguous(), self.offsets, dims, base=base,
+                    freqs=freqs)
+
+    def attend(self, layer: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
+               scale: float, softcap: float = 0.0) -> torch.Tensor:
+        """Write the chunk's K/V, then its attention (batches.py:84-132)."""
+        group = self.cache.layer_group[layer]
+        if self.cache.bits != 16:
+            raise NotImplementedError("prefill over 8-bit K/V has no MI355X kernel yet")
+        self.cache.write(layer, self._write[group.name], k, v)
+        out = paged_prefill_attention(
+            q.to(torch.float16).contiguous(), self.cache.keys[layer], self.cache.values[layer],
+            self._tables[group.name], start=self.start, page_size=self.cache.page_size,
+            scale=scale, window=group.window, softcap=softcap)
         return out.reshape(self.count, -1)

@@ -360,3 +360,42 @@ def pack_decode_step(seq_tables: torch.Tensor, slots: torch.Tensor, positions: t
         tables.data_ptr(), lengths.data_ptr(), rows.data_ptr(), ctypes.c_void_p(stream))
     _lib.check(rc)
     return tables, lengths, rows
+
+
+def paged_prefill_attention(queries: torch.Tensor, keys: torch.Tensor, values: torch.Tensor,
+                            table: torch.Tensor, *, start: int, page_size: int, scale: float,
+                            window: int = 0, softcap: float = 0.0,
+                            out: torch.Tensor | None = None) -> torch.Tensor:
+    """Attention of one prompt chunk (``PrefillBatch.attend``,
+    batches.py:84-132): ``queries`` ``[count, q_heads, D]`` at positions
+    ``start ..`` over the sequence's keys in the arena (either layout, the
+    chunk's own keys already written), ``table`` the sequence's int32 pages.
+    Causal, with the window and softcap of the decode call."""
+    _check_f16("queries", queries, 3)
+    count, q_heads, head_dim = (int(x) for x in queries.shape)
+    layout, arena_rows, kv_heads, a_dim = _arena_geometry(keys, page_size)
+    for name, t in (("keys", keys), ("values", values)):
+        _check_f16(name, t, keys.dim())
+    if tuple(values.shape) != tuple(keys.shape) or a_dim != head_dim:
+        raise ValueError("keys and values must match the queries' head_dim")
+    if q_heads % kv_heads:
+        raise ValueError("query heads must be a multiple of kv heads")
+    if table.dtype != torch.int32 or table.dim() != 1 or not table.is_cuda:
+        raise ValueError("table must be an int32 GPU vector")
+    table = table.contiguous()
+    if out is None:
+        out = torch.empty_like(queries)
+    else:
+        _check_f16("out", out, 3)
+        if tuple(out.shape) != tuple(queries.shape):
+            raise ValueError("out must have the queries' shape")
+    if count == 0:
+        return out
+    stream = torch.cuda.current_stream(queries.device).cuda_stream
+    rc = _lib.library().pda_paged_prefill_attention(
+        queries.data_ptr(), keys.data_ptr(), values.data_ptr(), table.data_ptr(),
+        int(table.shape[0]), int(start), count, out.data_ptr(), q_heads, kv_heads, head_dim,
+        int(page_size), arena_rows, layout, float(scale), int(window), float(softcap),
+        ctypes.c_void_p(stream))
+    _lib.check(rc)
+    return out

@@ -24,6 +24,9 @@ Functions and the reference lines they follow:
   unnormalised partials (acc, running max, sum), then the log-sum-exp merge
   that skips splits whose max is -inf. ``splits`` defaults to the reference
   rule ``clamp(ceil(span / 512), 1, 128)`` (metal_kernels.py:126-127,193-194).
+* :func:`paged_prefill_dense` — ``PrefillBatch.attend`` (batches.py:84-132):
+  one prompt chunk's causal (and windowed) attention over the keys gathered
+  from its page table, in float64.
 * :func:`cuda_closed_form_case` — the known answer of
   tests/cuda_tests.cu:207-262 (decode over 3 keys in 2 out-of-order pages).
 
@@ -115,6 +118,38 @@ def paged_decode_dense(q, keys, values, tables, lengths, *, page_size: int, scal
                             mask=valid[0][None, None, None, :], softcap=softcap)
         out[b] = o[0, :, 0, :]
     return out
+
+
+def paged_prefill_dense(q, keys, values, table, *, start: int, page_size: int, scale: float,
+                        window: int = 0, softcap: float = 0.0):
+    """Prefill attention of one chunk (``PrefillBatch.attend``,
+    python/instinct/batches.py:84-132, no images) in float64: queries
+    ``[count, HQ, D]`` at positions ``start ..``, keys/values the arena
+    ``[rows, HKV, D]``, ``table`` the sequence's pages. Query p sees keys
+    ``[first, p]``, ``first = max(0, start - window + 1)`` for the chunk and
+    the causal mask aligned to the newest key, plus ``key > p - window``
+    with a window; pages with a negative id are masked. Returns
+    ``[count, HQ, D]`` float64."""
+    q = np.asarray(q)
+    count, hq, dim = q.shape
+    end = start + count
+    first = max(0, start - window + 1) if window else 0
+    positions = np.arange(first, end)
+    table = np.asarray(table)
+    pages = table[positions // page_size]
+    usable = pages >= 0
+    rows = np.where(usable, pages.astype(np.int64) * page_size + positions % page_size, 0)
+    k = np.where(usable[:, None, None], np.asarray(keys)[rows].astype(np.float64), 0.0)
+    v = np.where(usable[:, None, None], np.asarray(values)[rows].astype(np.float64), 0.0)
+    qpos = np.arange(start, end)[:, None]
+    kpos = positions[None, :]
+    mask = (kpos <= qpos) & usable[None, :]
+    if window:
+        mask &= kpos > qpos - window
+    out = attention_plain(q.transpose(1, 0, 2)[None], k.transpose(1, 0, 2)[None],
+                          v.transpose(1, 0, 2)[None], scale=scale, mask=mask[None, None],
+                          softcap=softcap)
+    return out[0].transpose(1, 0, 2)
 
 
 def reference_splits(longest: int, window: int = 0) -> int:

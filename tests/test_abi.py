@@ -163,3 +163,44 @@ def test_append_alignment_and_empty_calls():
     # Rows layout needs no page size; rope_dims 0 needs no positions or table.
     assert append(n=0, layout=_lib.PDA_LAYOUT_ROWS, page_size=0) == _lib.PDA_OK
     assert append(n=0, rope_dims=0, positions=None, inv_freq=None) == _lib.PDA_OK
+
+
+def prefill(**overrides):
+    args = dict(q=FAKE, k=FAKE, v=FAKE, table=FAKE, table_len=64, start=0, count=256,
+                out=FAKE, q_heads=28, kv_heads=4, head_dim=128, page_size=16, arena_rows=4096,
+                layout=_lib.PDA_LAYOUT_PAGES, scale=0.088, window=0, softcap=0.0, stream=None)
+    args.update(overrides)
+    return _lib.library().pda_paged_prefill_attention(*args.values())
+
+
+@pytest.mark.parametrize("overrides,code", [
+    (dict(count=-1), _lib.PDA_ERR_INVALID_ARGUMENT),
+    (dict(start=-1), _lib.PDA_ERR_INVALID_ARGUMENT),
+    (dict(q_heads=0), _lib.PDA_ERR_INVALID_ARGUMENT),
+    (dict(kv_heads=0), _lib.PDA_ERR_INVALID_ARGUMENT),
+    (dict(page_size=0), _lib.PDA_ERR_INVALID_ARGUMENT),
+    (dict(table_len=-1), _lib.PDA_ERR_INVALID_ARGUMENT),
+    (dict(window=-1), _lib.PDA_ERR_INVALID_ARGUMENT),
+    (dict(q_heads=30), _lib.PDA_ERR_HEAD_RATIO),
+    (dict(head_dim=96), _lib.PDA_ERR_HEAD_DIM),
+    (dict(start=(1 << 31) - 100), _lib.PDA_ERR_TOO_LONG),
+    (dict(out=None), _lib.PDA_ERR_INVALID_ARGUMENT),
+    (dict(table=None), _lib.PDA_ERR_INVALID_ARGUMENT),
+    (dict(layout=2), _lib.PDA_ERR_INVALID_ARGUMENT),
+    (dict(arena_rows=8), _lib.PDA_ERR_INVALID_ARGUMENT),
+    (dict(scale=float("nan")), _lib.PDA_ERR_INVALID_ARGUMENT),
+    (dict(scale=float("inf")), _lib.PDA_ERR_INVALID_ARGUMENT),
+    (dict(softcap=-1.0), _lib.PDA_ERR_INVALID_ARGUMENT),
+    (dict(q=FAKE + 8), _lib.PDA_ERR_ALIGNMENT),
+    (dict(v=FAKE + 2), _lib.PDA_ERR_ALIGNMENT),
+    (dict(table=FAKE + 2), _lib.PDA_ERR_ALIGNMENT),
+    (dict(q_heads=1 << 16, kv_heads=1), _lib.PDA_ERR_INVALID_ARGUMENT),
+])
+def test_prefill_validation_rejects_bad_arguments(overrides, code):
+    assert prefill(**overrides) == code
+    assert _lib.library().pda_last_error()
+
+
+def test_prefill_empty_chunk_is_a_no_op():
+    assert prefill(count=0) == _lib.PDA_OK
+    assert prefill(count=0, q=None, k=None, v=None, table=None, out=None) == _lib.PDA_OK
