@@ -16,7 +16,8 @@ the oracle's threaded C++ restatement of the reference's split-K algorithm,
 timed on a bounded sample of the same workload on this host's cores.
 Also reported: the step before the call, RoPE of the new queries and keys
 plus the K/V append into the arena (one launch, "append"), and one layer's
-decode attention step (append then call, "layer_step_us"), both flushed.
+decode attention step (append then call, "layer_step_us"), both flushed, and
+the prefill attention of one prompt chunk ("prefill", matrix-core bound).
 
 Prints ONE JSON line. Only --gpus 1 is supported (a one-GPU build).
 """
@@ -37,6 +38,7 @@ for _p in (ROOT, ROOT / "llm-inference_amd"):
         sys.path.insert(0, str(_p))
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 matrix cores, published
 METRIC = "decode-attention effective K/V GB/s (% of HBM peak) + µs/layer-step"
 TRAFFIC_FILE = ROOT / "profiles" / "traffic_config2.json"
 SPIN_CYCLES = 2_000_000  # torch.cuda._sleep before each timed call
@@ -56,6 +58,9 @@ def parse():
                          "per layer, eager and as one captured HIP graph")
     ap.add_argument("--kv-bits", type=int, choices=[16, 8], default=16,
                     help="K/V storage: fp16, or int8 with a scale per (row, kv head)")
+    ap.add_argument("--prefill-tokens", type=int, default=4096,
+                    help="prompt chunk of the prefill timing (0 = skip): one sequence at the "
+                         "workload's heads, start 0, causal")
     ap.add_argument("--no-flush", action="store_true", help="skip the flushed pass")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="approximate CPU time budget of the CPU-baseline sample")
@@ -161,6 +166,52 @@ def decode_step(w, scales, layers, steps):
     return {"layers": layers, "launches_per_step": 1 + 3 * layers,
             "eager_us": round(eager, 1), "graph_us": round(graph, 1),
             "graph_us_per_layer": round(graph / layers, 2)}
+
+
+def prefill_leg(w, tokens, steps, start=0):
+    """One prompt chunk of `tokens` tokens at positions start.. of one
+    sequence, at the workload's heads and page size, through
+    pda_paged_prefill_attention (PrefillBatch.attend's attention,
+    batches.py:84-132). Algorithmic work: query p sees n_p = p + 1 keys (or
+    the window), 4 D n_p flops per query head (QK^T and PV, a multiply-add =
+    2 flops); roofline = fp16 dense matrix-core peak."""
+    import numpy as np
+    import torch
+
+    from instinct_amd.hip_kernels import paged_prefill_attention
+    from instinct_amd.paged_kv import rows_to_pages
+
+    dev = w.q.device
+    P, hq, hkv, d = w.page_size, w.q_heads, w.kv_heads, w.head_dim
+    pages = (start + tokens + P - 1) // P
+    gen = torch.Generator(device=dev).manual_seed(11)
+    keys = torch.randn((pages * P, hkv, d), generator=gen, device=dev).half()
+    values = torch.randn((pages * P, hkv, d), generator=gen, device=dev).half()
+    if w.layout == "pages":
+        keys, values = rows_to_pages(keys, P), rows_to_pages(values, P)
+    table = torch.as_tensor(np.random.default_rng(11).permutation(pages).astype(np.int32),
+                            device=dev)
+    q = torch.randn((tokens, hq, d), generator=gen, device=dev).half()
+    out = torch.empty_like(q)
+
+    def call():
+        paged_prefill_attention(q, keys, values, table, start=start, page_size=P,
+                                scale=w.scale, window=w.window, softcap=w.softcap, out=out)
+
+    for _ in range(3):
+        call()
+    (ms,), _ = time_calls([call], max(5, min(steps, 20)))
+    pos = np.arange(start, start + tokens, dtype=np.float64)
+    seen = pos + 1 if w.window <= 0 else np.minimum(pos + 1, w.window)
+    flops = 4.0 * d * hq * seen.sum()
+    med = statistics.median(ms)
+    tflops = flops / (med * 1e-3) / 1e12
+    return {"kernel": f"paged_prefill_kernel<{d}> (pda_paged_prefill_attention)",
+            "tokens": tokens, "start": start, "q_heads": hq, "kv_heads": hkv, "head_dim": d,
+            "us_median": round(med * 1e3, 2), "flops": flops,
+            "TFLOP_per_s": round(tflops, 2), "peak_TFLOP_per_s": MFMA_F16_PEAK_TFLOPS,
+            "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
+            "tokens_per_s": round(tokens / (med * 1e-3), 1)}
 
 
 def cpu_baseline(w, budget_s):
@@ -377,6 +428,8 @@ def main():
     line["layer_step_us"] = round(statistics.median(step_ms) * 1e3, 2)
     if args.step_layers > 0:
         line["decode_step"] = decode_step(w, scales, args.step_layers, args.steps)
+    if args.prefill_tokens > 0 and args.kv_bits == 16:
+        line["prefill"] = prefill_leg(w, args.prefill_tokens, args.steps)
     print(json.dumps(line), flush=True)
 
 

@@ -12,20 +12,31 @@
 //
 // MI355X design (a flash-attention tile loop on the matrix cores):
 //  * Workgroup = 4 waves = one query head and 128 queries (32 per wave).
-//    Keys are streamed in tiles of 32 through LDS (K and V rows gathered
-//    from the pages of the sequence's table, either arena layout).
+//    Keys are streamed in tiles of 32 through LDS, K and V rows gathered from
+//    the pages of the sequence's table (either arena layout). The LDS holds
+//    two tiles: the loads of tile t + 1 are issued into registers before the
+//    math of tile t and stored to the other half after it, one barrier per
+//    tile.
 //  * Each wave computes S^T = K Q^T for its 32 queries with
-//    v_mfma_f32_32x32x8_f16 (D / 8 instructions per key tile). In that
-//    product's accumulator layout a lane holds 16 keys of one query, which is
-//    exactly the B operand layout of the next product, so the probabilities
-//    P^T feed O^T += V^T P^T (D / 32 x 4 instructions) straight from
-//    registers; only V^T is read from LDS.
+//    v_mfma_f32_32x32x16_f16 (D / 16 instructions per key tile), Q held in
+//    registers. In that product's accumulator a lane holds 16 keys of one
+//    query; 8 of them per 16-key step are the B operand of the next product
+//    O^T += V^T P^T (D / 32 x 2 instructions per tile), so the probabilities
+//    never leave registers. The contraction pairs A and B by k-slot, so the
+//    V^T operand takes the keys in the order the accumulator holds them:
+//    two ds_read_b64_tr_b16 per operand give a lane four consecutive keys of
+//    one dimension each.
 //  * Online softmax per query in the log2 domain with a lazy running max
-//    (rescale only when a score passes the max by 2^8), masks for causality,
-//    the window and unusable pages, fp16 probabilities into the matrix core,
-//    fp32 accumulation, normalised fp16 output.
-//  * LDS rows are padded to 16 bytes past the head so the 32 lanes reading
-//    one column of K hit different banks.
+//    (rescale only when a score passes the max by 2^8), fp16 probabilities
+//    into the matrix core, fp32 accumulation, normalised fp16 output. Masks
+//    (causality, the window, unusable pages) are evaluated only on the tiles
+//    that need them; a wave skips the math of tiles none of its queries see.
+//  * Work order: the query tiles with the most keys start first, and the G
+//    query heads that read one kv head's tile are dispatched back to back to
+//    one XCD (workgroups go round robin over the 8 XCDs), so the L2 of that
+//    XCD serves the tile to all of them.
+//  * LDS rows are padded so that the 16 lanes of a 16-byte K read, and the
+//    four rows of a transposed V read, fall on distinct banks.
 
 #include <hip/hip_runtime.h>
 
@@ -38,9 +49,12 @@
 namespace {
 
 typedef _Float16 f16;
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 constexpr float kLog2e = 1.44269504088896340736f;
 constexpr float kSlack = 8.0f;
@@ -48,6 +62,7 @@ constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kQueries = 32 * kWaves;  // queries per workgroup
 constexpr int kKeys = 32;              // keys per tile
+constexpr int kXcds = 8;
 
 struct PrefillParams {
   const f16* q;        // [count, hq, D]
@@ -62,6 +77,7 @@ struct PrefillParams {
   int32_t table_len;
   int32_t start;
   int32_t count;
+  int32_t tiles;       // query tiles = ceil(count / kQueries)
   int32_t hq;
   int32_t hkv;
   int32_t page_size;
@@ -72,36 +88,62 @@ struct PrefillParams {
   float cap_out;  // softcap log2(e)
 };
 
+__device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+__device__ __forceinline__ f16x4 read_tr(const f16* p) {
+  return __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p));
+}
+
 template <int D>
 __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillParams p) {
-  constexpr int kRow = D + 8;  // LDS row (halves), 16-byte aligned
-  constexpr int kChunks = D / 8;  // 16-byte pieces of a row
-  __shared__ __align__(16) f16 s_k[kKeys * kRow];
-  __shared__ __align__(16) f16 s_v[kKeys * kRow];
-  __shared__ int s_ok[kKeys];
+  constexpr int kKRow = D + 8;    // K row in LDS (halves): 16-lane 16-byte reads hit distinct banks
+  constexpr int kVRow = D + 32;   // V row: the 4 rows of a transposed read hit distinct banks
+  constexpr int kPieces = kKeys * D / 8 / kThreads;  // 16-byte pieces per thread and tile
+  static_assert(kPieces >= 1 && kPieces * kThreads * 8 == kKeys * D, "tile shape");
+  __shared__ __align__(16) f16 s_k[2][kKeys * kKRow];
+  __shared__ __align__(16) f16 s_v[2][kKeys * kVRow];
+  __shared__ __align__(4) uint8_t s_ok[2][kWaves];  // usable-key bits, 8 keys per wave
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int w = tid >> 6;
+  const int w = uniform(tid >> 6);
   const int n = lane & 31;   // query column of this lane
   const int hh = lane >> 5;  // which half of the key rows this lane holds
-  const int h = blockIdx.y;
-  const int kvh = h / (p.hq / p.hkv);
-  // The last query tiles read the most keys (causal): they start first.
-  const int q0 = (gridDim.x - 1 - blockIdx.x) * kQueries;
+
+  // Work item. Logical order: query tiles from the last (most keys) to the
+  // first, then kv head, then the G query heads of that kv head. Workgroup
+  // ids go round robin over the XCDs; whole runs of G go to one XCD.
+  const int G = p.hq / p.hkv;
+  int item = blockIdx.x;
+  const int runs = p.tiles * p.hkv;
+  const int full = runs / kXcds * kXcds;
+  if (item < full * G) {
+    const int x = item % kXcds, j = item / kXcds;
+    item = ((j / G) * kXcds + x) * G + j % G;
+  }
+  const int run = item / G;
+  const int h = (run % p.hkv) * G + (item - run * G);
+  const int kvh = run % p.hkv;
+  const int tile = p.tiles - 1 - run / p.hkv;
+
+  const int q0 = tile * kQueries;
   const int q1 = min(q0 + kQueries, p.count);
   const int qi = q0 + 32 * w + n;  // this lane's query (may be past count)
   const bool q_live = qi < p.count;
   const int qpos = p.start + qi;
+  const int wq0 = q0 + 32 * w;
+  const bool wave_live = wq0 < p.count;
+  const int wfirst = p.start + wq0;
+  const int wlast = p.start + min(wq0 + 31, p.count - 1);
 
-  // Query fragments (B operand of S^T = K Q^T): elements 8c + 4hh .. + 3.
-  f16x4 qf[kChunks];
+  // Query fragments (B operand of S^T = K Q^T): dims 16 c + 8 hh .. + 7.
+  f16x8 qf[D / 16];
   {
-    const f16* qp = p.q + ((int64_t)(q_live ? qi : 0) * p.hq + h) * D + 4 * hh;
+    const f16* qp = p.q + ((int64_t)(q_live ? qi : 0) * p.hq + h) * D + 8 * hh;
 #pragma unroll
-    for (int c = 0; c < kChunks; ++c) {
-      f16x4 x = *reinterpret_cast<const f16x4*>(qp + 8 * c);
-      qf[c] = q_live ? x : f16x4{};
+    for (int c = 0; c < D / 16; ++c) {
+      const f16x8 x = *reinterpret_cast<const f16x8*>(qp + 16 * c);
+      qf[c] = q_live ? x : f16x8{};
     }
   }
 
@@ -111,98 +153,154 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
   float m = -INFINITY, l = 0.0f;
 
   // Keys this workgroup needs: from the first visible key of its first query
-  // to its last query.
+  // (rounded down to a tile) to its last query.
   const int last = p.start + q1 - 1;
-  int kmin = 0;
-  if (p.window > 0) kmin = max(0, p.start + q0 - p.window + 1);
+  const int kbase = p.window > 0 ? (max(0, p.start + q0 - p.window + 1) & ~(kKeys - 1)) : 0;
+  const int ntile = (last - kbase) / kKeys + 1;
 
-  for (int k0 = kmin; k0 <= last; k0 += kKeys) {
-    // Gather the tile's K and V rows into LDS (zeros for unusable keys).
-    for (int c = tid; c < kKeys * kChunks; c += kThreads) {
-      const int key = c / kChunks, part = c - key * kChunks;
-      const int kp = k0 + key;
-      bool ok = kp <= last;
-      int64_t at = 0;
-      if (ok) {
-        const int pi = kp / p.page_size;
-        const int page = pi < p.table_len ? p.table[pi] : -1;
-        ok = page >= 0 && page < p.arena_pages;
-        at = (int64_t)(ok ? page : 0) * p.page_elems + (int64_t)kvh * p.head_elems +
-             (int64_t)(kp - pi * p.page_size) * p.row_elems + part * 8;
-      }
-      f16x8 kx = f16x8{}, vx = f16x8{};
-      if (ok) {
-        kx = *reinterpret_cast<const f16x8*>(p.k + at);
-        vx = *reinterpret_cast<const f16x8*>(p.v + at);
-      }
-      *reinterpret_cast<f16x8*>(s_k + key * kRow + part * 8) = kx;
-      *reinterpret_cast<f16x8*>(s_v + key * kRow + part * 8) = vx;
-      if (part == 0) s_ok[key] = ok;
+  // Gather: thread tid moves key tid / 8 of a tile, pieces tid % 8 + 8 i.
+  const int gk = tid >> 3;
+  const int gp = tid & 7;
+  f16x8 kr[kPieces], vr[kPieces];
+  bool gok = false;
+  auto fetch = [&](int k0) {
+    const int kp = k0 + gk;
+    int page = -1, r = 0;
+    if (kp <= last) {
+      const int pi = kp / p.page_size;
+      r = kp - pi * p.page_size;
+      page = pi < p.table_len ? p.table[pi] : -1;
+      if (page >= p.arena_pages) page = -1;
     }
-    __syncthreads();
+    gok = page >= 0;
+    const int64_t at = (int64_t)(gok ? page : 0) * p.page_elems +
+                       (int64_t)kvh * p.head_elems + (int64_t)r * p.row_elems + gp * 8;
+#pragma unroll
+    for (int i = 0; i < kPieces; ++i) {
+      kr[i] = *reinterpret_cast<const f16x8*>(p.k + at + 64 * i);
+      vr[i] = *reinterpret_cast<const f16x8*>(p.v + at + 64 * i);
+    }
+  };
+  auto stash = [&](int buf) {
+    // Unusable keys are stored as zeros (their weight is 0; zero V keeps
+    // 0 * V finite whatever the arena holds there).
+    f16* kd = s_k[buf] + gk * kKRow + gp * 8;
+    f16* vd = s_v[buf] + gk * kVRow + gp * 8;
+#pragma unroll
+    for (int i = 0; i < kPieces; ++i) {
+      *reinterpret_cast<f16x8*>(kd + 64 * i) = gok ? kr[i] : f16x8{};
+      *reinterpret_cast<f16x8*>(vd + 64 * i) = gok ? vr[i] : f16x8{};
+    }
+    const uint64_t bits = __ballot(gok);
+    if (lane == 0) {
+      uint32_t m8 = 0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) m8 |= (uint32_t)((bits >> (8 * j)) & 1) << j;
+      s_ok[buf][w] = (uint8_t)m8;
+    }
+  };
 
-    // S^T (32 keys x 32 queries): lane holds keys 8 (v / 4) + 4 hh + v % 4.
-    f32x16 s = f32x16{};
+  // Lane part of the transposed V read: group g = lane / 16 reads dims
+  // 16 (g % 2) + 4 (s % 4) of key 4 (g / 2) + s / 4, s = lane % 16.
+  const int g16 = lane >> 4, s16 = lane & 15;
+  const int v_lane = (4 * (g16 >> 1) + (s16 >> 2)) * kVRow + 16 * (g16 & 1) + 4 * (s16 & 3);
+  const int k_lane = n * kKRow + 8 * hh;
+  const int qlo = p.window > 0 ? qpos - p.window : INT32_MIN;  // keys > qlo are in the window
+
+  fetch(kbase);
+  stash(0);
+  __syncthreads();
+  for (int t = 0; t < ntile; ++t) {
+    const int buf = t & 1;
+    const int k0 = kbase + t * kKeys;
+    const bool more = t + 1 < ntile;
+    if (more) fetch(k0 + kKeys);
+
+    const bool work =
+        wave_live && k0 <= wlast && (p.window <= 0 || k0 + kKeys - 1 > wfirst - p.window);
+    if (work) {
+      const f16* sk = s_k[buf];
+      const f16* sv = s_v[buf];
+      // S^T (32 keys x 32 queries): lane holds keys 8 (v / 4) + 4 hh + v % 4.
+      f32x16 s = f32x16{};
 #pragma unroll
-    for (int c = 0; c < kChunks; ++c) {
-      const f16x4 a = *reinterpret_cast<const f16x4*>(s_k + n * kRow + 8 * c + 4 * hh);
-      s = __builtin_amdgcn_mfma_f32_32x32x8f16(a, qf[c], s, 0, 0, 0);
-    }
-    // Scores in log2 units, masked.
-    float x[16];
-    float top = -INFINITY;
-#pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int key = 8 * (v / 4) + 4 * hh + (v % 4);
-      const int kp = k0 + key;
-      float t;
+      for (int c = 0; c < D / 16; ++c) {
+        const f16x8 a = *reinterpret_cast<const f16x8*>(sk + k_lane + 16 * c);
+        s = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[c], s, 0, 0, 0);
+      }
+      const uint32_t okm = *reinterpret_cast<const uint32_t*>(s_ok[buf]);
+      const bool edge = k0 + kKeys - 1 > wfirst || okm != 0xffffffffu ||
+                        (p.window > 0 && k0 <= wlast - p.window);
+      float x[16];
       if (p.softcap > 0.0f) {
-        const float e = __builtin_amdgcn_exp2f(s[v] * p.cap_in);
-        t = (1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f)) * p.cap_out;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const float e = __builtin_amdgcn_exp2f(s[v] * p.cap_in);
+          x[v] = (1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f)) * p.cap_out;
+        }
       } else {
-        t = s[v] * p.scale_log2;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) x[v] = s[v] * p.scale_log2;
       }
-      const bool vis = q_live && s_ok[key] && kp <= qpos &&
-                       (p.window <= 0 || kp > qpos - p.window);
-      x[v] = vis ? t : -INFINITY;
-      top = fmaxf(top, x[v]);
-    }
-    top = fmaxf(top, __shfl_xor(top, 32));  // the other half of this query's keys
-    // Lazy running max: rescale only when a score passes it by 2^8.
-    if (top > m + kSlack) {
-      const float f = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - top);
-      m = top;
-      l *= f;
+      if (edge) {
+        // Key k0 + key is visible to this lane's query when usable,
+        // <= qpos and > qlo.
+        const uint32_t okl = okm >> (4 * hh);
+        const int hi = qpos - k0 - 4 * hh;  // largest visible key offset
+        const int lo = qlo == INT32_MIN ? INT32_MIN : qlo - k0 - 4 * hh;
 #pragma unroll
-      for (int b = 0; b < D / 32; ++b)
+        for (int v = 0; v < 16; ++v) {
+          const int key = 8 * (v / 4) + (v % 4);  // minus 4 hh
+          const bool vis = ((okl >> key) & 1u) && key <= hi && key > lo;
+          x[v] = vis ? x[v] : -INFINITY;
+        }
+      }
+      float top = x[0];
 #pragma unroll
-        for (int v = 0; v < 16; ++v) o[b][v] *= f;
-    }
-    // Probabilities as the B operand of O^T += V^T P^T (keys 8j + 4hh + t).
-    f16x4 pf[4];
+      for (int v = 1; v < 16; ++v) top = fmaxf(top, x[v]);
+      top = fmaxf(top, __shfl_xor(top, 32));  // the other half of this query's keys
+      // Lazy running max: rescale only when a score passes it by 2^8.
+      if (top > m + kSlack) {
+        const float f = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - top);
+        m = top;
+        l *= f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+        for (int b = 0; b < D / 32; ++b)
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        // Masked keys weigh 0 (also while this query's max is still -inf).
-        const float xv = x[4 * j + t];
-        const float pr = xv == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(xv - m);
-        const f16 ph = (f16)pr;
-        l += (float)ph;
-        pf[j][t] = ph;
+          for (int v = 0; v < 16; ++v) o[b][v] *= f;
+      }
+      // While every key so far is masked, m is -inf and so is every x.
+      const float mu = m == -INFINITY ? 0.0f : m;
+      // P^T as the B operand: step ks holds values 8 ks .. 8 ks + 7, i.e.
+      // keys 16 ks + 8 (t / 4) + 4 hh + t % 4.
+      f16x8 pb[2];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+        for (int t2 = 0; t2 < 4; ++t2) {
+          const f16x2 ph = {(f16)__builtin_amdgcn_exp2f(x[8 * ks + 2 * t2] - mu),
+                            (f16)__builtin_amdgcn_exp2f(x[8 * ks + 2 * t2 + 1] - mu)};
+          l = __builtin_amdgcn_fdot2(ph, f16x2{(f16)1.0f, (f16)1.0f}, l, false);
+          pb[ks][2 * t2] = ph[0];
+          pb[ks][2 * t2 + 1] = ph[1];
+        }
+      }
+      // O^T += V^T P^T. A operand of step ks for rows 32 b ..: keys
+      // 16 ks + 4 hh + 0..3 (first read) and + 8 (second read).
+#pragma unroll
+      for (int b = 0; b < D / 32; ++b) {
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          const f16* vp = sv + v_lane + 16 * ks * kVRow + 32 * b;
+          const f16x4 lo4 = read_tr(vp);
+          const f16x4 hi4 = read_tr(vp + 8 * kVRow);
+          const f16x8 a = {lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+          o[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[ks], o[b], 0, 0, 0);
+        }
       }
     }
-#pragma unroll
-    for (int b = 0; b < D / 32; ++b) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        f16x4 a;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) a[t] = s_v[(8 * j + 4 * hh + t) * kRow + 32 * b + n];
-        o[b] = __builtin_amdgcn_mfma_f32_32x32x8f16(a, pf[j], o[b], 0, 0, 0);
-      }
-    }
-    __syncthreads();  // the next tile overwrites LDS
+    if (more) stash(buf ^ 1);
+    __syncthreads();  // the next tile is in LDS; this one may be overwritten
   }
 
   if (!q_live) return;
@@ -262,8 +360,8 @@ int pda_paged_prefill_attention(const void* queries, const void* keys, const voi
   if (mis & 15)
     return fail(PDA_ERR_ALIGNMENT, "fp16 buffers must be 16-byte aligned");
   if ((uintptr_t)table & 3) return fail(PDA_ERR_ALIGNMENT, "the table must be 4-byte aligned");
-  if ((int64_t)q_heads > 65535)
-    return fail(PDA_ERR_INVALID_ARGUMENT, "more than 65535 query heads");
+  if ((int64_t)((count + kQueries - 1) / kQueries) * q_heads > INT32_MAX)
+    return fail(PDA_ERR_INVALID_ARGUMENT, "query tiles x query heads exceeds 2^31");
 
   PrefillParams prm;
   prm.q = static_cast<const f16*>(queries);
@@ -283,6 +381,7 @@ int pda_paged_prefill_attention(const void* queries, const void* keys, const voi
   prm.table_len = table_len;
   prm.start = start;
   prm.count = count;
+  prm.tiles = (count + kQueries - 1) / kQueries;
   prm.hq = q_heads;
   prm.hkv = kv_heads;
   prm.page_size = page_size;
@@ -295,7 +394,7 @@ int pda_paged_prefill_attention(const void* queries, const void* keys, const voi
   const void* fn = head_dim == 64    ? reinterpret_cast<const void*>(paged_prefill_kernel<64>)
                    : head_dim == 128 ? reinterpret_cast<const void*>(paged_prefill_kernel<128>)
                                      : reinterpret_cast<const void*>(paged_prefill_kernel<256>);
-  const dim3 grid((count + kQueries - 1) / kQueries, q_heads);
+  const dim3 grid((unsigned)((int64_t)prm.tiles * q_heads));
   const hipError_t err =
       hipLaunchKernel(fn, grid, dim3(kThreads), args, 0, static_cast<hipStream_t>(stream));
   if (err != hipSuccess)

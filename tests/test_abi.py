@@ -194,7 +194,7 @@ def prefill(**overrides):
     (dict(q=FAKE + 8), _lib.PDA_ERR_ALIGNMENT),
     (dict(v=FAKE + 2), _lib.PDA_ERR_ALIGNMENT),
     (dict(table=FAKE + 2), _lib.PDA_ERR_ALIGNMENT),
-    (dict(q_heads=1 << 16, kv_heads=1), _lib.PDA_ERR_INVALID_ARGUMENT),
+    (dict(count=1 << 30, q_heads=256, kv_heads=1), _lib.PDA_ERR_INVALID_ARGUMENT),
 ])
 def test_prefill_validation_rejects_bad_arguments(overrides, code):
     assert prefill(**overrides) == code
