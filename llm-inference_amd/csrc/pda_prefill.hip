@@ -43,6 +43,8 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "pda.h"
 #include "pda_internal.h"
 
@@ -61,7 +63,6 @@ constexpr float kSlack = 8.0f;
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kQueries = 32 * kWaves;  // queries per workgroup
-constexpr int kKeys = 32;              // keys per tile
 constexpr int kXcds = 8;
 
 struct PrefillParams {
@@ -94,15 +95,25 @@ __device__ __forceinline__ f16x4 read_tr(const f16* p) {
   return __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p));
 }
 
+// Keys per tile: 64 (two 32-key blocks) where the registers allow it.
+template <int D>
+constexpr int blocks_per_tile() { return D <= 128 ? 2 : 1; }
+
 template <int D>
 __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillParams p) {
+  constexpr int KB = blocks_per_tile<D>();  // 32-key blocks per tile
+  constexpr int kKeys = 32 * KB;            // keys per tile
   constexpr int kKRow = D + 8;    // K row in LDS (halves): 16-lane 16-byte reads hit distinct banks
   constexpr int kVRow = D + 32;   // V row: the 4 rows of a transposed read hit distinct banks
-  constexpr int kPieces = kKeys * D / 8 / kThreads;  // 16-byte pieces per thread and tile
-  static_assert(kPieces >= 1 && kPieces * kThreads * 8 == kKeys * D, "tile shape");
+  constexpr int kTpk = kThreads / kKeys;               // gather threads per key
+  constexpr int kPieces = D / 8 / kTpk;                // 16-byte pieces per thread and tile
+  constexpr int kKeysPerWave = 64 / kTpk;              // keys one wave gathers
+  static_assert(kPieces >= 1 && kPieces * kTpk * 8 == D, "tile shape");
+  typedef typename std::conditional<kKeysPerWave == 16, uint16_t, uint8_t>::type okbits;
+  typedef typename std::conditional<KB == 2, uint64_t, uint32_t>::type okword;
   __shared__ __align__(16) f16 s_k[2][kKeys * kKRow];
   __shared__ __align__(16) f16 s_v[2][kKeys * kVRow];
-  __shared__ __align__(4) uint8_t s_ok[2][kWaves];  // usable-key bits, 8 keys per wave
+  __shared__ __align__(8) okbits s_ok[2][kWaves];  // usable-key bits of the tile
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -155,30 +166,36 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
   // Keys this workgroup needs: from the first visible key of its first query
   // (rounded down to a tile) to its last query.
   const int last = p.start + q1 - 1;
-  const int kbase = p.window > 0 ? (max(0, p.start + q0 - p.window + 1) & ~(kKeys - 1)) : 0;
+  const int kbase = p.window > 0 ? (max(0, p.start + q0 - p.window + 1) / kKeys * kKeys) : 0;
   const int ntile = (last - kbase) / kKeys + 1;
 
-  // Gather: thread tid moves key tid / 8 of a tile, pieces tid % 8 + 8 i.
-  const int gk = tid >> 3;
-  const int gp = tid & 7;
+  // Gather: thread tid moves key tid / kTpk of a tile, 16-byte pieces
+  // tid % kTpk + kTpk i (consecutive lanes read consecutive pieces of a row).
+  // The page of that key is looked up two tiles ahead (lookup), its rows
+  // loaded one tile ahead (fetch), so neither load is waited for in the
+  // iteration that issues it.
+  const int gk = tid / kTpk;
+  const int gp = tid % kTpk;
   f16x8 kr[kPieces], vr[kPieces];
   bool gok = false;
-  auto fetch = [&](int k0) {
+  // The table read is unconditional (index clamped, table_len >= 1) and its
+  // range check a separate flag, so the loaded page id is never merged with
+  // another value, which would wait for the load.
+  auto lookup = [&](int k0, int& page, bool& in, int& r) {
     const int kp = k0 + gk;
-    int page = -1, r = 0;
-    if (kp <= last) {
-      const int pi = kp / p.page_size;
-      r = kp - pi * p.page_size;
-      page = pi < p.table_len ? p.table[pi] : -1;
-      if (page >= p.arena_pages) page = -1;
-    }
-    gok = page >= 0;
+    const int pi = kp / p.page_size;
+    r = kp - pi * p.page_size;
+    in = kp <= last && pi < p.table_len;
+    page = p.table[min(pi, p.table_len - 1)];
+  };
+  auto fetch = [&](int page, bool in, int r) {
+    gok = in && page >= 0 && page < p.arena_pages;
     const int64_t at = (int64_t)(gok ? page : 0) * p.page_elems +
                        (int64_t)kvh * p.head_elems + (int64_t)r * p.row_elems + gp * 8;
 #pragma unroll
     for (int i = 0; i < kPieces; ++i) {
-      kr[i] = *reinterpret_cast<const f16x8*>(p.k + at + 64 * i);
-      vr[i] = *reinterpret_cast<const f16x8*>(p.v + at + 64 * i);
+      kr[i] = *reinterpret_cast<const f16x8*>(p.k + at + 8 * kTpk * i);
+      vr[i] = *reinterpret_cast<const f16x8*>(p.v + at + 8 * kTpk * i);
     }
   };
   auto stash = [&](int buf) {
@@ -188,15 +205,15 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
     f16* vd = s_v[buf] + gk * kVRow + gp * 8;
 #pragma unroll
     for (int i = 0; i < kPieces; ++i) {
-      *reinterpret_cast<f16x8*>(kd + 64 * i) = gok ? kr[i] : f16x8{};
-      *reinterpret_cast<f16x8*>(vd + 64 * i) = gok ? vr[i] : f16x8{};
+      *reinterpret_cast<f16x8*>(kd + 8 * kTpk * i) = gok ? kr[i] : f16x8{};
+      *reinterpret_cast<f16x8*>(vd + 8 * kTpk * i) = gok ? vr[i] : f16x8{};
     }
     const uint64_t bits = __ballot(gok);
     if (lane == 0) {
-      uint32_t m8 = 0;
+      uint32_t mk = 0;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) m8 |= (uint32_t)((bits >> (8 * j)) & 1) << j;
-      s_ok[buf][w] = (uint8_t)m8;
+      for (int j = 0; j < kKeysPerWave; ++j) mk |= (uint32_t)((bits >> (kTpk * j)) & 1) << j;
+      s_ok[buf][w] = (okbits)mk;
     }
   };
 
@@ -207,57 +224,68 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
   const int k_lane = n * kKRow + 8 * hh;
   const int qlo = p.window > 0 ? qpos - p.window : INT32_MIN;  // keys > qlo are in the window
 
-  fetch(kbase);
+  int page0, r0, page1, r1;
+  bool in0, in1;
+  lookup(kbase, page0, in0, r0);
+  lookup(kbase + kKeys, page1, in1, r1);
+  fetch(page0, in0, r0);
   stash(0);
   __syncthreads();
   for (int t = 0; t < ntile; ++t) {
     const int buf = t & 1;
     const int k0 = kbase + t * kKeys;
     const bool more = t + 1 < ntile;
-    if (more) fetch(k0 + kKeys);
+    if (more) fetch(page1, in1, r1);
+    lookup(k0 + 2 * kKeys, page1, in1, r1);
 
     const bool work =
         wave_live && k0 <= wlast && (p.window <= 0 || k0 + kKeys - 1 > wfirst - p.window);
     if (work) {
       const f16* sk = s_k[buf];
       const f16* sv = s_v[buf];
-      // S^T (32 keys x 32 queries): lane holds keys 8 (v / 4) + 4 hh + v % 4.
-      f32x16 s = f32x16{};
+      // S^T per 32-key block kb: lane holds keys 32 kb + 8 (v / 4) + 4 hh + v % 4.
+      f32x16 s[KB];
 #pragma unroll
-      for (int c = 0; c < D / 16; ++c) {
-        const f16x8 a = *reinterpret_cast<const f16x8*>(sk + k_lane + 16 * c);
-        s = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[c], s, 0, 0, 0);
+      for (int kb = 0; kb < KB; ++kb) {
+        f16x8 ka[D / 16];
+#pragma unroll
+        for (int c = 0; c < D / 16; ++c)
+          ka[c] = *reinterpret_cast<const f16x8*>(sk + k_lane + 32 * kb * kKRow + 16 * c);
+        s[kb] = f32x16{};
+#pragma unroll
+        for (int c = 0; c < D / 16; ++c)
+          s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[c], qf[c], s[kb], 0, 0, 0);
       }
-      const uint32_t okm = *reinterpret_cast<const uint32_t*>(s_ok[buf]);
-      const bool edge = k0 + kKeys - 1 > wfirst || okm != 0xffffffffu ||
+      const okword okm = *reinterpret_cast<const okword*>(s_ok[buf]);
+      const bool edge = k0 + kKeys - 1 > wfirst || okm != (okword)~(okword)0 ||
                         (p.window > 0 && k0 <= wlast - p.window);
-      float x[16];
+      float x[16 * KB];
       if (p.softcap > 0.0f) {
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const float e = __builtin_amdgcn_exp2f(s[v] * p.cap_in);
+        for (int v = 0; v < 16 * KB; ++v) {
+          const float e = __builtin_amdgcn_exp2f(s[v / 16][v % 16] * p.cap_in);
           x[v] = (1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f)) * p.cap_out;
         }
       } else {
 #pragma unroll
-        for (int v = 0; v < 16; ++v) x[v] = s[v] * p.scale_log2;
+        for (int v = 0; v < 16 * KB; ++v) x[v] = s[v / 16][v % 16] * p.scale_log2;
       }
       if (edge) {
         // Key k0 + key is visible to this lane's query when usable,
         // <= qpos and > qlo.
-        const uint32_t okl = okm >> (4 * hh);
+        const okword okl = okm >> (4 * hh);
         const int hi = qpos - k0 - 4 * hh;  // largest visible key offset
         const int lo = qlo == INT32_MIN ? INT32_MIN : qlo - k0 - 4 * hh;
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int key = 8 * (v / 4) + (v % 4);  // minus 4 hh
+        for (int v = 0; v < 16 * KB; ++v) {
+          const int key = 32 * (v / 16) + 8 * ((v % 16) / 4) + (v % 4);  // minus 4 hh
           const bool vis = ((okl >> key) & 1u) && key <= hi && key > lo;
           x[v] = vis ? x[v] : -INFINITY;
         }
       }
       float top = x[0];
 #pragma unroll
-      for (int v = 1; v < 16; ++v) top = fmaxf(top, x[v]);
+      for (int v = 1; v < 16 * KB; ++v) top = fmaxf(top, x[v]);
       top = fmaxf(top, __shfl_xor(top, 32));  // the other half of this query's keys
       // Lazy running max: rescale only when a score passes it by 2^8.
       if (top > m + kSlack) {
@@ -271,11 +299,11 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
       }
       // While every key so far is masked, m is -inf and so is every x.
       const float mu = m == -INFINITY ? 0.0f : m;
-      // P^T as the B operand: step ks holds values 8 ks .. 8 ks + 7, i.e.
-      // keys 16 ks + 8 (t / 4) + 4 hh + t % 4.
-      f16x8 pb[2];
+      // P^T as the B operand: 16-key step ks holds values 8 ks .. 8 ks + 7,
+      // i.e. keys 16 ks + 8 (t / 4) + 4 hh + t % 4.
+      f16x8 pb[2 * KB];
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
+      for (int ks = 0; ks < 2 * KB; ++ks) {
 #pragma unroll
         for (int t2 = 0; t2 < 4; ++t2) {
           const f16x2 ph = {(f16)__builtin_amdgcn_exp2f(x[8 * ks + 2 * t2] - mu),
@@ -290,7 +318,7 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
 #pragma unroll
       for (int b = 0; b < D / 32; ++b) {
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
+        for (int ks = 0; ks < 2 * KB; ++ks) {
           const f16* vp = sv + v_lane + 16 * ks * kVRow + 32 * b;
           const f16x4 lo4 = read_tr(vp);
           const f16x4 hi4 = read_tr(vp + 8 * kVRow);
@@ -344,6 +372,8 @@ int pda_paged_prefill_attention(const void* queries, const void* keys, const voi
     return fail(PDA_ERR_HEAD_DIM, "head_dim %d has no prefill kernel (64, 128, 256)",
                 head_dim);
   if (count == 0) return ok();
+  if (table_len == 0)
+    return fail(PDA_ERR_INVALID_ARGUMENT, "an empty page table holds no keys of the chunk");
   if ((int64_t)start + count > INT32_MAX)
     return fail(PDA_ERR_TOO_LONG, "start + count exceeds 2^31");
   if (!queries || !keys || !values || !table || !out)

@@ -180,6 +180,7 @@ def prefill(**overrides):
     (dict(kv_heads=0), _lib.PDA_ERR_INVALID_ARGUMENT),
     (dict(page_size=0), _lib.PDA_ERR_INVALID_ARGUMENT),
     (dict(table_len=-1), _lib.PDA_ERR_INVALID_ARGUMENT),
+    (dict(table_len=0), _lib.PDA_ERR_INVALID_ARGUMENT),
     (dict(window=-1), _lib.PDA_ERR_INVALID_ARGUMENT),
     (dict(q_heads=30), _lib.PDA_ERR_HEAD_RATIO),
     (dict(head_dim=96), _lib.PDA_ERR_HEAD_DIM),
