@@ -264,6 +264,19 @@ int pda_pack_decode_step(const int32_t* seq_tables, int32_t seq_stride,
                          int32_t page_size, int32_t* tables, int32_t* lengths,
                          int32_t* rows, void* stream);
 
+/* Key ranges and workspace of a prefill call (pda_paged_prefill_attention
+ * with the same start, count, q_heads, head_dim, window and splits).
+ * `splits` 0 lets the library choose: 1 when the chunk's query tiles and
+ * heads alone fill the GPU, else enough ranges to do so (a 512-token chunk
+ * over a long prefix, the reference's default prefill chunk,
+ * mlx_engine.py:74,430). `splits` > 0 forces that many (at most 64).
+ * Writes the count used to *splits_used (may be NULL) and the bytes to
+ * *bytes (0 for one range). No counterpart in the reference, whose prefill
+ * attention is one MLX call per chunk. */
+int pda_prefill_workspace_bytes(int32_t start, int32_t count, int32_t q_heads,
+                                int32_t head_dim, int32_t window, int32_t splits,
+                                int32_t* splits_used, size_t* bytes);
+
 /* Paged prefill attention for a chunk of one sequence's prompt. Replaces
  * PrefillBatch.attend's attention (batches.py:84-132; CUDA analogue
  * cuda/kernels.cu:260-304) after the chunk's keys and values were written
@@ -272,19 +285,25 @@ int pda_pack_decode_step(const int32_t* seq_tables, int32_t seq_stride,
  *                 positions start .. start + count - 1 (queries rotated)
  *   keys, values  one layer's fp16 arena (layout as for the decode call)
  *   table         [table_len] int32, the sequence's physical pages
+ *                 (table_len >= 1)
  * Query p attends keys [first(p), p]: first(p) = max(0, p - window + 1) with
  * a window, else 0; keys on a page id that is negative, not below
  * arena_rows / page_size or past table_len are masked (the reference raises
  * on released pages in range). The score is scale * q.k, softcapped when
- * softcap > 0. head_dim in {64, 128, 256}; no workspace; one launch on
- * `stream`. */
+ * softcap > 0. head_dim in {64, 128, 256}. With more than one key range
+ * (see pda_prefill_workspace_bytes; results do not depend on `splits`
+ * beyond fp32 rounding) the ranges' partials go to `workspace` (256-byte
+ * aligned, at least the bytes that call reports) and a second launch merges
+ * them; else one launch and no workspace. Both on `stream`. */
 int pda_paged_prefill_attention(const void* queries, const void* keys,
                                 const void* values, const int32_t* table,
                                 int32_t table_len, int32_t start, int32_t count,
                                 void* out, int32_t q_heads, int32_t kv_heads,
                                 int32_t head_dim, int32_t page_size,
                                 int64_t arena_rows, int32_t layout, float scale,
-                                int32_t window, float softcap, void* stream);
+                                int32_t window, float softcap, int32_t splits,
+                                void* workspace, size_t workspace_bytes,
+                                void* stream);
 
 #ifdef __cplusplus
 }

@@ -71,6 +71,8 @@ struct PrefillParams {
   const f16* v;
   const int32_t* table;
   f16* out;            // [count, hq, D]
+  float* part_o;       // [splits, count, hq, D] unnormalised partial outputs (splits > 1)
+  float2* part_ml;     // [splits, count, hq] (running max, sum) of each partial
   int64_t arena_pages;
   int64_t page_elems;  // elements between pages of the arena
   int32_t head_elems;  // between kv heads of one page
@@ -79,6 +81,7 @@ struct PrefillParams {
   int32_t start;
   int32_t count;
   int32_t tiles;       // query tiles = ceil(count / kQueries)
+  int32_t splits;      // key ranges per (query tile, head)
   int32_t hq;
   int32_t hkv;
   int32_t page_size;
@@ -122,11 +125,12 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
   const int hh = lane >> 5;  // which half of the key rows this lane holds
 
   // Work item. Logical order: query tiles from the last (most keys) to the
-  // first, then kv head, then the G query heads of that kv head. Workgroup
-  // ids go round robin over the XCDs; whole runs of G go to one XCD.
+  // first, then key range, then kv head, then the G query heads of that kv
+  // head. Workgroup ids go round robin over the XCDs; whole runs of G (the
+  // workgroups reading the same K/V tiles) go to one XCD.
   const int G = p.hq / p.hkv;
   int item = blockIdx.x;
-  const int runs = p.tiles * p.hkv;
+  const int runs = p.tiles * p.splits * p.hkv;
   const int full = runs / kXcds * kXcds;
   if (item < full * G) {
     const int x = item % kXcds, j = item / kXcds;
@@ -135,7 +139,8 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
   const int run = item / G;
   const int h = (run % p.hkv) * G + (item - run * G);
   const int kvh = run % p.hkv;
-  const int tile = p.tiles - 1 - run / p.hkv;
+  const int split = (run / p.hkv) % p.splits;
+  const int tile = p.tiles - 1 - run / p.hkv / p.splits;
 
   const int q0 = tile * kQueries;
   const int q1 = min(q0 + kQueries, p.count);
@@ -168,6 +173,9 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
   const int last = p.start + q1 - 1;
   const int kbase = p.window > 0 ? (max(0, p.start + q0 - p.window + 1) / kKeys * kKeys) : 0;
   const int ntile = (last - kbase) / kKeys + 1;
+  // This workgroup's key range: tiles [t_begin, t_end) of the ntile.
+  const int t_begin = (int)((int64_t)ntile * split / p.splits);
+  const int t_end = (int)((int64_t)ntile * (split + 1) / p.splits);
 
   // Gather: thread tid moves key tid / kTpk of a tile, 16-byte pieces
   // tid % kTpk + kTpk i (consecutive lanes read consecutive pieces of a row).
@@ -226,15 +234,15 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
 
   int page0, r0, page1, r1;
   bool in0, in1;
-  lookup(kbase, page0, in0, r0);
-  lookup(kbase + kKeys, page1, in1, r1);
+  lookup(kbase + t_begin * kKeys, page0, in0, r0);
+  lookup(kbase + (t_begin + 1) * kKeys, page1, in1, r1);
   fetch(page0, in0, r0);
   stash(0);
   __syncthreads();
-  for (int t = 0; t < ntile; ++t) {
-    const int buf = t & 1;
+  for (int t = t_begin; t < t_end; ++t) {
+    const int buf = (t - t_begin) & 1;
     const int k0 = kbase + t * kKeys;
-    const bool more = t + 1 < ntile;
+    const bool more = t + 1 < t_end;
     if (more) fetch(page1, in1, r1);
     lookup(k0 + 2 * kKeys, page1, in1, r1);
 
@@ -333,6 +341,20 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
 
   if (!q_live) return;
   l += __shfl_xor(l, 32);
+  if (p.splits > 1) {
+    // Unnormalised partial and its (max, sum) for the merge; an empty or
+    // fully masked range leaves m = -inf, l = 0 and zeros.
+    const int64_t at = ((int64_t)split * p.count + qi) * p.hq + h;
+    float* dst = p.part_o + at * D;
+#pragma unroll
+    for (int b = 0; b < D / 32; ++b)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        *reinterpret_cast<float4*>(dst + 32 * b + 8 * g + 4 * hh) =
+            make_float4(o[b][4 * g], o[b][4 * g + 1], o[b][4 * g + 2], o[b][4 * g + 3]);
+    if (hh == 0) p.part_ml[at] = make_float2(m, l);
+    return;
+  }
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;
   f16* dst = p.out + ((int64_t)qi * p.hq + h) * D;
   // O^T rows: element 32 b + 8 (v / 4) + 4 hh + v % 4 of query n.
@@ -348,6 +370,72 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
   }
 }
 
+// Merge of the key ranges of a split prefill: for each (query, head),
+// M = max_s m_s, w_s = 2^(m_s - M) (0 for an empty range), out =
+// sum_s w_s o_s / sum_s w_s l_s (0 when nothing was visible). The same LSE
+// merge as the reference's decode merge (metal_kernels.py:103-124), in the
+// log2 domain. One thread per 4 dims, D / 4 threads per (query, head).
+template <int D>
+__global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restrict__ part_o,
+                                                            const float2* __restrict__ part_ml,
+                                                            f16* __restrict__ out, int64_t pairs,
+                                                            int splits) {
+  constexpr int kT = D / 4;
+  const int64_t pair = (int64_t)blockIdx.x * (256 / kT) + threadIdx.x / kT;
+  if (pair >= pairs) return;
+  const int d = 4 * (threadIdx.x % kT);
+  float top = -INFINITY;
+  for (int s = 0; s < splits; ++s) top = fmaxf(top, part_ml[s * pairs + pair].x);
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  float sum = 0.0f;
+  if (top != -INFINITY) {
+    for (int s = 0; s < splits; ++s) {
+      const float2 ml = part_ml[s * pairs + pair];
+      if (ml.x == -INFINITY) continue;
+      const float w = __builtin_amdgcn_exp2f(ml.x - top);
+      const float4 x = *reinterpret_cast<const float4*>(part_o + (s * pairs + pair) * D + d);
+      acc.x += w * x.x;
+      acc.y += w * x.y;
+      acc.z += w * x.z;
+      acc.w += w * x.w;
+      sum += w * ml.y;
+    }
+  }
+  const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+  f16x4 y = {(f16)(acc.x * inv), (f16)(acc.y * inv), (f16)(acc.z * inv), (f16)(acc.w * inv)};
+  *reinterpret_cast<f16x4*>(out + pair * D + d) = y;
+}
+
+constexpr int kCus = 256;       // MI355X compute units
+constexpr int kMaxSplits = 64;
+
+// Key ranges per (query tile, head): 1 when the tiles and heads alone give
+// every CU its workgroups (at the kernel's occupancy), else enough ranges to
+// do so, each at least 4 key tiles long. `request` > 0 forces a count.
+int prefill_splits(int start, int count, int q_heads, int head_dim, int window, int request) {
+  if (request > 0) return request < kMaxSplits ? request : kMaxSplits;
+  const int64_t wgs = (int64_t)(count + kQueries - 1) / kQueries * q_heads;
+  const int occupancy = head_dim == 64 ? 3 : head_dim == 128 ? 2 : 1;
+  const int64_t target = (int64_t)kCus * occupancy;
+  if (wgs >= target) return 1;
+  const int keys = 32 * (head_dim <= 128 ? 2 : 1);
+  int64_t span = (int64_t)start + count;
+  if (window > 0 && span > (int64_t)window + kQueries) span = (int64_t)window + kQueries;
+  const int64_t by_keys = (span + keys - 1) / keys / 4;
+  int64_t s = (target + wgs - 1) / wgs;
+  if (s > by_keys) s = by_keys;
+  if (s > kMaxSplits) s = kMaxSplits;
+  return s < 1 ? 1 : (int)s;
+}
+
+size_t prefill_workspace(int splits, int count, int q_heads, int head_dim) {
+  if (splits <= 1) return 0;
+  const size_t pairs = (size_t)count * q_heads;
+  // Partial outputs, then the (max, sum) pairs, each 256-byte aligned.
+  const size_t o_bytes = ((size_t)splits * pairs * head_dim * 4 + 255) & ~(size_t)255;
+  return o_bytes + (((size_t)splits * pairs * 8 + 255) & ~(size_t)255);
+}
+
 using pda_internal::fail;
 using pda_internal::ok;
 
@@ -355,17 +443,34 @@ using pda_internal::ok;
 
 extern "C" {
 
+int pda_prefill_workspace_bytes(int32_t start, int32_t count, int32_t q_heads,
+                                int32_t head_dim, int32_t window, int32_t splits,
+                                int32_t* splits_used, size_t* bytes) {
+  if (count < 0 || start < 0 || q_heads <= 0 || window < 0 || splits < 0 || !bytes)
+    return fail(PDA_ERR_INVALID_ARGUMENT, "count=%d start=%d q_heads=%d window=%d splits=%d",
+                count, start, q_heads, window, splits);
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256)
+    return fail(PDA_ERR_HEAD_DIM, "head_dim %d has no prefill kernel (64, 128, 256)",
+                head_dim);
+  const int s = count == 0 ? 1 : prefill_splits(start, count, q_heads, head_dim, window, splits);
+  if (splits_used) *splits_used = s;
+  *bytes = prefill_workspace(s, count, q_heads, head_dim);
+  return ok();
+}
+
 int pda_paged_prefill_attention(const void* queries, const void* keys, const void* values,
                                 const int32_t* table, int32_t table_len, int32_t start,
                                 int32_t count, void* out, int32_t q_heads, int32_t kv_heads,
                                 int32_t head_dim, int32_t page_size, int64_t arena_rows,
                                 int32_t layout, float scale, int32_t window, float softcap,
+                                int32_t splits, void* workspace, size_t workspace_bytes,
                                 void* stream) {
   if (count < 0 || start < 0 || q_heads <= 0 || kv_heads <= 0 || page_size <= 0 ||
-      table_len < 0 || window < 0)
+      table_len < 0 || window < 0 || splits < 0)
     return fail(PDA_ERR_INVALID_ARGUMENT,
-                "count=%d start=%d q_heads=%d kv_heads=%d page_size=%d table_len=%d window=%d",
-                count, start, q_heads, kv_heads, page_size, table_len, window);
+                "count=%d start=%d q_heads=%d kv_heads=%d page_size=%d table_len=%d window=%d "
+                "splits=%d",
+                count, start, q_heads, kv_heads, page_size, table_len, window, splits);
   if (q_heads % kv_heads)
     return fail(PDA_ERR_HEAD_RATIO, "query heads must be a multiple of kv heads");
   if (head_dim != 64 && head_dim != 128 && head_dim != 256)
@@ -390,8 +495,14 @@ int pda_paged_prefill_attention(const void* queries, const void* keys, const voi
   if (mis & 15)
     return fail(PDA_ERR_ALIGNMENT, "fp16 buffers must be 16-byte aligned");
   if ((uintptr_t)table & 3) return fail(PDA_ERR_ALIGNMENT, "the table must be 4-byte aligned");
-  if ((int64_t)((count + kQueries - 1) / kQueries) * q_heads > INT32_MAX)
-    return fail(PDA_ERR_INVALID_ARGUMENT, "query tiles x query heads exceeds 2^31");
+  const int nsplit = prefill_splits(start, count, q_heads, head_dim, window, splits);
+  if ((int64_t)((count + kQueries - 1) / kQueries) * q_heads * nsplit > INT32_MAX)
+    return fail(PDA_ERR_INVALID_ARGUMENT, "query tiles x query heads x splits exceeds 2^31");
+  const size_t need = prefill_workspace(nsplit, count, q_heads, head_dim);
+  if (need > 0 && (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 255)))
+    return fail(PDA_ERR_WORKSPACE,
+                "%d key ranges need a 256-byte aligned workspace of %zu bytes (got %zu)", nsplit,
+                need, workspace ? workspace_bytes : (size_t)0);
 
   PrefillParams prm;
   prm.q = static_cast<const f16*>(queries);
@@ -399,6 +510,12 @@ int pda_paged_prefill_attention(const void* queries, const void* keys, const voi
   prm.v = static_cast<const f16*>(values);
   prm.table = table;
   prm.out = static_cast<f16*>(out);
+  const size_t pairs = (size_t)count * q_heads;
+  prm.part_o = nsplit > 1 ? static_cast<float*>(workspace) : nullptr;
+  prm.part_ml = nsplit > 1 ? reinterpret_cast<float2*>(
+                                 static_cast<char*>(workspace) +
+                                 (((size_t)nsplit * pairs * head_dim * 4 + 255) & ~(size_t)255))
+                           : nullptr;
   prm.arena_pages = arena_rows / page_size;
   prm.page_elems = (int64_t)page_size * kv_heads * head_dim;
   if (layout == PDA_LAYOUT_ROWS) {
@@ -412,6 +529,7 @@ int pda_paged_prefill_attention(const void* queries, const void* keys, const voi
   prm.start = start;
   prm.count = count;
   prm.tiles = (count + kQueries - 1) / kQueries;
+  prm.splits = nsplit;
   prm.hq = q_heads;
   prm.hkv = kv_heads;
   prm.page_size = page_size;
@@ -424,11 +542,28 @@ int pda_paged_prefill_attention(const void* queries, const void* keys, const voi
   const void* fn = head_dim == 64    ? reinterpret_cast<const void*>(paged_prefill_kernel<64>)
                    : head_dim == 128 ? reinterpret_cast<const void*>(paged_prefill_kernel<128>)
                                      : reinterpret_cast<const void*>(paged_prefill_kernel<256>);
-  const dim3 grid((unsigned)((int64_t)prm.tiles * q_heads));
-  const hipError_t err =
-      hipLaunchKernel(fn, grid, dim3(kThreads), args, 0, static_cast<hipStream_t>(stream));
+  const hipStream_t hs = static_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)((int64_t)prm.tiles * q_heads * nsplit));
+  hipError_t err = hipLaunchKernel(fn, grid, dim3(kThreads), args, 0, hs);
   if (err != hipSuccess)
     return fail(PDA_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(err));
+  if (nsplit > 1) {
+    const int64_t npairs = (int64_t)pairs;
+    const int per_block = 256 / (head_dim / 4);
+    const float* po = prm.part_o;
+    const float2* pml = prm.part_ml;
+    f16* o16 = prm.out;
+    int ns = nsplit;
+    void* margs[] = {&po, &pml, &o16, (void*)&npairs, &ns};
+    const void* mfn =
+        head_dim == 64    ? reinterpret_cast<const void*>(prefill_merge_kernel<64>)
+        : head_dim == 128 ? reinterpret_cast<const void*>(prefill_merge_kernel<128>)
+                          : reinterpret_cast<const void*>(prefill_merge_kernel<256>);
+    err = hipLaunchKernel(mfn, dim3((unsigned)((npairs + per_block - 1) / per_block)),
+                          dim3(256), margs, 0, hs);
+    if (err != hipSuccess)
+      return fail(PDA_ERR_HIP, "merge launch failed: %s", hipGetErrorString(err));
+  }
   return ok();
 }
 

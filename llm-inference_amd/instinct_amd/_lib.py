@@ -59,7 +59,11 @@ SIGNATURES["pda_rope_append"] = (
 SIGNATURES["pda_paged_prefill_attention"] = (
     ctypes.c_int,
     [c_void_p] * 4 + [c_int32] * 3 + [c_void_p] + [c_int32] * 4
-    + [c_int64, c_int32, c_float, c_int32, c_float, c_void_p],
+    + [c_int64, c_int32, c_float, c_int32, c_float, c_int32, c_void_p, c_size_t, c_void_p],
+)
+SIGNATURES["pda_prefill_workspace_bytes"] = (
+    ctypes.c_int,
+    [c_int32] * 6 + [c_void_p, c_void_p],
 )
 SIGNATURES["pda_pack_decode_step"] = (
     ctypes.c_int,
@@ -118,6 +122,16 @@ def workspace_bytes(batch, q_heads, kv_heads, head_dim, page_size, table_stride,
                                         table_stride, longest, window, split_pages,
                                         ctypes.byref(out)))
     return out.value
+
+
+def prefill_workspace_bytes(start, count, q_heads, head_dim, window=0,
+                            splits=0) -> tuple[int, int]:
+    """(key ranges, workspace bytes) of a prefill call."""
+    used = c_int32(0)
+    out = c_size_t(0)
+    check(library().pda_prefill_workspace_bytes(start, count, q_heads, head_dim, window,
+                                                splits, ctypes.byref(used), ctypes.byref(out)))
+    return used.value, out.value
 
 
 def plan(batch, q_heads, kv_heads, head_dim, page_size, table_stride, longest, window,

@@ -364,13 +364,15 @@ def pack_decode_step(seq_tables: torch.Tensor, slots: torch.Tensor, positions: t
 
 def paged_prefill_attention(queries: torch.Tensor, keys: torch.Tensor, values: torch.Tensor,
                             table: torch.Tensor, *, start: int, page_size: int, scale: float,
-                            window: int = 0, softcap: float = 0.0,
+                            window: int = 0, softcap: float = 0.0, splits: int = 0,
                             out: torch.Tensor | None = None) -> torch.Tensor:
     """Attention of one prompt chunk (``PrefillBatch.attend``,
     batches.py:84-132): ``queries`` ``[count, q_heads, D]`` at positions
     ``start ..`` over the sequence's keys in the arena (either layout, the
     chunk's own keys already written), ``table`` the sequence's int32 pages.
-    Causal, with the window and softcap of the decode call."""
+    Causal, with the window and softcap of the decode call. ``splits`` 0
+    lets the library split long key ranges to fill the GPU; > 0 forces a
+    count (results do not depend on it beyond rounding)."""
     _check_f16("queries", queries, 3)
     count, q_heads, head_dim = (int(x) for x in queries.shape)
     layout, arena_rows, kv_heads, a_dim = _arena_geometry(keys, page_size)
@@ -382,6 +384,8 @@ def paged_prefill_attention(queries: torch.Tensor, keys: torch.Tensor, values: t
         raise ValueError("query heads must be a multiple of kv heads")
     if table.dtype != torch.int32 or table.dim() != 1 or not table.is_cuda:
         raise ValueError("table must be an int32 GPU vector")
+    if table.shape[0] == 0 and count > 0:
+        raise ValueError("the table holds no pages")
     table = table.contiguous()
     if out is None:
         out = torch.empty_like(queries)
@@ -391,11 +395,15 @@ def paged_prefill_attention(queries: torch.Tensor, keys: torch.Tensor, values: t
             raise ValueError("out must have the queries' shape")
     if count == 0:
         return out
+    _, need = _lib.prefill_workspace_bytes(int(start), count, q_heads, head_dim, int(window),
+                                           int(splits))
+    ws = workspace(queries.device, need) if need else None
     stream = torch.cuda.current_stream(queries.device).cuda_stream
     rc = _lib.library().pda_paged_prefill_attention(
         queries.data_ptr(), keys.data_ptr(), values.data_ptr(), table.data_ptr(),
         int(table.shape[0]), int(start), count, out.data_ptr(), q_heads, kv_heads, head_dim,
         int(page_size), arena_rows, layout, float(scale), int(window), float(softcap),
-        ctypes.c_void_p(stream))
+        int(splits), ws.data_ptr() if ws is not None else None,
+        ws.numel() if ws is not None else 0, ctypes.c_void_p(stream))
     _lib.check(rc)
     return out

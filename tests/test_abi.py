@@ -168,7 +168,8 @@ def test_append_alignment_and_empty_calls():
 def prefill(**overrides):
     args = dict(q=FAKE, k=FAKE, v=FAKE, table=FAKE, table_len=64, start=0, count=256,
                 out=FAKE, q_heads=28, kv_heads=4, head_dim=128, page_size=16, arena_rows=4096,
-                layout=_lib.PDA_LAYOUT_PAGES, scale=0.088, window=0, softcap=0.0, stream=None)
+                layout=_lib.PDA_LAYOUT_PAGES, scale=0.088, window=0, softcap=0.0, splits=1,
+                workspace=None, workspace_bytes=0, stream=None)
     args.update(overrides)
     return _lib.library().pda_paged_prefill_attention(*args.values())
 
@@ -182,6 +183,10 @@ def prefill(**overrides):
     (dict(table_len=-1), _lib.PDA_ERR_INVALID_ARGUMENT),
     (dict(table_len=0), _lib.PDA_ERR_INVALID_ARGUMENT),
     (dict(window=-1), _lib.PDA_ERR_INVALID_ARGUMENT),
+    (dict(splits=-1), _lib.PDA_ERR_INVALID_ARGUMENT),
+    (dict(splits=4), _lib.PDA_ERR_WORKSPACE),
+    (dict(splits=4, workspace=FAKE, workspace_bytes=1 << 20), _lib.PDA_ERR_WORKSPACE),
+    (dict(splits=4, workspace=FAKE + 16, workspace_bytes=1 << 30), _lib.PDA_ERR_WORKSPACE),
     (dict(q_heads=30), _lib.PDA_ERR_HEAD_RATIO),
     (dict(head_dim=96), _lib.PDA_ERR_HEAD_DIM),
     (dict(start=(1 << 31) - 100), _lib.PDA_ERR_TOO_LONG),
@@ -205,3 +210,21 @@ def test_prefill_validation_rejects_bad_arguments(overrides, code):
 def test_prefill_empty_chunk_is_a_no_op():
     assert prefill(count=0) == _lib.PDA_OK
     assert prefill(count=0, q=None, k=None, v=None, table=None, out=None) == _lib.PDA_OK
+
+
+def test_prefill_split_plan():
+    # The reference's 512-token chunk over a 4096-token prefix: 4 query tiles
+    # x 28 heads = 112 workgroups, split to fill 256 CUs at 2 per CU.
+    splits, need = _lib.prefill_workspace_bytes(4096, 512, 28, 128)
+    assert splits == 5
+    assert need == 5 * 512 * 28 * 128 * 4 + 5 * 512 * 28 * 8
+    # Enough query tiles: one range, no workspace.
+    assert _lib.prefill_workspace_bytes(0, 4096, 28, 128) == (1, 0)
+    # A short prefix caps the ranges at 4 key tiles each.
+    assert _lib.prefill_workspace_bytes(0, 512, 28, 128)[0] == 2
+    # Forced counts, capped at 64; empty chunks need nothing.
+    assert _lib.prefill_workspace_bytes(0, 100, 8, 64, splits=3)[0] == 3
+    assert _lib.prefill_workspace_bytes(0, 100, 8, 64, splits=500)[0] == 64
+    assert _lib.prefill_workspace_bytes(0, 0, 8, 64, splits=3) == (1, 0)
+    with pytest.raises(_lib.PdaError):
+        _lib.prefill_workspace_bytes(0, 10, 8, 96)

@@ -38,10 +38,10 @@ def case(gpu, *, hq, hkv, d, start, count, page=16, layout="pages", seed=0, rele
                    torch.as_tensor(table, device=gpu)))
 
 
-def check(c, *, scale, window=0, softcap=0.0, what=""):
+def check(c, *, scale, window=0, softcap=0.0, splits=0, what=""):
     q, k, v, table = c["t"]
     got = paged_prefill_attention(q, k, v, table, start=c["start"], page_size=c["page"],
-                                  scale=scale, window=window, softcap=softcap)
+                                  scale=scale, window=window, softcap=softcap, splits=splits)
     torch.cuda.synchronize()
     got = got.float().cpu().numpy()
     assert np.isfinite(got).all(), f"{what}: non-finite"
@@ -76,6 +76,40 @@ def test_window_softcap_and_released_pages(gpu):
     # Pages released before the window of every query are never visible.
     c = case(gpu, hq=8, hkv=4, d=128, start=2000, count=64, seed=9, released=(0, 1, 2, 3))
     check(c, scale=128 ** -0.5, window=512, what="released pages outside the window")
+
+
+@pytest.mark.parametrize("splits", [2, 3, 7, 64])
+def test_forced_key_ranges(gpu, splits):
+    """The key split and its merge: any number of ranges, including more
+    ranges than key tiles (empty ranges), gives the oracle's result."""
+    c = case(gpu, hq=28, hkv=4, d=128, start=37, count=300, seed=20 + splits)
+    check(c, scale=128 ** -0.5, splits=splits, what=f"splits {splits}")
+
+
+@pytest.mark.parametrize("d", [64, 256])
+def test_forced_key_ranges_head_dims(gpu, d):
+    c = case(gpu, hq=8, hkv=2, d=d, start=500, count=200, seed=d)
+    check(c, scale=d ** -0.5, splits=3, what=f"D{d} splits 3")
+
+
+def test_key_ranges_with_window_and_released_pages(gpu):
+    # Ranges wholly outside every query's window, or on released pages, are
+    # empty partials (max -inf) that the merge skips.
+    c = case(gpu, hq=8, hkv=4, d=128, start=2000, count=64, seed=21, released=(0, 1, 2, 3))
+    check(c, scale=128 ** -0.5, window=512, splits=5, what="window 512, released, splits 5")
+    c = case(gpu, hq=16, hkv=2, d=128, start=0, count=400, seed=22)
+    check(c, scale=128 ** -0.5, softcap=30.0, splits=4, what="softcap, splits 4")
+
+
+def test_long_prefix_chunk_splits_automatically(gpu):
+    """A chunk over a long prefix (the reference prefills 512-token chunks,
+    mlx_engine.py:74,430): the library splits the keys on its own."""
+    from instinct_amd import _lib
+
+    splits, _ = _lib.prefill_workspace_bytes(3000, 256, 8, 128)
+    assert splits > 1
+    c = case(gpu, hq=8, hkv=2, d=128, start=3000, count=256, seed=23)
+    check(c, scale=128 ** -0.5, what=f"start 3000 count 256 (auto, {splits} ranges)")
 
 
 def test_long_chunk(gpu):
