@@ -82,6 +82,7 @@ struct PrefillParams {
   int32_t count;
   int32_t tiles;       // query tiles = ceil(count / kQueries)
   int32_t splits;      // key ranges per (query tile, head)
+  int32_t page_step;   // keys per tile / page_size when that divides, else 0
   int32_t hq;
   int32_t hkv;
   int32_t page_size;
@@ -188,22 +189,33 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
   bool gok = false;
   // The table read is unconditional (index clamped, table_len >= 1) and its
   // range check a separate flag, so the loaded page id is never merged with
-  // another value, which would wait for the load.
-  auto lookup = [&](int k0, int& page, bool& in, int& r) {
-    const int kp = k0 + gk;
-    const int pi = kp / p.page_size;
-    r = kp - pi * p.page_size;
+  // another value, which would wait for the load. The cursor (key kp, page
+  // index pi, row r in the page) advances one tile per lookup; when the page
+  // size divides the tile, r stays fixed and pi steps by a constant.
+  int kp = kbase + t_begin * kKeys + gk;
+  int pi = kp / p.page_size;
+  int r = kp - pi * p.page_size;
+  auto lookup = [&](int& page, bool& in, int& row_off) {
     in = kp <= last && pi < p.table_len;
     page = p.table[min(pi, p.table_len - 1)];
+    row_off = r * p.row_elems + kvh * p.head_elems + gp * 8;
+    kp += kKeys;
+    if (p.page_step > 0) {
+      pi += p.page_step;
+    } else {
+      pi = kp / p.page_size;
+      r = kp - pi * p.page_size;
+    }
   };
-  auto fetch = [&](int page, bool in, int r) {
+  auto fetch = [&](int page, bool in, int row_off) {
     gok = in && page >= 0 && page < p.arena_pages;
-    const int64_t at = (int64_t)(gok ? page : 0) * p.page_elems +
-                       (int64_t)kvh * p.head_elems + (int64_t)r * p.row_elems + gp * 8;
+    const uint64_t at = (uint64_t)(uint32_t)(gok ? page : 0) * (uint64_t)p.page_elems + row_off;
+    const f16* kb = p.k + at;
+    const f16* vb = p.v + at;
 #pragma unroll
     for (int i = 0; i < kPieces; ++i) {
-      kr[i] = *reinterpret_cast<const f16x8*>(p.k + at + 8 * kTpk * i);
-      vr[i] = *reinterpret_cast<const f16x8*>(p.v + at + 8 * kTpk * i);
+      kr[i] = *reinterpret_cast<const f16x8*>(kb + 8 * kTpk * i);
+      vr[i] = *reinterpret_cast<const f16x8*>(vb + 8 * kTpk * i);
     }
   };
   auto stash = [&](int buf) {
@@ -211,12 +223,20 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
     // 0 * V finite whatever the arena holds there).
     f16* kd = s_k[buf] + gk * kKRow + gp * 8;
     f16* vd = s_v[buf] + gk * kVRow + gp * 8;
-#pragma unroll
-    for (int i = 0; i < kPieces; ++i) {
-      *reinterpret_cast<f16x8*>(kd + 8 * kTpk * i) = gok ? kr[i] : f16x8{};
-      *reinterpret_cast<f16x8*>(vd + 8 * kTpk * i) = gok ? vr[i] : f16x8{};
-    }
     const uint64_t bits = __ballot(gok);
+    if (bits == ~0ull) {  // wave-uniform: the usual case stores without selects
+#pragma unroll
+      for (int i = 0; i < kPieces; ++i) {
+        *reinterpret_cast<f16x8*>(kd + 8 * kTpk * i) = kr[i];
+        *reinterpret_cast<f16x8*>(vd + 8 * kTpk * i) = vr[i];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < kPieces; ++i) {
+        *reinterpret_cast<f16x8*>(kd + 8 * kTpk * i) = gok ? kr[i] : f16x8{};
+        *reinterpret_cast<f16x8*>(vd + 8 * kTpk * i) = gok ? vr[i] : f16x8{};
+      }
+    }
     if (lane == 0) {
       uint32_t mk = 0;
 #pragma unroll
@@ -231,11 +251,12 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
   const int v_lane = (4 * (g16 >> 1) + (s16 >> 2)) * kVRow + 16 * (g16 & 1) + 4 * (s16 & 3);
   const int k_lane = n * kKRow + 8 * hh;
   const int qlo = p.window > 0 ? qpos - p.window : INT32_MIN;  // keys > qlo are in the window
+  const float c = p.softcap <= 0.0f && p.scale_log2 > 0.0f ? p.scale_log2 : 1.0f;
 
   int page0, r0, page1, r1;
   bool in0, in1;
-  lookup(kbase + t_begin * kKeys, page0, in0, r0);
-  lookup(kbase + (t_begin + 1) * kKeys, page1, in1, r1);
+  lookup(page0, in0, r0);
+  lookup(page1, in1, r1);
   fetch(page0, in0, r0);
   stash(0);
   __syncthreads();
@@ -244,7 +265,7 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
     const int k0 = kbase + t * kKeys;
     const bool more = t + 1 < t_end;
     if (more) fetch(page1, in1, r1);
-    lookup(k0 + 2 * kKeys, page1, in1, r1);
+    lookup(page1, in1, r1);
 
     const bool work =
         wave_live && k0 <= wlast && (p.window <= 0 || k0 + kKeys - 1 > wfirst - p.window);
@@ -267,6 +288,10 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
       const okword okm = *reinterpret_cast<const okword*>(s_ok[buf]);
       const bool edge = k0 + kKeys - 1 > wfirst || okm != (okword)~(okword)0 ||
                         (p.window > 0 && k0 <= wlast - p.window);
+      // x = score in units that exp2(x * c - m) turns into the weight: the
+      // raw q.k with c = scale log2(e) when that is positive (the max of raw
+      // scores gives the max of the scaled ones), else the scaled or
+      // softcapped score in log2 units with c = 1.
       float x[16 * KB];
       if (p.softcap > 0.0f) {
 #pragma unroll
@@ -274,6 +299,9 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
           const float e = __builtin_amdgcn_exp2f(s[v / 16][v % 16] * p.cap_in);
           x[v] = (1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f)) * p.cap_out;
         }
+      } else if (p.scale_log2 > 0.0f) {
+#pragma unroll
+        for (int v = 0; v < 16 * KB; ++v) x[v] = s[v / 16][v % 16];
       } else {
 #pragma unroll
         for (int v = 0; v < 16 * KB; ++v) x[v] = s[v / 16][v % 16] * p.scale_log2;
@@ -294,7 +322,7 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
       float top = x[0];
 #pragma unroll
       for (int v = 1; v < 16 * KB; ++v) top = fmaxf(top, x[v]);
-      top = fmaxf(top, __shfl_xor(top, 32));  // the other half of this query's keys
+      top = fmaxf(top, __shfl_xor(top, 32)) * c;  // with the other half of this query's keys
       // Lazy running max: rescale only when a score passes it by 2^8.
       if (top > m + kSlack) {
         const float f = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - top);
@@ -314,8 +342,8 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
       for (int ks = 0; ks < 2 * KB; ++ks) {
 #pragma unroll
         for (int t2 = 0; t2 < 4; ++t2) {
-          const f16x2 ph = {(f16)__builtin_amdgcn_exp2f(x[8 * ks + 2 * t2] - mu),
-                            (f16)__builtin_amdgcn_exp2f(x[8 * ks + 2 * t2 + 1] - mu)};
+          const f16x2 ph = {(f16)__builtin_amdgcn_exp2f(fmaf(x[8 * ks + 2 * t2], c, -mu)),
+                            (f16)__builtin_amdgcn_exp2f(fmaf(x[8 * ks + 2 * t2 + 1], c, -mu))};
           l = __builtin_amdgcn_fdot2(ph, f16x2{(f16)1.0f, (f16)1.0f}, l, false);
           pb[ks][2 * t2] = ph[0];
           pb[ks][2 * t2 + 1] = ph[1];
@@ -485,6 +513,8 @@ int pda_paged_prefill_attention(const void* queries, const void* keys, const voi
     return fail(PDA_ERR_INVALID_ARGUMENT, "null buffer pointer");
   if (layout != PDA_LAYOUT_ROWS && layout != PDA_LAYOUT_PAGES)
     return fail(PDA_ERR_INVALID_ARGUMENT, "unknown K/V layout %d", layout);
+  if ((int64_t)page_size * kv_heads * head_dim > INT32_MAX)
+    return fail(PDA_ERR_INVALID_ARGUMENT, "a page of one layer holds more than 2^31 elements");
   if (arena_rows < page_size)
     return fail(PDA_ERR_INVALID_ARGUMENT, "arena_rows %lld holds no whole page",
                 (long long)arena_rows);
@@ -530,6 +560,8 @@ int pda_paged_prefill_attention(const void* queries, const void* keys, const voi
   prm.count = count;
   prm.tiles = (count + kQueries - 1) / kQueries;
   prm.splits = nsplit;
+  const int tile_keys = head_dim <= 128 ? 64 : 32;
+  prm.page_step = tile_keys % page_size == 0 ? tile_keys / page_size : 0;
   prm.hq = q_heads;
   prm.hkv = kv_heads;
   prm.page_size = page_size;
