@@ -58,9 +58,10 @@ def parse():
                          "per layer, eager and as one captured HIP graph")
     ap.add_argument("--kv-bits", type=int, choices=[16, 8], default=16,
                     help="K/V storage: fp16, or int8 with a scale per (row, kv head)")
-    ap.add_argument("--prefill-tokens", type=int, default=4096,
-                    help="prompt chunk of the prefill timing (0 = skip): one sequence at the "
-                         "workload's heads, start 0, causal")
+    ap.add_argument("--prefill", default="4096@0,512@32256",
+                    help="prefill chunks to time, TOKENS@START comma-separated ('' = skip): "
+                         "one sequence at the workload's heads, causal; the reference prefills "
+                         "512-token chunks (mlx_engine.py:74)")
     ap.add_argument("--no-flush", action="store_true", help="skip the flushed pass")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="approximate CPU time budget of the CPU-baseline sample")
@@ -201,13 +202,16 @@ def prefill_leg(w, tokens, steps, start=0):
     for _ in range(3):
         call()
     (ms,), _ = time_calls([call], max(5, min(steps, 20)))
+    from instinct_amd import _lib
+    splits, _ = _lib.prefill_workspace_bytes(start, tokens, hq, d, w.window)
     pos = np.arange(start, start + tokens, dtype=np.float64)
     seen = pos + 1 if w.window <= 0 else np.minimum(pos + 1, w.window)
     flops = 4.0 * d * hq * seen.sum()
     med = statistics.median(ms)
     tflops = flops / (med * 1e-3) / 1e12
     return {"kernel": f"paged_prefill_kernel<{d}> (pda_paged_prefill_attention)",
-            "tokens": tokens, "start": start, "q_heads": hq, "kv_heads": hkv, "head_dim": d,
+            "tokens": tokens, "start": start, "key_ranges": splits, "q_heads": hq,
+            "kv_heads": hkv, "head_dim": d,
             "us_median": round(med * 1e3, 2), "flops": flops,
             "TFLOP_per_s": round(tflops, 2), "peak_TFLOP_per_s": MFMA_F16_PEAK_TFLOPS,
             "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
@@ -428,8 +432,11 @@ def main():
     line["layer_step_us"] = round(statistics.median(step_ms) * 1e3, 2)
     if args.step_layers > 0:
         line["decode_step"] = decode_step(w, scales, args.step_layers, args.steps)
-    if args.prefill_tokens > 0 and args.kv_bits == 16:
-        line["prefill"] = prefill_leg(w, args.prefill_tokens, args.steps)
+    if args.prefill and args.kv_bits == 16:
+        line["prefill"] = []
+        for case in args.prefill.split(","):
+            tokens, start = (int(x) for x in case.split("@"))
+            line["prefill"].append(prefill_leg(w, tokens, args.steps, start=start))
     print(json.dumps(line), flush=True)
 
 
