@@ -438,19 +438,22 @@ constexpr int kCus = 256;       // MI355X compute units
 constexpr int kMaxSplits = 64;
 
 // Key ranges per (query tile, head): 1 when the tiles and heads alone give
-// every CU its workgroups (at the kernel's occupancy), else enough ranges to
-// do so, each at least 4 key tiles long. `request` > 0 forces a count.
+// every workgroup slot of the GPU (CUs x the kernel's occupancy) its work,
+// else as many as fit the slots in one round: the ranges of a chunk over a
+// long prefix are all alike, so a partly filled second round would cost a
+// whole range's time. Each range holds at least 8 key tiles. `request` > 0
+// forces a count.
 int prefill_splits(int start, int count, int q_heads, int head_dim, int window, int request) {
   if (request > 0) return request < kMaxSplits ? request : kMaxSplits;
   const int64_t wgs = (int64_t)(count + kQueries - 1) / kQueries * q_heads;
   const int occupancy = head_dim == 64 ? 3 : head_dim == 128 ? 2 : 1;
-  const int64_t target = (int64_t)kCus * occupancy;
-  if (wgs >= target) return 1;
+  const int64_t slots = (int64_t)kCus * occupancy;
+  if (wgs * 2 > slots) return 1;
   const int keys = 32 * (head_dim <= 128 ? 2 : 1);
   int64_t span = (int64_t)start + count;
   if (window > 0 && span > (int64_t)window + kQueries) span = (int64_t)window + kQueries;
-  const int64_t by_keys = (span + keys - 1) / keys / 4;
-  int64_t s = (target + wgs - 1) / wgs;
+  const int64_t by_keys = (span + keys - 1) / keys / 8;
+  int64_t s = slots / wgs;
   if (s > by_keys) s = by_keys;
   if (s > kMaxSplits) s = kMaxSplits;
   return s < 1 ? 1 : (int)s;

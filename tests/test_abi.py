@@ -214,14 +214,18 @@ def test_prefill_empty_chunk_is_a_no_op():
 
 def test_prefill_split_plan():
     # The reference's 512-token chunk over a 4096-token prefix: 4 query tiles
-    # x 28 heads = 112 workgroups, split to fill 256 CUs at 2 per CU.
+    # x 28 heads = 112 workgroups; 4 ranges fill the 512 slots (256 CUs x 2)
+    # in one round (5 would leave a second round of 48).
     splits, need = _lib.prefill_workspace_bytes(4096, 512, 28, 128)
-    assert splits == 5
-    assert need == 5 * 512 * 28 * 128 * 4 + 5 * 512 * 28 * 8
+    assert splits == 4
+    assert need == 4 * 512 * 28 * 128 * 4 + 4 * 512 * 28 * 8
+    assert _lib.prefill_workspace_bytes(3072, 1024, 28, 128)[0] == 2
     # Enough query tiles: one range, no workspace.
     assert _lib.prefill_workspace_bytes(0, 4096, 28, 128) == (1, 0)
-    # A short prefix caps the ranges at 4 key tiles each.
-    assert _lib.prefill_workspace_bytes(0, 512, 28, 128)[0] == 2
+    assert _lib.prefill_workspace_bytes(8192, 2048, 28, 128) == (1, 0)
+    # A short prefix: ranges of at least 8 key tiles.
+    assert _lib.prefill_workspace_bytes(0, 512, 28, 128) == (1, 0)
+    assert _lib.prefill_workspace_bytes(500, 512, 28, 128)[0] == 2
     # Forced counts, capped at 64; empty chunks need nothing.
     assert _lib.prefill_workspace_bytes(0, 100, 8, 64, splits=3)[0] == 3
     assert _lib.prefill_workspace_bytes(0, 100, 8, 64, splits=500)[0] == 64
