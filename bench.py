@@ -65,7 +65,7 @@ def parse():
     ap.add_argument("--no-flush", action="store_true", help="skip the flushed pass")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="approximate CPU time budget of the CPU-baseline sample")
-    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true", help="skip every CPU-baseline timing")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (rocprof counter scale)")
     return ap.parse_args()
@@ -167,6 +167,87 @@ def decode_step(w, scales, layers, steps):
     return {"layers": layers, "launches_per_step": 1 + 3 * layers,
             "eager_us": round(eager, 1), "graph_us": round(graph, 1),
             "graph_us_per_layer": round(graph / layers, 2)}
+
+
+def blas_threads() -> int:
+    """Threads numpy's OpenBLAS runs with (its environment variables, else
+    the host's cores)."""
+    for name in ("OPENBLAS_NUM_THREADS", "OMP_NUM_THREADS"):
+        if os.environ.get(name, "").isdigit():
+            return int(os.environ[name])
+    return os.cpu_count() or 1
+
+
+def prefill_cpu_baseline(w, tokens, start, budget_s):
+    """The oracle's dense prefill attention in float32 (the portable path's
+    arithmetic, portable.py:173-188) on the chunk's last queries (the ones
+    with the most keys), the sample doubled until one call takes a third of
+    budget_s; FLOP/s on the same count as the GPU leg. Each call gathers the
+    whole visible prefix (as the portable path does once per chunk), so a
+    small sample understates the CPU's rate on a whole chunk."""
+    import numpy as np
+
+    from oracle import paged_attention as pa
+
+    P, hq, hkv, d = w.page_size, w.q_heads, w.kv_heads, w.head_dim
+    end = start + tokens
+    pages = (end + P - 1) // P
+    rng = np.random.default_rng(5)
+    keys = rng.standard_normal((pages * P, hkv, d)).astype(np.float16)
+    values = rng.standard_normal((pages * P, hkv, d)).astype(np.float16)
+    table = rng.permutation(pages)
+    sample, took = 8, 0.0
+    while True:
+        n = min(sample, tokens)
+        q = rng.standard_normal((n, hq, d)).astype(np.float16)
+        t0 = time.perf_counter()
+        pa.paged_prefill_dense(q, keys, values, table, start=end - n, page_size=P,
+                               scale=w.scale, window=w.window, softcap=w.softcap,
+                               dtype=np.float32)
+        took = time.perf_counter() - t0
+        if took >= budget_s / 3 or n == tokens:
+            break
+        sample *= 2
+    pos = np.arange(end - n, end, dtype=np.float64)
+    seen = pos + 1 if w.window <= 0 else np.minimum(pos + 1, w.window)
+    flops = 4.0 * d * hq * seen.sum()
+    return {"value": round(float(flops / took / 1e12), 5), "unit": "TFLOP/s",
+            "cores": blas_threads(), "kind": "port",
+            "sample": (f"last {n} of the {tokens} queries ({flops / 1e9:.1f} GFLOP, "
+                       f"{took:.2f} s, the gather of {end} key rows included): oracle "
+                       "paged_prefill_dense in float32, NumPy/OpenBLAS, restating "
+                       "PrefillBatch.attend (batches.py:84-132)")}
+
+
+def append_cpu_baseline(w, budget_s):
+    """The oracle's RoPE + K/V write (oracle/rope_append.py, restating
+    portable.py:115-132 and paged_kv.py:278-283) on the same 64-token step,
+    repeated for ~budget_s; GB/s on the same byte count as the GPU leg."""
+    import numpy as np
+
+    from oracle import rope_append as ra
+
+    rng = np.random.default_rng(6)
+    n, hq, hkv, d, P = w.batch, w.q_heads, w.kv_heads, w.head_dim, w.page_size
+    q = rng.standard_normal((n, hq, d)).astype(np.float16)
+    k = rng.standard_normal((n, hkv, d)).astype(np.float16)
+    v = rng.standard_normal((n, hkv, d)).astype(np.float16)
+    pages = n
+    k_arena = np.zeros((pages, hkv, P, d), np.float16)
+    v_arena = np.zeros_like(k_arena)
+    positions = rng.integers(0, 8192, n)
+    rows = rng.permutation(pages * P)[:n]
+    inverse = ra.inv_freq(d, base=1e6)
+    reps, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < budget_s or reps < 3:
+        ra.rope_append(q, k, v, k_arena, v_arena, positions, rows, dims=d, inverse=inverse,
+                       layout="pages", page_size=P)
+        reps += 1
+    took = (time.perf_counter() - t0) / reps
+    nbytes = 2 * q.size * 2 + 2 * (k.size + v.size) * 2
+    return {"value": round(nbytes / took / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": (f"the {n}-token step x {reps} calls ({took * 1e6:.0f} us each): oracle "
+                       "rope_append in NumPy (its arena copies included)")}
 
 
 def prefill_leg(w, tokens, steps, start=0):
@@ -429,6 +510,8 @@ def main():
         "bytes": abytes,
         "GB_per_s": round(abytes / (app_med * 1e-3) / 1e9, 2),
     }
+    if not args.no_cpu and args.kv_bits == 16:
+        line["append"]["cpu_baseline"] = append_cpu_baseline(w, 2.0)
     line["layer_step_us"] = round(statistics.median(step_ms) * 1e3, 2)
     if args.step_layers > 0:
         line["decode_step"] = decode_step(w, scales, args.step_layers, args.steps)
@@ -436,7 +519,10 @@ def main():
         line["prefill"] = []
         for case in args.prefill.split(","):
             tokens, start = (int(x) for x in case.split("@"))
-            line["prefill"].append(prefill_leg(w, tokens, args.steps, start=start))
+            leg = prefill_leg(w, tokens, args.steps, start=start)
+            if not args.no_cpu:
+                leg["cpu_baseline"] = prefill_cpu_baseline(w, tokens, start, 6.0)
+            line["prefill"].append(leg)
     print(json.dumps(line), flush=True)
 
 

@@ -65,12 +65,15 @@ def decode_rows(tables: np.ndarray, lengths: np.ndarray, *, page_size: int, span
     return rows, valid
 
 
-def attention_plain(q, k, v, *, scale: float, mask=None, softcap: float = 0.0):
+def attention_plain(q, k, v, *, scale: float, mask=None, softcap: float = 0.0,
+                    dtype=np.float64):
     """``[B, H, Q, D]`` attention with K/V ``[B, HKV, N, D]`` (portable.py:173-188),
-    in float64. ``mask`` is a boolean array broadcastable to the scores."""
-    q = np.asarray(q, dtype=np.float64)
-    k = np.asarray(k, dtype=np.float64)
-    v = np.asarray(v, dtype=np.float64)
+    in float64 (``dtype=np.float32``: the portable path's own float32
+    arithmetic, used only for bench's CPU-baseline timing). ``mask`` is a
+    boolean array broadcastable to the scores."""
+    q = np.asarray(q, dtype=dtype)
+    k = np.asarray(k, dtype=dtype)
+    v = np.asarray(v, dtype=dtype)
     groups = q.shape[1] // k.shape[1]
     if groups > 1:
         k = np.repeat(k, groups, axis=1)
@@ -121,7 +124,7 @@ def paged_decode_dense(q, keys, values, tables, lengths, *, page_size: int, scal
 
 
 def paged_prefill_dense(q, keys, values, table, *, start: int, page_size: int, scale: float,
-                        window: int = 0, softcap: float = 0.0):
+                        window: int = 0, softcap: float = 0.0, dtype=np.float64):
     """Prefill attention of one chunk (``PrefillBatch.attend``,
     python/instinct/batches.py:84-132, no images) in float64: queries
     ``[count, HQ, D]`` at positions ``start ..``, keys/values the arena
@@ -129,7 +132,7 @@ def paged_prefill_dense(q, keys, values, table, *, start: int, page_size: int, s
     ``[first, p]``, ``first = max(0, start - window + 1)`` for the chunk and
     the causal mask aligned to the newest key, plus ``key > p - window``
     with a window; pages with a negative id are masked. Returns
-    ``[count, HQ, D]`` float64."""
+    ``[count, HQ, D]`` float64 (``dtype``: as for :func:`attention_plain`)."""
     q = np.asarray(q)
     count, hq, dim = q.shape
     end = start + count
@@ -139,8 +142,8 @@ def paged_prefill_dense(q, keys, values, table, *, start: int, page_size: int, s
     pages = table[positions // page_size]
     usable = pages >= 0
     rows = np.where(usable, pages.astype(np.int64) * page_size + positions % page_size, 0)
-    k = np.where(usable[:, None, None], np.asarray(keys)[rows].astype(np.float64), 0.0)
-    v = np.where(usable[:, None, None], np.asarray(values)[rows].astype(np.float64), 0.0)
+    k = np.where(usable[:, None, None], np.asarray(keys)[rows].astype(dtype), dtype(0))
+    v = np.where(usable[:, None, None], np.asarray(values)[rows].astype(dtype), dtype(0))
     qpos = np.arange(start, end)[:, None]
     kpos = positions[None, :]
     mask = (kpos <= qpos) & usable[None, :]
@@ -148,7 +151,7 @@ def paged_prefill_dense(q, keys, values, table, *, start: int, page_size: int, s
         mask &= kpos > qpos - window
     out = attention_plain(q.transpose(1, 0, 2)[None], k.transpose(1, 0, 2)[None],
                           v.transpose(1, 0, 2)[None], scale=scale, mask=mask[None, None],
-                          softcap=softcap)
+                          softcap=softcap, dtype=dtype)
     return out[0].transpose(1, 0, 2)
 
 
