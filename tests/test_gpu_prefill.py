@@ -67,6 +67,19 @@ def test_chunk_positions(gpu, start, count):
     check(c, scale=128 ** -0.5, what=f"start {start} count {count}")
 
 
+@pytest.mark.parametrize("layout", ["pages", "rows"])
+@pytest.mark.parametrize("page,d", [(8, 128), (32, 128), (48, 128), (64, 128), (128, 128),
+                                    (16, 256), (64, 256), (48, 64)])
+def test_page_sizes(gpu, layout, page, d):
+    """Page sizes that divide the key tile (the page cursor steps by a
+    constant) and that do not (it divides per tile), with and without key
+    ranges."""
+    c = case(gpu, hq=8, hkv=2, d=d, start=333, count=260, page=page, layout=layout,
+             seed=page + d)
+    check(c, scale=d ** -0.5, what=f"page {page} D{d} {layout}")
+    check(c, scale=d ** -0.5, splits=3, what=f"page {page} D{d} {layout} splits 3")
+
+
 def test_window_softcap_and_released_pages(gpu):
     c = case(gpu, hq=8, hkv=4, d=256, start=900, count=200, seed=7)
     check(c, scale=256 ** -0.5, window=128, what="window 128")
