@@ -305,6 +305,26 @@ int pda_paged_prefill_attention(const void* queries, const void* keys,
                                 void* workspace, size_t workspace_bytes,
                                 void* stream);
 
+/* Paged prefill attention over an 8-bit K/V cache. Replaces
+ * PrefillBatch.attend's attention with KVCache(bits=8) (batches.py:84-132,
+ * whose gather dequantizes, paged_kv.py:285-292): the arguments of
+ * pda_paged_prefill_attention with int8 `keys`/`values` and their fp16 scale
+ * arenas after `values` ([rows, kv_heads] beside the row arena,
+ * [pages, kv_heads, page_size] beside page tiles, as for
+ * pda_paged_decode_attention_q8). Each row is dequantized to
+ * fp16(int8 x scale) as the reference's gather does, then attended as in
+ * the fp16 call; the same workspace sizing (pda_prefill_workspace_bytes). */
+int pda_paged_prefill_attention_q8(const void* queries, const void* keys,
+                                   const void* values, const void* key_scales,
+                                   const void* value_scales, const int32_t* table,
+                                   int32_t table_len, int32_t start, int32_t count,
+                                   void* out, int32_t q_heads, int32_t kv_heads,
+                                   int32_t head_dim, int32_t page_size,
+                                   int64_t arena_rows, int32_t layout, float scale,
+                                   int32_t window, float softcap, int32_t splits,
+                                   void* workspace, size_t workspace_bytes,
+                                   void* stream);
+
 #ifdef __cplusplus
 }
 #endif

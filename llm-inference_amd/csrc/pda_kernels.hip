@@ -280,14 +280,8 @@ __device__ __forceinline__ f16x8 zero_unless(f16x8 x, bool keep) {
   return __builtin_bit_cast(f16x8, bits);
 }
 
-// Four int8 values (one dword) as two fp16 pairs, exactly: each byte b is
-// moved, with its sign bit flipped (b + 128), under the fp16 exponent byte
-// 0x64, which reads as 1024 + b + 128; subtracting 1152 leaves b. `sel_a` /
-// `sel_b` choose which bytes (and in which order) form the two pairs.
-__device__ __forceinline__ f16x2 bytes_to_f16x2(uint32_t flipped, uint32_t sel) {
-  const f16x2 biased = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, flipped, sel));
-  return biased - f16x2{(f16)1152.0f, (f16)1152.0f};
-}
+// Int8 bytes to fp16 pairs, exactly (pda_internal.h).
+using pda_internal::bytes_to_f16x2;
 
 struct SeqGeometry {
   int len, first, first_page, npages;

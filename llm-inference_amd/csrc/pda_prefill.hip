@@ -67,8 +67,13 @@ constexpr int kXcds = 8;
 
 struct PrefillParams {
   const f16* q;        // [count, hq, D]
-  const f16* k;        // arena
-  const f16* v;
+  const void* k;       // arena: fp16, or int8 with per-(row, kv head) fp16 scales
+  const void* v;
+  const f16* kscale;   // 8-bit only: scale arenas
+  const f16* vscale;
+  int64_t scale_page;  // scale elements between pages,
+  int32_t scale_head;  //   between kv heads of one page,
+  int32_t scale_row;   //   between rows of one page and kv head
   const int32_t* table;
   f16* out;            // [count, hq, D]
   float* part_o;       // [splits, count, hq, D] unnormalised partial outputs (splits > 1)
@@ -103,7 +108,11 @@ __device__ __forceinline__ f16x4 read_tr(const f16* p) {
 template <int D>
 constexpr int blocks_per_tile() { return D <= 128 ? 2 : 1; }
 
-template <int D>
+// Q8: the arena holds int8 rows and fp16 scales; the gather dequantizes each
+// row to fp16(int8 x scale) on its way into LDS, the values the reference's
+// 8-bit gather hands to attention (paged_kv.py:285-292), and the rest of the
+// kernel is the fp16 one.
+template <int D, bool Q8>
 __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillParams p) {
   constexpr int KB = blocks_per_tile<D>();  // 32-key blocks per tile
   constexpr int kKeys = 32 * KB;            // keys per tile
@@ -185,7 +194,11 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
   // iteration that issues it.
   const int gk = tid / kTpk;
   const int gp = tid % kTpk;
-  f16x8 kr[kPieces], vr[kPieces];
+  // Staged rows: 16 bytes (8 fp16) per piece, or 8 bytes (8 int8) and the
+  // key's two scales.
+  typedef typename std::conditional<Q8, uint2, f16x8>::type piece_t;
+  piece_t kr[kPieces], vr[kPieces];
+  f16 ksc = (f16)0.0f, vsc = (f16)0.0f;
   bool gok = false;
   // The table read is unconditional (index clamped, table_len >= 1) and its
   // range check a separate flag, so the loaded page id is never merged with
@@ -195,10 +208,11 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
   int kp = kbase + t_begin * kKeys + gk;
   int pi = kp / p.page_size;
   int r = kp - pi * p.page_size;
-  auto lookup = [&](int& page, bool& in, int& row_off) {
+  auto lookup = [&](int& page, bool& in, int& row_off, int& scale_off) {
     in = kp <= last && pi < p.table_len;
     page = p.table[min(pi, p.table_len - 1)];
     row_off = r * p.row_elems + kvh * p.head_elems + gp * 8;
+    scale_off = r * p.scale_row + kvh * p.scale_head;
     kp += kKeys;
     if (p.page_step > 0) {
       pi += p.page_step;
@@ -207,15 +221,45 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
       r = kp - pi * p.page_size;
     }
   };
-  auto fetch = [&](int page, bool in, int row_off) {
+  auto fetch = [&](int page, bool in, int row_off, int scale_off) {
     gok = in && page >= 0 && page < p.arena_pages;
-    const uint64_t at = (uint64_t)(uint32_t)(gok ? page : 0) * (uint64_t)p.page_elems + row_off;
-    const f16* kb = p.k + at;
-    const f16* vb = p.v + at;
+    const uint32_t pg = (uint32_t)(gok ? page : 0);
+    const uint64_t at = (uint64_t)pg * (uint64_t)p.page_elems + row_off;
+    if constexpr (Q8) {
+      const uint8_t* kb = static_cast<const uint8_t*>(p.k) + at;
+      const uint8_t* vb = static_cast<const uint8_t*>(p.v) + at;
 #pragma unroll
-    for (int i = 0; i < kPieces; ++i) {
-      kr[i] = *reinterpret_cast<const f16x8*>(kb + 8 * kTpk * i);
-      vr[i] = *reinterpret_cast<const f16x8*>(vb + 8 * kTpk * i);
+      for (int i = 0; i < kPieces; ++i) {
+        kr[i] = *reinterpret_cast<const uint2*>(kb + 8 * kTpk * i);
+        vr[i] = *reinterpret_cast<const uint2*>(vb + 8 * kTpk * i);
+      }
+      const uint64_t sat = (uint64_t)pg * (uint64_t)p.scale_page + scale_off;
+      ksc = p.kscale[sat];
+      vsc = p.vscale[sat];
+    } else {
+      const f16* kb = static_cast<const f16*>(p.k) + at;
+      const f16* vb = static_cast<const f16*>(p.v) + at;
+#pragma unroll
+      for (int i = 0; i < kPieces; ++i) {
+        kr[i] = *reinterpret_cast<const f16x8*>(kb + 8 * kTpk * i);
+        vr[i] = *reinterpret_cast<const f16x8*>(vb + 8 * kTpk * i);
+      }
+    }
+  };
+  // A staged piece as 8 fp16 values (8-bit: fp16(int8 x scale), one
+  // rounding of the exact product).
+  auto as_f16 = [&](const piece_t& x, f16 scale) -> f16x8 {
+    if constexpr (Q8) {
+      const f16x2 s2 = {scale, scale};
+      const uint32_t lo = x.x ^ 0x80808080u, hi = x.y ^ 0x80808080u;
+      const f16x2 e0 = pda_internal::bytes_to_f16x2(lo, 0x04010400u) * s2;
+      const f16x2 e1 = pda_internal::bytes_to_f16x2(lo, 0x04030402u) * s2;
+      const f16x2 e2 = pda_internal::bytes_to_f16x2(hi, 0x04010400u) * s2;
+      const f16x2 e3 = pda_internal::bytes_to_f16x2(hi, 0x04030402u) * s2;
+      return f16x8{e0[0], e0[1], e1[0], e1[1], e2[0], e2[1], e3[0], e3[1]};
+    } else {
+      (void)scale;
+      return x;
     }
   };
   auto stash = [&](int buf) {
@@ -227,14 +271,14 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
     if (bits == ~0ull) {  // wave-uniform: the usual case stores without selects
 #pragma unroll
       for (int i = 0; i < kPieces; ++i) {
-        *reinterpret_cast<f16x8*>(kd + 8 * kTpk * i) = kr[i];
-        *reinterpret_cast<f16x8*>(vd + 8 * kTpk * i) = vr[i];
+        *reinterpret_cast<f16x8*>(kd + 8 * kTpk * i) = as_f16(kr[i], ksc);
+        *reinterpret_cast<f16x8*>(vd + 8 * kTpk * i) = as_f16(vr[i], vsc);
       }
     } else {
 #pragma unroll
       for (int i = 0; i < kPieces; ++i) {
-        *reinterpret_cast<f16x8*>(kd + 8 * kTpk * i) = gok ? kr[i] : f16x8{};
-        *reinterpret_cast<f16x8*>(vd + 8 * kTpk * i) = gok ? vr[i] : f16x8{};
+        *reinterpret_cast<f16x8*>(kd + 8 * kTpk * i) = gok ? as_f16(kr[i], ksc) : f16x8{};
+        *reinterpret_cast<f16x8*>(vd + 8 * kTpk * i) = gok ? as_f16(vr[i], vsc) : f16x8{};
       }
     }
     if (lane == 0) {
@@ -253,19 +297,19 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
   const int qlo = p.window > 0 ? qpos - p.window : INT32_MIN;  // keys > qlo are in the window
   const float c = p.softcap <= 0.0f && p.scale_log2 > 0.0f ? p.scale_log2 : 1.0f;
 
-  int page0, r0, page1, r1;
+  int page0, r0, s0, page1, r1, s1;
   bool in0, in1;
-  lookup(page0, in0, r0);
-  lookup(page1, in1, r1);
-  fetch(page0, in0, r0);
+  lookup(page0, in0, r0, s0);
+  lookup(page1, in1, r1, s1);
+  fetch(page0, in0, r0, s0);
   stash(0);
   __syncthreads();
   for (int t = t_begin; t < t_end; ++t) {
     const int buf = (t - t_begin) & 1;
     const int k0 = kbase + t * kKeys;
     const bool more = t + 1 < t_end;
-    if (more) fetch(page1, in1, r1);
-    lookup(page1, in1, r1);
+    if (more) fetch(page1, in1, r1, s1);
+    lookup(page1, in1, r1, s1);
 
     const bool work =
         wave_live && k0 <= wlast && (p.window <= 0 || k0 + kKeys - 1 > wfirst - p.window);
@@ -470,32 +514,12 @@ size_t prefill_workspace(int splits, int count, int q_heads, int head_dim) {
 using pda_internal::fail;
 using pda_internal::ok;
 
-}  // namespace
-
-extern "C" {
-
-int pda_prefill_workspace_bytes(int32_t start, int32_t count, int32_t q_heads,
-                                int32_t head_dim, int32_t window, int32_t splits,
-                                int32_t* splits_used, size_t* bytes) {
-  if (count < 0 || start < 0 || q_heads <= 0 || window < 0 || splits < 0 || !bytes)
-    return fail(PDA_ERR_INVALID_ARGUMENT, "count=%d start=%d q_heads=%d window=%d splits=%d",
-                count, start, q_heads, window, splits);
-  if (head_dim != 64 && head_dim != 128 && head_dim != 256)
-    return fail(PDA_ERR_HEAD_DIM, "head_dim %d has no prefill kernel (64, 128, 256)",
-                head_dim);
-  const int s = count == 0 ? 1 : prefill_splits(start, count, q_heads, head_dim, window, splits);
-  if (splits_used) *splits_used = s;
-  *bytes = prefill_workspace(s, count, q_heads, head_dim);
-  return ok();
-}
-
-int pda_paged_prefill_attention(const void* queries, const void* keys, const void* values,
-                                const int32_t* table, int32_t table_len, int32_t start,
-                                int32_t count, void* out, int32_t q_heads, int32_t kv_heads,
-                                int32_t head_dim, int32_t page_size, int64_t arena_rows,
-                                int32_t layout, float scale, int32_t window, float softcap,
-                                int32_t splits, void* workspace, size_t workspace_bytes,
-                                void* stream) {
+int prefill(const void* queries, const void* keys, const void* values, const void* key_scales,
+            const void* value_scales, bool q8, const int32_t* table, int32_t table_len,
+            int32_t start, int32_t count, void* out, int32_t q_heads, int32_t kv_heads,
+            int32_t head_dim, int32_t page_size, int64_t arena_rows, int32_t layout, float scale,
+            int32_t window, float softcap, int32_t splits, void* workspace,
+            size_t workspace_bytes, void* stream) {
   if (count < 0 || start < 0 || q_heads <= 0 || kv_heads <= 0 || page_size <= 0 ||
       table_len < 0 || window < 0 || splits < 0)
     return fail(PDA_ERR_INVALID_ARGUMENT,
@@ -512,7 +536,7 @@ int pda_paged_prefill_attention(const void* queries, const void* keys, const voi
     return fail(PDA_ERR_INVALID_ARGUMENT, "an empty page table holds no keys of the chunk");
   if ((int64_t)start + count > INT32_MAX)
     return fail(PDA_ERR_TOO_LONG, "start + count exceeds 2^31");
-  if (!queries || !keys || !values || !table || !out)
+  if (!queries || !keys || !values || !table || !out || (q8 && (!key_scales || !value_scales)))
     return fail(PDA_ERR_INVALID_ARGUMENT, "null buffer pointer");
   if (layout != PDA_LAYOUT_ROWS && layout != PDA_LAYOUT_PAGES)
     return fail(PDA_ERR_INVALID_ARGUMENT, "unknown K/V layout %d", layout);
@@ -526,7 +550,9 @@ int pda_paged_prefill_attention(const void* queries, const void* keys, const voi
   const uintptr_t mis = (uintptr_t)queries | (uintptr_t)keys | (uintptr_t)values |
                         (uintptr_t)out;
   if (mis & 15)
-    return fail(PDA_ERR_ALIGNMENT, "fp16 buffers must be 16-byte aligned");
+    return fail(PDA_ERR_ALIGNMENT, "query, K/V and output buffers must be 16-byte aligned");
+  if (q8 && (((uintptr_t)key_scales | (uintptr_t)value_scales) & 1))
+    return fail(PDA_ERR_ALIGNMENT, "fp16 scale arenas must be 2-byte aligned");
   if ((uintptr_t)table & 3) return fail(PDA_ERR_ALIGNMENT, "the table must be 4-byte aligned");
   const int nsplit = prefill_splits(start, count, q_heads, head_dim, window, splits);
   if ((int64_t)((count + kQueries - 1) / kQueries) * q_heads * nsplit > INT32_MAX)
@@ -539,8 +565,15 @@ int pda_paged_prefill_attention(const void* queries, const void* keys, const voi
 
   PrefillParams prm;
   prm.q = static_cast<const f16*>(queries);
-  prm.k = static_cast<const f16*>(keys);
-  prm.v = static_cast<const f16*>(values);
+  prm.k = keys;
+  prm.v = values;
+  prm.kscale = static_cast<const f16*>(key_scales);
+  prm.vscale = static_cast<const f16*>(value_scales);
+  // Scale arenas: [rows, kv_heads] beside the row arena, [pages, kv_heads,
+  // page_size] beside page tiles (as the decode call's).
+  prm.scale_page = (int64_t)page_size * kv_heads;
+  prm.scale_row = layout == PDA_LAYOUT_ROWS ? kv_heads : 1;
+  prm.scale_head = layout == PDA_LAYOUT_ROWS ? 1 : page_size;
   prm.table = table;
   prm.out = static_cast<f16*>(out);
   const size_t pairs = (size_t)count * q_heads;
@@ -574,9 +607,13 @@ int pda_paged_prefill_attention(const void* queries, const void* keys, const voi
   prm.cap_in = softcap > 0.0f ? 2.0f * kLog2e * scale / softcap : 0.0f;
   prm.cap_out = softcap * kLog2e;
   void* args[] = {&prm};
-  const void* fn = head_dim == 64    ? reinterpret_cast<const void*>(paged_prefill_kernel<64>)
-                   : head_dim == 128 ? reinterpret_cast<const void*>(paged_prefill_kernel<128>)
-                                     : reinterpret_cast<const void*>(paged_prefill_kernel<256>);
+  const void* fn =
+      q8 ? (head_dim == 64    ? reinterpret_cast<const void*>(paged_prefill_kernel<64, true>)
+            : head_dim == 128 ? reinterpret_cast<const void*>(paged_prefill_kernel<128, true>)
+                              : reinterpret_cast<const void*>(paged_prefill_kernel<256, true>))
+         : (head_dim == 64    ? reinterpret_cast<const void*>(paged_prefill_kernel<64, false>)
+            : head_dim == 128 ? reinterpret_cast<const void*>(paged_prefill_kernel<128, false>)
+                              : reinterpret_cast<const void*>(paged_prefill_kernel<256, false>));
   const hipStream_t hs = static_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)((int64_t)prm.tiles * q_heads * nsplit));
   hipError_t err = hipLaunchKernel(fn, grid, dim3(kThreads), args, 0, hs);
@@ -600,6 +637,50 @@ int pda_paged_prefill_attention(const void* queries, const void* keys, const voi
       return fail(PDA_ERR_HIP, "merge launch failed: %s", hipGetErrorString(err));
   }
   return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+int pda_prefill_workspace_bytes(int32_t start, int32_t count, int32_t q_heads,
+                                int32_t head_dim, int32_t window, int32_t splits,
+                                int32_t* splits_used, size_t* bytes) {
+  if (count < 0 || start < 0 || q_heads <= 0 || window < 0 || splits < 0 || !bytes)
+    return fail(PDA_ERR_INVALID_ARGUMENT, "count=%d start=%d q_heads=%d window=%d splits=%d",
+                count, start, q_heads, window, splits);
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256)
+    return fail(PDA_ERR_HEAD_DIM, "head_dim %d has no prefill kernel (64, 128, 256)",
+                head_dim);
+  const int s = count == 0 ? 1 : prefill_splits(start, count, q_heads, head_dim, window, splits);
+  if (splits_used) *splits_used = s;
+  *bytes = prefill_workspace(s, count, q_heads, head_dim);
+  return ok();
+}
+
+int pda_paged_prefill_attention(const void* queries, const void* keys, const void* values,
+                                const int32_t* table, int32_t table_len, int32_t start,
+                                int32_t count, void* out, int32_t q_heads, int32_t kv_heads,
+                                int32_t head_dim, int32_t page_size, int64_t arena_rows,
+                                int32_t layout, float scale, int32_t window, float softcap,
+                                int32_t splits, void* workspace, size_t workspace_bytes,
+                                void* stream) {
+  return prefill(queries, keys, values, nullptr, nullptr, false, table, table_len, start, count,
+                 out, q_heads, kv_heads, head_dim, page_size, arena_rows, layout, scale, window,
+                 softcap, splits, workspace, workspace_bytes, stream);
+}
+
+int pda_paged_prefill_attention_q8(const void* queries, const void* keys, const void* values,
+                                   const void* key_scales, const void* value_scales,
+                                   const int32_t* table, int32_t table_len, int32_t start,
+                                   int32_t count, void* out, int32_t q_heads, int32_t kv_heads,
+                                   int32_t head_dim, int32_t page_size, int64_t arena_rows,
+                                   int32_t layout, float scale, int32_t window, float softcap,
+                                   int32_t splits, void* workspace, size_t workspace_bytes,
+                                   void* stream) {
+  return prefill(queries, keys, values, key_scales, value_scales, true, table, table_len, start,
+                 count, out, q_heads, kv_heads, head_dim, page_size, arena_rows, layout, scale,
+                 window, softcap, splits, workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

@@ -122,8 +122,8 @@ class PrefillBatch:
     """A chunk of one sequence's prompt (batches.py:26-132 without image
     tokens): positions ``start .. start + count - 1``, the chunk's K/V written
     to the cache first, then causal attention over the sequence's pages on
-    the GPU (``pda_paged_prefill_attention``), ``[count, q_heads * head_dim]``
-    out."""
+    the GPU (``pda_paged_prefill_attention``, ``_q8`` for an 8-bit cache),
+    ``[count, q_heads * head_dim]`` out."""
 
     prefill = True
 
@@ -157,13 +157,14 @@ class PrefillBatch:
 
     def attend(self, layer: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
                scale: float, softcap: float = 0.0) -> torch.Tensor:
-        """Write the chunk's K/V, then its attention (batches.py:84-132)."""
+        """Write the chunk's K/V (quantized in an 8-bit cache), then its
+        attention over the dequantized rows (batches.py:84-132,
+        paged_kv.py:285-292)."""
         group = self.cache.layer_group[layer]
-        if self.cache.bits != 16:
-            raise NotImplementedError("prefill over 8-bit K/V has no MI355X kernel yet")
         self.cache.write(layer, self._write[group.name], k, v)
         out = paged_prefill_attention(
             q.to(torch.float16).contiguous(), self.cache.keys[layer], self.cache.values[layer],
             self._tables[group.name], start=self.start, page_size=self.cache.page_size,
-            scale=scale, window=group.window, softcap=softcap)
+            scale=scale, window=group.window, softcap=softcap,
+            scales=self.cache.scales(layer))
         return out.reshape(self.count, -1)

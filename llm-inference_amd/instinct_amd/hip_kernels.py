@@ -365,6 +365,7 @@ def pack_decode_step(seq_tables: torch.Tensor, slots: torch.Tensor, positions: t
 def paged_prefill_attention(queries: torch.Tensor, keys: torch.Tensor, values: torch.Tensor,
                             table: torch.Tensor, *, start: int, page_size: int, scale: float,
                             window: int = 0, softcap: float = 0.0, splits: int = 0,
+                            scales: tuple[Any, Any] | None = None,
                             out: torch.Tensor | None = None) -> torch.Tensor:
     """Attention of one prompt chunk (``PrefillBatch.attend``,
     batches.py:84-132): ``queries`` ``[count, q_heads, D]`` at positions
@@ -372,12 +373,27 @@ def paged_prefill_attention(queries: torch.Tensor, keys: torch.Tensor, values: t
     chunk's own keys already written), ``table`` the sequence's int32 pages.
     Causal, with the window and softcap of the decode call. ``splits`` 0
     lets the library split long key ranges to fill the GPU; > 0 forces a
-    count (results do not depend on it beyond rounding)."""
+    count (results do not depend on it beyond rounding). ``scales`` =
+    (key_scales, value_scales) selects an 8-bit cache (int8 arenas, fp16
+    scales shaped as for :func:`paged_decode_attention`), dequantized as the
+    reference's gather does (paged_kv.py:285-292)."""
     _check_f16("queries", queries, 3)
     count, q_heads, head_dim = (int(x) for x in queries.shape)
     layout, arena_rows, kv_heads, a_dim = _arena_geometry(keys, page_size)
+    q8 = scales is not None
     for name, t in (("keys", keys), ("values", values)):
-        _check_f16(name, t, keys.dim())
+        if q8:
+            if t.dtype != torch.int8 or not t.is_cuda or not t.is_contiguous():
+                raise TypeError(f"{name} must be a contiguous int8 GPU tensor")
+        else:
+            _check_f16(name, t, keys.dim())
+    if q8:
+        scale_shape = tuple(keys.shape[:-1])
+        for name, t in zip(("key_scales", "value_scales"), scales):
+            if t.dtype != torch.float16 or tuple(t.shape) != scale_shape:
+                raise ValueError(f"{name} must be float16 {list(scale_shape)}")
+            if not t.is_cuda or not t.is_contiguous():
+                raise ValueError(f"{name} must be a contiguous GPU tensor")
     if tuple(values.shape) != tuple(keys.shape) or a_dim != head_dim:
         raise ValueError("keys and values must match the queries' head_dim")
     if q_heads % kv_heads:
@@ -399,8 +415,10 @@ def paged_prefill_attention(queries: torch.Tensor, keys: torch.Tensor, values: t
                                            int(splits))
     ws = workspace(queries.device, need) if need else None
     stream = torch.cuda.current_stream(queries.device).cuda_stream
-    rc = _lib.library().pda_paged_prefill_attention(
-        queries.data_ptr(), keys.data_ptr(), values.data_ptr(), table.data_ptr(),
+    entry = "pda_paged_prefill_attention" + ("_q8" if q8 else "")
+    extra = (scales[0].data_ptr(), scales[1].data_ptr()) if q8 else ()
+    rc = getattr(_lib.library(), entry)(
+        queries.data_ptr(), keys.data_ptr(), values.data_ptr(), *extra, table.data_ptr(),
         int(table.shape[0]), int(start), count, out.data_ptr(), q_heads, kv_heads, head_dim,
         int(page_size), arena_rows, layout, float(scale), int(window), float(softcap),
         int(splits), ws.data_ptr() if ws is not None else None,

@@ -13,6 +13,9 @@ Functions and the reference lines they follow:
   half to even.
 * :func:`dequantize` — what the reference's checks compare against
   (tests/test_mlx_engine.py:465-467): ``int8 * scale`` in float32.
+* :func:`gather_dequantize` — ``KVCache.gather`` at 8 bits
+  (paged_kv.py:285-292): the same product cast to fp16, what prefill
+  attention reads.
 * The attention itself is the fp16 path's oracle applied to the dequantized
   arena: the Metal kernel multiplies the score by the key's scale and the
   probability that weights the value row by the value's scale
@@ -21,8 +24,10 @@ Functions and the reference lines they follow:
 
 Pinning (tests/test_kv8_oracle.py): hand-computed rows (exact scales, ties
 rounding to even, the 1e-4 floor, clipping), round-trip error bounds
-(|x - dequantize(quantize(x))| <= scale / 2), scale invariance, and brute
-force on tiny rows.
+(|x - dequantize(quantize(x))| <= scale / 2), scale invariance, brute
+force on tiny rows, and gather_dequantize against exact rational products
+rounded half-to-even to fp16 (every int8 value, normal and subnormal
+scales).
 """
 
 from __future__ import annotations
@@ -42,6 +47,14 @@ def quantize(x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
 def dequantize(q: np.ndarray, scale: np.ndarray) -> np.ndarray:
     """int8 rows times their fp16 scales, float32."""
     return q.astype(np.float32) * scale.astype(np.float32)[..., None]
+
+
+def gather_dequantize(q: np.ndarray, scale: np.ndarray) -> np.ndarray:
+    """The rows the reference's 8-bit ``KVCache.gather`` hands to prefill
+    attention (python/instinct/paged_kv.py:285-292): ``int8 * scale`` in
+    float32, cast to the model dtype (fp16). The float32 product is exact
+    (8-bit times 11-bit significands), so this is one rounding to fp16."""
+    return dequantize(q, scale).astype(np.float16)
 
 
 def quantize_brute(row) -> tuple[list[int], float]:

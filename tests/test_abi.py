@@ -232,3 +232,21 @@ def test_prefill_split_plan():
     assert _lib.prefill_workspace_bytes(0, 0, 8, 64, splits=3) == (1, 0)
     with pytest.raises(_lib.PdaError):
         _lib.prefill_workspace_bytes(0, 10, 8, 96)
+
+
+def test_prefill_q8_validation():
+    lib = _lib.library()
+
+    def call(ks=FAKE, vs=FAKE, **overrides):
+        args = dict(q=FAKE, k=FAKE, v=FAKE, ks=ks, vs=vs, table=FAKE, table_len=64, start=0,
+                    count=256, out=FAKE, q_heads=28, kv_heads=4, head_dim=128, page_size=16,
+                    arena_rows=4096, layout=_lib.PDA_LAYOUT_PAGES, scale=0.088, window=0,
+                    softcap=0.0, splits=1, workspace=None, workspace_bytes=0, stream=None)
+        args.update(overrides)
+        return lib.pda_paged_prefill_attention_q8(*args.values())
+
+    assert call(ks=None) == _lib.PDA_ERR_INVALID_ARGUMENT
+    assert call(vs=None) == _lib.PDA_ERR_INVALID_ARGUMENT
+    assert call(ks=FAKE + 1) == _lib.PDA_ERR_ALIGNMENT
+    assert call(head_dim=80) == _lib.PDA_ERR_HEAD_DIM
+    assert call(count=0, ks=None, vs=None) == _lib.PDA_OK

@@ -11,6 +11,7 @@ import torch
 from instinct_amd.batches import PrefillBatch
 from instinct_amd.hip_kernels import paged_prefill_attention
 from instinct_amd.paged_kv import KVCache, KVGroup, pages_to_rows, rows_to_pages
+from oracle import kv8
 from oracle import paged_attention as pa
 
 pytestmark = pytest.mark.gpu
@@ -158,4 +159,94 @@ def test_prefill_batch_chunks_then_decode(gpu, layout):
                                   table, start=0, page_size=page, scale=d ** -0.5)
     err_max, err_mean = pa.error_stats(got, want)
     print(f"PrefillBatch {layout}: max_abs={err_max:.3e} mean_abs={err_mean:.3e}")
+    assert err_max <= MAX_ABS and err_mean <= MEAN_ABS
+
+
+def scales_to_pages(scales: torch.Tensor, page_size: int) -> torch.Tensor:
+    """[rows, kv_heads] -> [pages, kv_heads, page_size]."""
+    rows, heads = scales.shape
+    return scales.view(rows // page_size, page_size, heads).permute(0, 2, 1).contiguous()
+
+
+@pytest.mark.parametrize("layout", ["pages", "rows"])
+@pytest.mark.parametrize("hq,hkv,d,splits,window,page", [
+    (28, 4, 128, 0, 0, 16), (28, 4, 128, 3, 0, 16), (14, 2, 64, 2, 0, 48),
+    (8, 4, 256, 0, 0, 16), (16, 8, 256, 2, 512, 64), (8, 2, 128, 0, 100, 128),
+])
+def test_8bit_cache(gpu, layout, hq, hkv, d, splits, window, page):
+    """An 8-bit cache (int8 rows, one fp16 scale per (row, kv head), as
+    KVCache(bits=8) holds them, paged_kv.py:50-55): attention over the rows
+    the reference's gather dequantizes (oracle kv8.gather_dequantize)."""
+    rng = np.random.default_rng(d + hq + page)
+    start, count = 700, 300
+    pages = (start + count + page - 1) // page
+    arena_pages = pages + 3
+    table = rng.permutation(arena_pages)[:pages].astype(np.int32)
+    rows = arena_pages * page
+    kq, ks = kv8.quantize(rng.standard_normal((rows, hkv, d)).astype(np.float16))
+    vq, vs = kv8.quantize(rng.standard_normal((rows, hkv, d)).astype(np.float16))
+    q = rng.standard_normal((count, hq, d)).astype(np.float16)
+    keys, values = torch.as_tensor(kq, device=gpu), torch.as_tensor(vq, device=gpu)
+    k_s, v_s = torch.as_tensor(ks, device=gpu), torch.as_tensor(vs, device=gpu)
+    if layout == "pages":
+        keys, values = rows_to_pages(keys, page), rows_to_pages(values, page)
+        k_s, v_s = scales_to_pages(k_s, page), scales_to_pages(v_s, page)
+    got = paged_prefill_attention(torch.as_tensor(q, device=gpu), keys, values,
+                                  torch.as_tensor(table, device=gpu), start=start,
+                                  page_size=page, scale=d ** -0.5, window=window,
+                                  splits=splits, scales=(k_s, v_s))
+    torch.cuda.synchronize()
+    want = pa.paged_prefill_dense(q, kv8.gather_dequantize(kq, ks),
+                                  kv8.gather_dequantize(vq, vs), table, start=start,
+                                  page_size=page, scale=d ** -0.5, window=window)
+    err_max, err_mean = pa.error_stats(got.float().cpu().numpy(), want)
+    print(f"8-bit {hq}/{hkv} D{d} page {page} {layout}: max_abs={err_max:.3e} "
+          f"mean_abs={err_mean:.3e}", flush=True)
+    assert err_max <= MAX_ABS and err_mean <= MEAN_ABS
+
+
+@pytest.mark.parametrize("layout", ["pages", "rows"])
+def test_prefill_batch_8bit(gpu, layout):
+    """PrefillBatch over KVCache(bits=8): the chunks' K/V are quantized on
+    write (pda_rope_append_q8, rows = the chunk's positions), then attended
+    over the dequantized rows; two chunks against the oracle on the cache's
+    own int8 rows and scales."""
+    page, hq, hkv, d = 16, 14, 2, 64
+    groups = [KVGroup("full", (0,), kv_heads=hkv, head_dim=d)]
+    cache = KVCache(groups, page_size=page, capacities={"full": 64}, device=gpu, layout=layout,
+                    bits=8)
+    n = 300
+    table = np.array([cache.pools["full"].allocate(reserved=False)
+                      for _ in range((n + page - 1) // page)])
+    gen = torch.Generator(device=gpu).manual_seed(7)
+    q = torch.randn((n, hq, d), generator=gen, device=gpu).half()
+    k = torch.randn((n, hkv, d), generator=gen, device=gpu).half()
+    v = torch.randn((n, hkv, d), generator=gen, device=gpu).half()
+    outs = []
+    for a, b in ((0, 130), (130, n)):
+        chunk = PrefillBatch(cache, torch.zeros(b - a, device=gpu), start=a,
+                             tables={"full": table})
+        outs.append(chunk.attend(0, q[a:b], k[a:b], v[a:b], scale=d ** -0.5))
+    torch.cuda.synchronize()
+    got = torch.cat(outs).view(n, hq, d).float().cpu().numpy()
+    keys, values = cache.keys[0], cache.values[0]
+    k_s, v_s = cache.key_scales[0], cache.value_scales[0]
+    if layout == "pages":
+        keys, values = pages_to_rows(keys), pages_to_rows(values)
+        k_s = k_s.permute(0, 2, 1).reshape(-1, hkv)
+        v_s = v_s.permute(0, 2, 1).reshape(-1, hkv)
+    kq, vq = keys.cpu().numpy(), values.cpu().numpy()
+    ks, vs = k_s.cpu().numpy(), v_s.cpu().numpy()
+    # The write quantized the chunks' rows as the oracle does.
+    rows = np.concatenate([table[p // page] * page + np.arange(p % page, min(page, n - p))
+                           for p in range(0, n, page)])
+    want_kq, want_ks = kv8.quantize(k.cpu().numpy())
+    np.testing.assert_array_equal(vq[rows], kv8.quantize(v.cpu().numpy())[0])
+    np.testing.assert_array_equal(ks[rows], want_ks)
+    assert np.abs(kq[rows].astype(int) - want_kq.astype(int)).max() <= 0
+    want = pa.paged_prefill_dense(q.cpu().numpy(), kv8.gather_dequantize(kq, ks),
+                                  kv8.gather_dequantize(vq, vs), table, start=0,
+                                  page_size=page, scale=d ** -0.5)
+    err_max, err_mean = pa.error_stats(got, want)
+    print(f"PrefillBatch 8-bit {layout}: max_abs={err_max:.3e} mean_abs={err_mean:.3e}")
     assert err_max <= MAX_ABS and err_mean <= MEAN_ABS

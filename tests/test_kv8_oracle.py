@@ -55,3 +55,41 @@ def test_scale_invariance_and_brute_force():
     for row, qrow, srow in zip(x, q1, s1):
         want, scale = kv8.quantize_brute(row)
         assert qrow.tolist() == want and float(srow) == scale
+
+
+def _round_to_f16(value):
+    """A Fraction rounded half to even to the nearest fp16 (finite range),
+    from the fp16 grid alone."""
+    from fractions import Fraction
+
+    if value == 0:
+        return 0.0
+    sign = -1 if value < 0 else 1
+    mag = abs(value)
+    # fp16: 10 fraction bits, exponents -14..15, subnormal step 2^-24.
+    exp = max(-14, min(15, mag.numerator.bit_length() - mag.denominator.bit_length()))
+    while exp > -14 and Fraction(2) ** exp > mag:
+        exp -= 1
+    while exp < 15 and Fraction(2) ** (exp + 1) <= mag:
+        exp += 1
+    step = Fraction(2) ** (exp - 10)
+    k, rem = divmod(mag, step)
+    k = int(k)
+    if rem * 2 > step or (rem * 2 == step and k % 2 == 1):
+        k += 1
+    return sign * float(k * step)
+
+
+def test_gather_dequantize_is_one_rounding_of_the_exact_product():
+    """Every int8 value times normal and subnormal fp16 scales: the float32
+    product cast to fp16 (paged_kv.py:289-291) equals the exact rational
+    product rounded half to even to fp16."""
+    from fractions import Fraction
+
+    q = np.arange(-127, 128, dtype=np.int8)
+    scales = np.array([1e-4 / 127, 3e-6, 6.1e-5, 0.0078125, 0.01234, 0.5, 1.0, 3.3, 200.0],
+                      dtype=np.float16)
+    got = kv8.gather_dequantize(np.repeat(q[None, :], len(scales), axis=0), scales)
+    for i, s in enumerate(scales):
+        exact = [_round_to_f16(Fraction(int(b)) * Fraction(float(s))) for b in q]
+        np.testing.assert_array_equal(got[i].astype(np.float64), np.array(exact))
