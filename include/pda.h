@@ -290,7 +290,11 @@ int pda_prefill_workspace_bytes(int32_t start, int32_t count, int32_t q_heads,
  * a window, else 0; keys on a page id that is negative, not below
  * arena_rows / page_size or past table_len are masked (the reference raises
  * on released pages in range). The score is scale * q.k, softcapped when
- * softcap > 0. head_dim in {64, 128, 256}. With more than one key range
+ * softcap > 0. `images` (device int32 [num_images, 2], may be NULL when
+ * num_images is 0) lists image-token spans [begin, end) of positions: a
+ * query inside a span also sees every key of that span up to the chunk's
+ * end, whatever the causal limit and the window (batches.py:107-118).
+ * head_dim in {64, 128, 256}. With more than one key range
  * (see pda_prefill_workspace_bytes; results do not depend on `splits`
  * beyond fp32 rounding) the ranges' partials go to `workspace` (256-byte
  * aligned, at least the bytes that call reports) and a second launch merges
@@ -301,9 +305,10 @@ int pda_paged_prefill_attention(const void* queries, const void* keys,
                                 void* out, int32_t q_heads, int32_t kv_heads,
                                 int32_t head_dim, int32_t page_size,
                                 int64_t arena_rows, int32_t layout, float scale,
-                                int32_t window, float softcap, int32_t splits,
-                                void* workspace, size_t workspace_bytes,
-                                void* stream);
+                                int32_t window, float softcap,
+                                const int32_t* images, int32_t num_images,
+                                int32_t splits, void* workspace,
+                                size_t workspace_bytes, void* stream);
 
 /* Paged prefill attention over an 8-bit K/V cache. Replaces
  * PrefillBatch.attend's attention with KVCache(bits=8) (batches.py:84-132,
@@ -321,9 +326,10 @@ int pda_paged_prefill_attention_q8(const void* queries, const void* keys,
                                    void* out, int32_t q_heads, int32_t kv_heads,
                                    int32_t head_dim, int32_t page_size,
                                    int64_t arena_rows, int32_t layout, float scale,
-                                   int32_t window, float softcap, int32_t splits,
-                                   void* workspace, size_t workspace_bytes,
-                                   void* stream);
+                                   int32_t window, float softcap,
+                                   const int32_t* images, int32_t num_images,
+                                   int32_t splits, void* workspace,
+                                   size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -75,6 +75,8 @@ struct PrefillParams {
   int32_t scale_head;  //   between kv heads of one page,
   int32_t scale_row;   //   between rows of one page and kv head
   const int32_t* table;
+  const int32_t* images;  // [num_images, 2] image spans [begin, end) of positions
+  int32_t num_images;
   f16* out;            // [count, hq, D]
   float* part_o;       // [splits, count, hq, D] unnormalised partial outputs (splits > 1)
   float2* part_ml;     // [splits, count, hq] (running max, sum) of each partial
@@ -180,8 +182,28 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
 
   // Keys this workgroup needs: from the first visible key of its first query
   // (rounded down to a tile) to its last query.
-  const int last = p.start + q1 - 1;
-  const int kbase = p.window > 0 ? (max(0, p.start + q0 - p.window + 1) / kKeys * kKeys) : 0;
+  int last = p.start + q1 - 1;
+  int kfirst = p.window > 0 ? max(0, p.start + q0 - p.window + 1) : 0;
+  // Image spans (batches.py:107-118): a query inside one also sees the
+  // span's later keys, whatever the window. The lane keeps its query's span
+  // [img_lo, img_hi); the workgroup and each wave extend their key ranges to
+  // the spans their queries touch (keys stop at the chunk's end).
+  int img_lo = 0, img_hi = 0, wave_last = wlast;
+  bool wave_img = false;
+  for (int i = 0; i < p.num_images; ++i) {
+    const int a = p.images[2 * i], b = min(p.images[2 * i + 1], p.start + p.count);
+    if (a >= b) continue;
+    if (qpos >= a && qpos < b) img_lo = a, img_hi = b;
+    if (a <= last && b > p.start + q0) {
+      last = max(last, b - 1);
+      kfirst = min(kfirst, a);
+    }
+    if (wave_live && a <= wlast && b > wfirst) {
+      wave_last = max(wave_last, b - 1);
+      wave_img = true;
+    }
+  }
+  const int kbase = kfirst / kKeys * kKeys;
   const int ntile = (last - kbase) / kKeys + 1;
   // This workgroup's key range: tiles [t_begin, t_end) of the ntile.
   const int t_begin = (int)((int64_t)ntile * split / p.splits);
@@ -311,8 +333,8 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
     if (more) fetch(page1, in1, r1, s1);
     lookup(page1, in1, r1, s1);
 
-    const bool work =
-        wave_live && k0 <= wlast && (p.window <= 0 || k0 + kKeys - 1 > wfirst - p.window);
+    const bool work = wave_live && k0 <= wave_last &&
+                      (p.window <= 0 || wave_img || k0 + kKeys - 1 > wfirst - p.window);
     if (work) {
       const f16* sk = s_k[buf];
       const f16* sv = s_v[buf];
@@ -356,11 +378,17 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
         const okword okl = okm >> (4 * hh);
         const int hi = qpos - k0 - 4 * hh;  // largest visible key offset
         const int lo = qlo == INT32_MIN ? INT32_MIN : qlo - k0 - 4 * hh;
+        const int ilo = img_lo - k0 - 4 * hh, ihi = img_hi - k0 - 4 * hh;  // image span
+        // Bitwise operators, not && / ||: the short-circuit form compiled to
+        // nested exec-mask branches, one of which dropped the restore of the
+        // score for lanes visible through the image span only.
 #pragma unroll
         for (int v = 0; v < 16 * KB; ++v) {
           const int key = 32 * (v / 16) + 8 * ((v % 16) / 4) + (v % 4);  // minus 4 hh
-          const bool vis = ((okl >> key) & 1u) && key <= hi && key > lo;
-          x[v] = vis ? x[v] : -INFINITY;
+          const bool usable_key = ((okl >> key) & 1u) != 0;
+          const bool causal = (key <= hi) & (key > lo);
+          const bool image = (key >= ilo) & (key < ihi);
+          x[v] = usable_key & (causal | image) ? x[v] : -INFINITY;
         }
       }
       float top = x[0];
@@ -518,8 +546,8 @@ int prefill(const void* queries, const void* keys, const void* values, const voi
             const void* value_scales, bool q8, const int32_t* table, int32_t table_len,
             int32_t start, int32_t count, void* out, int32_t q_heads, int32_t kv_heads,
             int32_t head_dim, int32_t page_size, int64_t arena_rows, int32_t layout, float scale,
-            int32_t window, float softcap, int32_t splits, void* workspace,
-            size_t workspace_bytes, void* stream) {
+            int32_t window, float softcap, const int32_t* images, int32_t num_images,
+            int32_t splits, void* workspace, size_t workspace_bytes, void* stream) {
   if (count < 0 || start < 0 || q_heads <= 0 || kv_heads <= 0 || page_size <= 0 ||
       table_len < 0 || window < 0 || splits < 0)
     return fail(PDA_ERR_INVALID_ARGUMENT,
@@ -538,6 +566,10 @@ int prefill(const void* queries, const void* keys, const void* values, const voi
     return fail(PDA_ERR_TOO_LONG, "start + count exceeds 2^31");
   if (!queries || !keys || !values || !table || !out || (q8 && (!key_scales || !value_scales)))
     return fail(PDA_ERR_INVALID_ARGUMENT, "null buffer pointer");
+  if (num_images < 0 || (num_images > 0 && !images))
+    return fail(PDA_ERR_INVALID_ARGUMENT, "num_images=%d needs an image span array",
+                num_images);
+  if ((uintptr_t)images & 3) return fail(PDA_ERR_ALIGNMENT, "image spans must be 4-byte aligned");
   if (layout != PDA_LAYOUT_ROWS && layout != PDA_LAYOUT_PAGES)
     return fail(PDA_ERR_INVALID_ARGUMENT, "unknown K/V layout %d", layout);
   if ((int64_t)page_size * kv_heads * head_dim > INT32_MAX)
@@ -575,6 +607,8 @@ int prefill(const void* queries, const void* keys, const void* values, const voi
   prm.scale_row = layout == PDA_LAYOUT_ROWS ? kv_heads : 1;
   prm.scale_head = layout == PDA_LAYOUT_ROWS ? 1 : page_size;
   prm.table = table;
+  prm.images = images;
+  prm.num_images = num_images;
   prm.out = static_cast<f16*>(out);
   const size_t pairs = (size_t)count * q_heads;
   prm.part_o = nsplit > 1 ? static_cast<float*>(workspace) : nullptr;
@@ -663,11 +697,11 @@ int pda_paged_prefill_attention(const void* queries, const void* keys, const voi
                                 int32_t count, void* out, int32_t q_heads, int32_t kv_heads,
                                 int32_t head_dim, int32_t page_size, int64_t arena_rows,
                                 int32_t layout, float scale, int32_t window, float softcap,
-                                int32_t splits, void* workspace, size_t workspace_bytes,
-                                void* stream) {
+                                const int32_t* images, int32_t num_images, int32_t splits,
+                                void* workspace, size_t workspace_bytes, void* stream) {
   return prefill(queries, keys, values, nullptr, nullptr, false, table, table_len, start, count,
                  out, q_heads, kv_heads, head_dim, page_size, arena_rows, layout, scale, window,
-                 softcap, splits, workspace, workspace_bytes, stream);
+                 softcap, images, num_images, splits, workspace, workspace_bytes, stream);
 }
 
 int pda_paged_prefill_attention_q8(const void* queries, const void* keys, const void* values,
@@ -676,11 +710,11 @@ int pda_paged_prefill_attention_q8(const void* queries, const void* keys, const 
                                    int32_t count, void* out, int32_t q_heads, int32_t kv_heads,
                                    int32_t head_dim, int32_t page_size, int64_t arena_rows,
                                    int32_t layout, float scale, int32_t window, float softcap,
-                                   int32_t splits, void* workspace, size_t workspace_bytes,
-                                   void* stream) {
+                                   const int32_t* images, int32_t num_images, int32_t splits,
+                                   void* workspace, size_t workspace_bytes, void* stream) {
   return prefill(queries, keys, values, key_scales, value_scales, true, table, table_len, start,
                  count, out, q_heads, kv_heads, head_dim, page_size, arena_rows, layout, scale,
-                 window, softcap, splits, workspace, workspace_bytes, stream);
+                 window, softcap, images, num_images, splits, workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

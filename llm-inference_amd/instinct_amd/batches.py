@@ -22,7 +22,8 @@ from typing import Any
 import numpy as np
 import torch
 
-from .hip_kernels import paged_decode_attention, paged_prefill_attention, rope, rope_append
+from .hip_kernels import (image_spans, paged_decode_attention, paged_prefill_attention, rope,
+                          rope_append)
 from .paged_kv import KVCache
 
 
@@ -119,22 +120,27 @@ class DecodeBatch:
 
 
 class PrefillBatch:
-    """A chunk of one sequence's prompt (batches.py:26-132 without image
-    tokens): positions ``start .. start + count - 1``, the chunk's K/V written
-    to the cache first, then causal attention over the sequence's pages on
-    the GPU (``pda_paged_prefill_attention``, ``_q8`` for an 8-bit cache),
-    ``[count, q_heads * head_dim]`` out."""
+    """A chunk of one sequence's prompt (batches.py:26-132): positions
+    ``start .. start + count - 1``, the chunk's K/V written to the cache
+    first, then causal attention over the sequence's pages on the GPU
+    (``pda_paged_prefill_attention``, ``_q8`` for an 8-bit cache),
+    ``[count, q_heads * head_dim]`` out. ``images``: (at, embeddings) as the
+    reference takes them (or (at, length)); their tokens also see the rest of
+    their image (batches.py:107-118)."""
 
     prefill = True
 
     def __init__(self, cache: KVCache, tokens: torch.Tensor, *, start: int,
-                 tables: dict[str, np.ndarray]) -> None:
+                 tables: dict[str, np.ndarray], images: Any = ()) -> None:
         device = cache.device
         self.cache = cache
         self.tokens = tokens
         self.count = int(tokens.shape[0])
         self.start = int(start)
+        self.images = list(images)
         end = self.start + self.count
+        self._spans = image_spans(
+            [(at, x if isinstance(x, int) else int(x.shape[0])) for at, x in self.images], device)
         self.offsets = torch.arange(self.start, end, dtype=torch.int32, device=device)
         self._write: dict[str, torch.Tensor] = {}
         self._tables: dict[str, torch.Tensor] = {}
@@ -147,6 +153,16 @@ class PrefillBatch:
     @property
     def positions(self) -> torch.Tensor:
         return self.offsets
+
+    def inject(self, x: torch.Tensor) -> torch.Tensor:
+        """Put image embeddings in place of their placeholder tokens
+        (batches.py:63-68)."""
+        for at, embeddings in self.images:
+            if isinstance(embeddings, int):
+                continue
+            offset = at - self.start
+            x[offset:offset + int(embeddings.shape[0])] = embeddings.to(x.dtype)
+        return x
 
     def rope(self, x: torch.Tensor, dims: int, *, base: float | None = None,
              freqs: Any = None) -> torch.Tensor:
@@ -166,5 +182,6 @@ class PrefillBatch:
             q.to(torch.float16).contiguous(), self.cache.keys[layer], self.cache.values[layer],
             self._tables[group.name], start=self.start, page_size=self.cache.page_size,
             scale=scale, window=group.window, softcap=softcap,
-            scales=self.cache.scales(layer))
+            scales=self.cache.scales(layer),
+            images=self._spans if self._spans is not None else ())
         return out.reshape(self.count, -1)

@@ -362,10 +362,26 @@ def pack_decode_step(seq_tables: torch.Tensor, slots: torch.Tensor, positions: t
     return tables, lengths, rows
 
 
+def image_spans(images: Any, device: torch.device) -> torch.Tensor | None:
+    """Image spans as the prefill call takes them: an int32 ``[n, 2]`` GPU
+    tensor of [begin, end) positions (None for none), from (at, length)
+    pairs or such a tensor."""
+    if isinstance(images, torch.Tensor):
+        if images.numel() == 0:
+            return None
+        if images.dtype != torch.int32 or images.dim() != 2 or images.shape[1] != 2:
+            raise ValueError("image spans must be an int32 [n, 2] tensor")
+        return images.to(device).contiguous()
+    pairs = [(int(at), int(at) + int(length)) for at, length in images if int(length) > 0]
+    if not pairs:
+        return None
+    return torch.tensor(pairs, dtype=torch.int32, device=device)
+
+
 def paged_prefill_attention(queries: torch.Tensor, keys: torch.Tensor, values: torch.Tensor,
                             table: torch.Tensor, *, start: int, page_size: int, scale: float,
                             window: int = 0, softcap: float = 0.0, splits: int = 0,
-                            scales: tuple[Any, Any] | None = None,
+                            scales: tuple[Any, Any] | None = None, images: Any = (),
                             out: torch.Tensor | None = None) -> torch.Tensor:
     """Attention of one prompt chunk (``PrefillBatch.attend``,
     batches.py:84-132): ``queries`` ``[count, q_heads, D]`` at positions
@@ -376,7 +392,10 @@ def paged_prefill_attention(queries: torch.Tensor, keys: torch.Tensor, values: t
     count (results do not depend on it beyond rounding). ``scales`` =
     (key_scales, value_scales) selects an 8-bit cache (int8 arenas, fp16
     scales shaped as for :func:`paged_decode_attention`), dequantized as the
-    reference's gather does (paged_kv.py:285-292)."""
+    reference's gather does (paged_kv.py:285-292). ``images``: (at, length)
+    spans of image tokens, or an int32 GPU tensor ``[n, 2]`` of [begin, end)
+    positions; a query inside one also sees the span's later keys
+    (batches.py:107-118)."""
     _check_f16("queries", queries, 3)
     count, q_heads, head_dim = (int(x) for x in queries.shape)
     layout, arena_rows, kv_heads, a_dim = _arena_geometry(keys, page_size)
@@ -415,12 +434,15 @@ def paged_prefill_attention(queries: torch.Tensor, keys: torch.Tensor, values: t
                                            int(splits))
     ws = workspace(queries.device, need) if need else None
     stream = torch.cuda.current_stream(queries.device).cuda_stream
+    spans = image_spans(images, queries.device)
     entry = "pda_paged_prefill_attention" + ("_q8" if q8 else "")
     extra = (scales[0].data_ptr(), scales[1].data_ptr()) if q8 else ()
     rc = getattr(_lib.library(), entry)(
         queries.data_ptr(), keys.data_ptr(), values.data_ptr(), *extra, table.data_ptr(),
         int(table.shape[0]), int(start), count, out.data_ptr(), q_heads, kv_heads, head_dim,
         int(page_size), arena_rows, layout, float(scale), int(window), float(softcap),
+        spans.data_ptr() if spans is not None else None,
+        int(spans.shape[0]) if spans is not None else 0,
         int(splits), ws.data_ptr() if ws is not None else None,
         ws.numel() if ws is not None else 0, ctypes.c_void_p(stream))
     _lib.check(rc)

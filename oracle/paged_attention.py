@@ -124,15 +124,18 @@ def paged_decode_dense(q, keys, values, tables, lengths, *, page_size: int, scal
 
 
 def paged_prefill_dense(q, keys, values, table, *, start: int, page_size: int, scale: float,
-                        window: int = 0, softcap: float = 0.0, dtype=np.float64):
+                        window: int = 0, softcap: float = 0.0, images=(), dtype=np.float64):
     """Prefill attention of one chunk (``PrefillBatch.attend``,
     python/instinct/batches.py:84-132, no images) in float64: queries
     ``[count, HQ, D]`` at positions ``start ..``, keys/values the arena
     ``[rows, HKV, D]``, ``table`` the sequence's pages. Query p sees keys
     ``[first, p]``, ``first = max(0, start - window + 1)`` for the chunk and
     the causal mask aligned to the newest key, plus ``key > p - window``
-    with a window; pages with a negative id are masked. Returns
-    ``[count, HQ, D]`` float64 (``dtype``: as for :func:`attention_plain`)."""
+    with a window; pages with a negative id are masked. ``images``: (at,
+    length) spans of image tokens; a query inside a span also sees every key
+    of that span (batches.py:107-118), whatever the causal limit and the
+    window. Returns ``[count, HQ, D]`` float64 (``dtype``: as for
+    :func:`attention_plain`)."""
     q = np.asarray(q)
     count, hq, dim = q.shape
     end = start + count
@@ -149,6 +152,9 @@ def paged_prefill_dense(q, keys, values, table, *, start: int, page_size: int, s
     mask = (kpos <= qpos) & usable[None, :]
     if window:
         mask &= kpos > qpos - window
+    for at, length in images:
+        inside = (qpos >= at) & (qpos < at + length)
+        mask |= inside & (kpos >= at) & (kpos < at + length) & usable[None, :]
     out = attention_plain(q.transpose(1, 0, 2)[None], k.transpose(1, 0, 2)[None],
                           v.transpose(1, 0, 2)[None], scale=scale, mask=mask[None, None],
                           softcap=softcap, dtype=dtype)

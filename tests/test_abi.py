@@ -168,8 +168,8 @@ def test_append_alignment_and_empty_calls():
 def prefill(**overrides):
     args = dict(q=FAKE, k=FAKE, v=FAKE, table=FAKE, table_len=64, start=0, count=256,
                 out=FAKE, q_heads=28, kv_heads=4, head_dim=128, page_size=16, arena_rows=4096,
-                layout=_lib.PDA_LAYOUT_PAGES, scale=0.088, window=0, softcap=0.0, splits=1,
-                workspace=None, workspace_bytes=0, stream=None)
+                layout=_lib.PDA_LAYOUT_PAGES, scale=0.088, window=0, softcap=0.0, images=None,
+                num_images=0, splits=1, workspace=None, workspace_bytes=0, stream=None)
     args.update(overrides)
     return _lib.library().pda_paged_prefill_attention(*args.values())
 
@@ -184,6 +184,9 @@ def prefill(**overrides):
     (dict(table_len=0), _lib.PDA_ERR_INVALID_ARGUMENT),
     (dict(window=-1), _lib.PDA_ERR_INVALID_ARGUMENT),
     (dict(splits=-1), _lib.PDA_ERR_INVALID_ARGUMENT),
+    (dict(num_images=-1), _lib.PDA_ERR_INVALID_ARGUMENT),
+    (dict(num_images=2), _lib.PDA_ERR_INVALID_ARGUMENT),      # spans missing
+    (dict(num_images=2, images=FAKE + 2), _lib.PDA_ERR_ALIGNMENT),
     (dict(splits=4), _lib.PDA_ERR_WORKSPACE),
     (dict(splits=4, workspace=FAKE, workspace_bytes=1 << 20), _lib.PDA_ERR_WORKSPACE),
     (dict(splits=4, workspace=FAKE + 16, workspace_bytes=1 << 30), _lib.PDA_ERR_WORKSPACE),
@@ -241,7 +244,8 @@ def test_prefill_q8_validation():
         args = dict(q=FAKE, k=FAKE, v=FAKE, ks=ks, vs=vs, table=FAKE, table_len=64, start=0,
                     count=256, out=FAKE, q_heads=28, kv_heads=4, head_dim=128, page_size=16,
                     arena_rows=4096, layout=_lib.PDA_LAYOUT_PAGES, scale=0.088, window=0,
-                    softcap=0.0, splits=1, workspace=None, workspace_bytes=0, stream=None)
+                    softcap=0.0, images=None, num_images=0, splits=1, workspace=None,
+                    workspace_bytes=0, stream=None)
         args.update(overrides)
         return lib.pda_paged_prefill_attention_q8(*args.values())
 

@@ -39,16 +39,17 @@ def case(gpu, *, hq, hkv, d, start, count, page=16, layout="pages", seed=0, rele
                    torch.as_tensor(table, device=gpu)))
 
 
-def check(c, *, scale, window=0, softcap=0.0, splits=0, what=""):
+def check(c, *, scale, window=0, softcap=0.0, splits=0, images=(), what=""):
     q, k, v, table = c["t"]
     got = paged_prefill_attention(q, k, v, table, start=c["start"], page_size=c["page"],
-                                  scale=scale, window=window, softcap=softcap, splits=splits)
+                                  scale=scale, window=window, softcap=softcap, splits=splits,
+                                  images=images)
     torch.cuda.synchronize()
     got = got.float().cpu().numpy()
     assert np.isfinite(got).all(), f"{what}: non-finite"
     want = pa.paged_prefill_dense(c["q"], c["keys"], c["values"], c["table"], start=c["start"],
                                   page_size=c["page"], scale=scale, window=window,
-                                  softcap=softcap)
+                                  softcap=softcap, images=images)
     err_max, err_mean = pa.error_stats(got, want)
     print(f"{what}: max_abs={err_max:.3e} mean_abs={err_mean:.3e}", flush=True)
     assert err_max <= MAX_ABS and err_mean <= MEAN_ABS, (what, err_max, err_mean)
@@ -250,3 +251,79 @@ def test_prefill_batch_8bit(gpu, layout):
     err_max, err_mean = pa.error_stats(got, want)
     print(f"PrefillBatch 8-bit {layout}: max_abs={err_max:.3e} mean_abs={err_mean:.3e}")
     assert err_max <= MAX_ABS and err_mean <= MEAN_ABS
+
+
+@pytest.mark.parametrize("splits", [0, 3])
+@pytest.mark.parametrize("hq,hkv,d", [(28, 4, 128), (14, 2, 64), (8, 4, 256)])
+def test_image_spans(gpu, hq, hkv, d, splits):
+    """Image tokens see their whole image (batches.py:107-118): spans inside
+    one wave's queries, across waves and across 128-query workgroup tiles,
+    one at the chunk's end, with and without key ranges."""
+    c = case(gpu, hq=hq, hkv=hkv, d=d, start=100, count=420, seed=30 + d + splits)
+    images = [(110, 7), (150, 40), (220, 200), (500, 20)]
+    check(c, scale=d ** -0.5, splits=splits, images=images,
+          what=f"images {hq}/{hkv} D{d} splits {splits}")
+
+
+def test_image_spans_with_window_and_8bit(gpu):
+    # An image longer than the window: its tokens see all of it.
+    c = case(gpu, hq=8, hkv=2, d=128, start=1000, count=300, seed=41)
+    check(c, scale=128 ** -0.5, window=64, images=[(1010, 150), (1200, 3)],
+          what="images with window 64")
+    check(c, scale=128 ** -0.5, window=64, splits=4, images=[(1010, 150)],
+          what="images with window 64, splits 4")
+    # Spans outside the chunk change nothing; an empty span is ignored.
+    check(c, scale=128 ** -0.5, images=[(0, 500), (1400, 0)], what="images outside the chunk")
+
+
+@pytest.mark.parametrize("bits", [16, 8])
+def test_prefill_batch_images(gpu, bits):
+    """PrefillBatch with an image (as (at, embeddings)): inject puts the
+    embeddings in place; attention lets the image's tokens see all of it."""
+    page, hq, hkv, d = 16, 8, 2, 128
+    groups = [KVGroup("full", (0,), kv_heads=hkv, head_dim=d)]
+    cache = KVCache(groups, page_size=page, capacities={"full": 64}, device=gpu, bits=bits)
+    n = 260
+    table = np.array([cache.pools["full"].allocate(reserved=False)
+                      for _ in range((n + page - 1) // page)])
+    gen = torch.Generator(device=gpu).manual_seed(9)
+    q = torch.randn((n, hq, d), generator=gen, device=gpu).half()
+    k = torch.randn((n, hkv, d), generator=gen, device=gpu).half()
+    v = torch.randn((n, hkv, d), generator=gen, device=gpu).half()
+    embeddings = torch.randn((64, 32), generator=gen, device=gpu)
+    batch = PrefillBatch(cache, torch.zeros(n, device=gpu), start=0, tables={"full": table},
+                         images=[(70, embeddings)])
+    x = torch.zeros((n, 32), device=gpu)
+    assert torch.equal(batch.inject(x)[70:134], embeddings) and not x[:70].any()
+    got = batch.attend(0, q, k, v, scale=d ** -0.5).view(n, hq, d).float().cpu().numpy()
+    keys, values = pages_to_rows(cache.keys[0]), pages_to_rows(cache.values[0])
+    kn, vn = keys.cpu().numpy(), values.cpu().numpy()
+    if bits == 8:
+        ks = cache.key_scales[0].permute(0, 2, 1).reshape(-1, hkv).cpu().numpy()
+        vs = cache.value_scales[0].permute(0, 2, 1).reshape(-1, hkv).cpu().numpy()
+        kn, vn = kv8.gather_dequantize(kn, ks), kv8.gather_dequantize(vn, vs)
+    want = pa.paged_prefill_dense(q.cpu().numpy(), kn, vn, table, start=0, page_size=page,
+                                  scale=d ** -0.5, images=[(70, 64)])
+    err_max, err_mean = pa.error_stats(got, want)
+    print(f"PrefillBatch images {bits}-bit: max_abs={err_max:.3e} mean_abs={err_mean:.3e}")
+    assert err_max <= MAX_ABS and err_mean <= MEAN_ABS
+
+
+def test_image_span_at_every_position(gpu):
+    """Regression: a query whose only visible keys in a tile come from its
+    image span, at every slot of the score layout (spans of 2 and 5 tokens
+    at each position of two workgroup tiles, crossing every 4-key group,
+    wave and tile boundary)."""
+    c = case(gpu, hq=2, hkv=1, d=64, start=0, count=200, seed=12)
+    q, k, v, table = c["t"]
+    worst = 0.0
+    for n in (2, 5):
+        for a in range(0, 200 - n + 1):
+            got = paged_prefill_attention(q, k, v, table, start=0, page_size=16, scale=0.125,
+                                          images=[(a, n)]).float().cpu().numpy()
+            want = pa.paged_prefill_dense(c["q"], c["keys"], c["values"], c["table"], start=0,
+                                          page_size=16, scale=0.125, images=[(a, n)])
+            err = float(np.abs(got - want).max())
+            worst = max(worst, err)
+            assert err <= MAX_ABS, (a, n, err)
+    print(f"image spans at every position: worst max_abs={worst:.3e}")

@@ -90,3 +90,46 @@ def test_planted_mistakes_change_the_result():
     shifted = pa.paged_decode_dense(q[2][None], keys, values, table[None], np.array([5]),
                                     page_size=P, scale=0.5)
     assert np.abs(good[2] - shifted[0]).max() > 1e-3
+
+
+def test_image_spans_brute_force_and_invariants():
+    """Image spans (batches.py:107-118): a query inside a span also sees the
+    span's later keys, even outside the window; others stay causal."""
+    rng = np.random.default_rng(11)
+    P, hq, hkv, d = 4, 2, 1, 4
+    table = rng.permutation(8)
+    keys, values = arena(rng, 32, hkv, d)
+    start, count = 5, 14
+    q = rng.standard_normal((count, hq, d))
+    images = [(7, 4), (13, 3)]
+    out = pa.paged_prefill_dense(q, keys, values, table, start=start, page_size=P, scale=0.6,
+                                 window=3, images=images)
+    for t in range(count):
+        p = start + t
+        seen = [k for k in range(p + 1) if k > p - 3]
+        for at, n in images:
+            if at <= p < at + n:
+                seen = sorted(set(seen) | set(range(at, at + n)))
+        for h in range(hq):
+            scores = [0.6 * sum(q[t, h, i] * keys[table[k // P] * P + k % P, 0, i]
+                                for i in range(d)) for k in seen]
+            top = max(scores)
+            wts = [math.exp(x - top) for x in scores]
+            acc = [sum(wk * values[table[k // P] * P + k % P, 0, i] for wk, k in zip(wts, seen))
+                   for i in range(d)]
+            np.testing.assert_allclose(out[t, h], np.array(acc) / sum(wts), rtol=1e-10)
+    # A one-token image changes nothing; queries outside every image are causal.
+    plain = pa.paged_prefill_dense(q, keys, values, table, start=start, page_size=P, scale=0.6,
+                                   window=3)
+    one = pa.paged_prefill_dense(q, keys, values, table, start=start, page_size=P, scale=0.6,
+                                 window=3, images=[(9, 1)])
+    np.testing.assert_allclose(one, plain, rtol=1e-12)
+    outside = [t for t in range(count)
+               if not any(at <= start + t < at + n for at, n in images)]
+    np.testing.assert_allclose(out[outside], plain[outside], rtol=1e-12)
+    # Identical queries inside one span see the same keys: identical outputs.
+    q2 = q.copy()
+    q2[2:6] = q2[2]
+    out2 = pa.paged_prefill_dense(q2, keys, values, table, start=start, page_size=P, scale=0.6,
+                                  images=[(7, 4)])
+    np.testing.assert_allclose(out2[3:6], np.broadcast_to(out2[2], out2[3:6].shape), rtol=1e-12)
