@@ -147,6 +147,40 @@ int pda_decode_merge(const void* queries, const void* keys, const void* values,
                      int32_t split_pages,
                      void* workspace, size_t workspace_bytes, void* stream);
 
+/* bf16: the same calls with queries, K/V arenas and output in bf16, the
+ * model dtype of the reference's bf16 models (their KVCache holds the model
+ * dtype, paged_kv.py:156-292; the Metal kernel is templated on it,
+ * metal_kernels.py:196-206). q.k and p.v run on bf16 v_dot2 (products exact,
+ * fp32 accumulation); the probabilities are rounded to bf16 for p.v (and
+ * the sum uses the same values). Same workspace sizing and plan. */
+int pda_paged_decode_attention_bf16(const void* queries, const void* keys,
+                                    const void* values, const int32_t* tables,
+                                    const int32_t* lengths, void* out,
+                                    int32_t batch, int32_t q_heads,
+                                    int32_t kv_heads, int32_t head_dim,
+                                    int32_t page_size, int32_t table_stride,
+                                    int64_t arena_rows, int32_t layout,
+                                    int32_t longest, float scale,
+                                    int32_t window, float softcap,
+                                    int32_t split_pages, void* workspace,
+                                    size_t workspace_bytes, void* stream);
+int pda_decode_split_bf16(const void* queries, const void* keys, const void* values,
+                          const int32_t* tables, const int32_t* lengths, void* out,
+                          int32_t batch, int32_t q_heads, int32_t kv_heads,
+                          int32_t head_dim, int32_t page_size, int32_t table_stride,
+                          int64_t arena_rows, int32_t layout, int32_t longest,
+                          float scale, int32_t window, float softcap,
+                          int32_t split_pages,
+                          void* workspace, size_t workspace_bytes, void* stream);
+int pda_decode_merge_bf16(const void* queries, const void* keys, const void* values,
+                          const int32_t* tables, const int32_t* lengths, void* out,
+                          int32_t batch, int32_t q_heads, int32_t kv_heads,
+                          int32_t head_dim, int32_t page_size, int32_t table_stride,
+                          int64_t arena_rows, int32_t layout, int32_t longest,
+                          float scale, int32_t window, float softcap,
+                          int32_t split_pages,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
 /* 8-bit K/V: pda_paged_decode_attention over int8 arenas with one fp16 scale
  * per (row, kv head) of keys and of values. Replaces the reference's
  * quantized path, paged_decode_attention(..., scales=(key_scales,

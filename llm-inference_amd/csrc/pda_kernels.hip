@@ -89,6 +89,9 @@ namespace {
 typedef _Float16 f16;
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16;
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 constexpr float kLog2e = 1.44269504088896340736f;
@@ -235,6 +238,13 @@ __device__ __forceinline__ float dot2_first(f16x2 a, f16x2 b) {
   return d;
 }
 
+// bf16 counterpart of dot2_first.
+__device__ __forceinline__ float dot2_first_bf16(bf16x2 a, bf16x2 b) {
+  float d;
+  asm("v_dot2_f32_bf16 %0, %1, %2, 0" : "=v"(d) : "v"(a), "v"(b));
+  return d;
+}
+
 __device__ __forceinline__ float wave_max(float x) {
   x = fmaxf(x, dpp<0xB1>(x));
   x = fmaxf(x, dpp<0x4E>(x));
@@ -355,9 +365,14 @@ __device__ void build_prefix(const Params& p, int* s_prefix, int* s_len) {
 // Split kernel: a persistent grid of wave pairs (see the file comment).
 // At least two waves per SIMD (<= 256 registers): with G = 7 or 8 heads the
 // few values that do not fit live outside the main loop.
-template <int D, int G, bool Q8>
+// BF: queries, K/V and output in bf16 (the model dtype of the reference's
+// bf16 models; their arenas hold the model dtype, paged_kv.py:156-292). The
+// 16-bit buffers are addressed as fp16 storage and reinterpreted: q.k and
+// p.v run on bf16 v_dot2, the probabilities are rounded to bf16 for p.v.
+template <int D, int G, bool Q8, bool BF>
 __global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void paged_decode_kernel(const Params p) {
+  static_assert(!(Q8 && BF), "8-bit K/V is dequantized to fp16");
   using Gm = Geom<D, Q8>;
   constexpr int EPL = Gm::EPL, NV = Gm::NV, DC = Gm::DC, R = Gm::R, KPS = Gm::KPS;
   constexpr bool PV2 = Gm::PV2;
@@ -461,7 +476,8 @@ void paged_decode_kernel(const Params p) {
     const int h0 = kvh * p.gtot + (kvg - kvh * p.nhg) * G;
     const int32_t* const table = p.tables + (int64_t)b * p.table_stride + first_page;
 
-    // Queries of the G heads, this lane's slice, as fp16 pairs for v_dot2.
+    // Queries of the G heads, this lane's slice, as fp16 pairs for v_dot2
+    // (bf16: the same bits, read as bf16 pairs where used).
     f16x2 q[G][EPL / 2];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
@@ -638,9 +654,19 @@ void paged_decode_kernel(const Params p) {
       float s[G];
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        float acc = dot2_first(q[g][0], kp2[0]);
+        float acc;
+        if constexpr (BF) {
+          acc = dot2_first_bf16(__builtin_bit_cast(bf16x2, q[g][0]),
+                                __builtin_bit_cast(bf16x2, kp2[0]));
 #pragma unroll
-        for (int i = 1; i < EPL / 2; ++i) acc = __builtin_amdgcn_fdot2(q[g][i], kp2[i], acc, false);
+          for (int i = 1; i < EPL / 2; ++i)
+            acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, q[g][i]),
+                                                  __builtin_bit_cast(bf16x2, kp2[i]), acc, false);
+        } else {
+          acc = dot2_first(q[g][0], kp2[0]);
+#pragma unroll
+          for (int i = 1; i < EPL / 2; ++i) acc = __builtin_amdgcn_fdot2(q[g][i], kp2[i], acc, false);
+        }
         s[g] = acc;
       }
 #pragma unroll
@@ -767,10 +793,19 @@ void paged_decode_kernel(const Params p) {
           // values, so the weights stay a normalised combination.
           const float pr = __builtin_amdgcn_exp2f(x[g]);
           const float other = pair_swap<R>(pr);
-          const f16x2 pp = f16x2{(f16)pr, (f16)other};
-          l[g] = __builtin_amdgcn_fdot2(pp, f16x2{(f16)1.0f, (f16)1.0f}, l[g], false);
+          if constexpr (BF) {
+            const bf16x2 pp = bf16x2{(bf16)pr, (bf16)other};
+            l[g] = __builtin_amdgcn_fdot2_f32_bf16(pp, bf16x2{(bf16)1.0f, (bf16)1.0f}, l[g], false);
 #pragma unroll
-          for (int i = 0; i < 8; ++i) o[g][i] = __builtin_amdgcn_fdot2(pp, vv[i], o[g][i], false);
+            for (int i = 0; i < 8; ++i)
+              o[g][i] = __builtin_amdgcn_fdot2_f32_bf16(pp, __builtin_bit_cast(bf16x2, vv[i]),
+                                                        o[g][i], false);
+          } else {
+            const f16x2 pp = f16x2{(f16)pr, (f16)other};
+            l[g] = __builtin_amdgcn_fdot2(pp, f16x2{(f16)1.0f, (f16)1.0f}, l[g], false);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) o[g][i] = __builtin_amdgcn_fdot2(pp, vv[i], o[g][i], false);
+          }
         }
       } else {
 #pragma unroll
@@ -781,7 +816,9 @@ void paged_decode_kernel(const Params p) {
           for (int v = 0; v < NV; ++v) {
 #pragma unroll
             for (int i = 0; i < 8; ++i)
-              o[g][8 * v + i] = __builtin_fmaf(pr, (float)vd[v][i], o[g][8 * v + i]);
+              o[g][8 * v + i] = __builtin_fmaf(
+                  pr, BF ? (float)__builtin_bit_cast(bf16x8, vd[v])[i] : (float)vd[v][i],
+                  o[g][8 * v + i]);
           }
         }
       }
@@ -834,10 +871,17 @@ void paged_decode_kernel(const Params p) {
         f16* dst = p.out + ((int64_t)b * p.hq + h0 + g) * D + e0;
 #pragma unroll
         for (int v = 0; v < OPL / 8; ++v) {
-          f16x8 y;
+          if constexpr (BF) {
+            bf16x8 y;
 #pragma unroll
-          for (int i = 0; i < 8; ++i) y[i] = (f16)(o[g][8 * v + i] * inv);
-          *reinterpret_cast<f16x8*>(dst + estride * v) = y;
+            for (int i = 0; i < 8; ++i) y[i] = (bf16)(o[g][8 * v + i] * inv);
+            *reinterpret_cast<bf16x8*>(dst + estride * v) = y;
+          } else {
+            f16x8 y;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) y[i] = (f16)(o[g][8 * v + i] * inv);
+            *reinterpret_cast<f16x8*>(dst + estride * v) = y;
+          }
         }
       }
     } else {
@@ -902,7 +946,7 @@ void paged_decode_kernel(const Params p) {
 // hold no visible key and weigh 0; a zero total gives 0, :116,122). Batches
 // and waves are folded in a fixed order, so the result does not depend on
 // timing.
-template <int D, int G>
+template <int D, int G, bool BF>
 __global__ __launch_bounds__(kMergeMaxWaves * 64) void paged_decode_merge_kernel(const Params p) {
   constexpr int kChunks = (D + 63) / 64;  // elements l, l + 64, ... of lane l
   constexpr int kBatch = 32 / kChunks;    // candidates whose loads go out together
@@ -1008,7 +1052,12 @@ __global__ __launch_bounds__(kMergeMaxWaves * 64) void paged_decode_merge_kernel
   const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
 #pragma unroll
   for (int c = 0; c < kChunks; ++c)
-    if (c * 64 + lane < D) dst[c * 64 + lane] = (f16)(acc[c] * inv);
+    if (c * 64 + lane < D) {
+      if constexpr (BF)
+        dst[c * 64 + lane] = __builtin_bit_cast(f16, (bf16)(acc[c] * inv));
+      else
+        dst[c * 64 + lane] = (f16)(acc[c] * inv);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1024,29 +1073,40 @@ struct KernelPair {
   KernelFn merge = nullptr;
 };
 
-template <int D, int G, bool Q8>
+template <int D, int G, bool Q8, bool BF>
 KernelPair pair() {
-  return {paged_decode_kernel<D, G, Q8>, paged_decode_merge_kernel<D, G>};
+  return {paged_decode_kernel<D, G, Q8, BF>, paged_decode_merge_kernel<D, G, BF>};
 }
 
-template <int D, bool Q8>
+template <int D, bool Q8, bool BF = false>
 KernelPair kernels_for_g(int g) {
   switch (g) {
-    case 1: return pair<D, 1, Q8>();
-    case 2: return pair<D, 2, Q8>();
-    case 3: return pair<D, 3, Q8>();
-    case 4: return pair<D, 4, Q8>();
-    case 5: return pair<D, 5, Q8>();
-    case 6: return pair<D, 6, Q8>();
-    case 7: return pair<D, 7, Q8>();
-    case 8: return pair<D, 8, Q8>();
+    case 1: return pair<D, 1, Q8, BF>();
+    case 2: return pair<D, 2, Q8, BF>();
+    case 3: return pair<D, 3, Q8, BF>();
+    case 4: return pair<D, 4, Q8, BF>();
+    case 5: return pair<D, 5, Q8, BF>();
+    case 6: return pair<D, 6, Q8, BF>();
+    case 7: return pair<D, 7, Q8, BF>();
+    case 8: return pair<D, 8, Q8, BF>();
   }
   return {};
 }
 
-// Compiled head dims: fp16 K/V 64, 80, 96, 128, 256, 512; 8-bit K/V the
-// dims whose p.v runs on key pairs (64, 128, 256, 512).
-KernelPair kernels_for(int d, int g, bool q8) {
+// Compiled head dims: fp16 and bf16 K/V 64, 80, 96, 128, 256, 512; 8-bit K/V
+// the dims whose p.v runs on key pairs (64, 128, 256, 512).
+KernelPair kernels_for(int d, int g, bool q8, bool bf16 = false) {
+  if (bf16) {
+    switch (d) {
+      case 64: return kernels_for_g<64, false, true>(g);
+      case 80: return kernels_for_g<80, false, true>(g);
+      case 96: return kernels_for_g<96, false, true>(g);
+      case 128: return kernels_for_g<128, false, true>(g);
+      case 256: return kernels_for_g<256, false, true>(g);
+      case 512: return kernels_for_g<512, false, true>(g);
+    }
+    return {};
+  }
   if (q8) {
     switch (d) {
       case 64: return kernels_for_g<64, true>(g);
@@ -1239,9 +1299,10 @@ constexpr int kPassSplit = 1;
 constexpr int kPassMerge = 2;
 
 // Validates, plans and launches the split pass, the merge pass or both.
-// key_scales / value_scales non-null: 8-bit K/V (int8 arenas).
+// key_scales / value_scales non-null: 8-bit K/V (int8 arenas); bf16: q, K/V
+// and out in bf16 instead of fp16.
 int decode(int passes, const void* queries, const void* keys, const void* values,
-           const void* key_scales, const void* value_scales,
+           const void* key_scales, const void* value_scales, bool bf16,
            const int32_t* tables, const int32_t* lengths, void* out, int32_t batch,
            int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t page_size,
            int32_t table_stride, int64_t arena_rows, int32_t layout, int32_t longest,
@@ -1281,7 +1342,7 @@ int decode(int passes, const void* queries, const void* keys, const void* values
   if ((uintptr_t)workspace & 255)
     return fail(PDA_ERR_ALIGNMENT, "workspace must be 256-byte aligned");
 
-  const KernelPair kp = kernels_for(head_dim, pl.G, q8);
+  const KernelPair kp = kernels_for(head_dim, pl.G, q8, bf16);
   const size_t lds = (size_t)(2 * batch + 1) * sizeof(int32_t);
   const int groups = resident_groups(kp.split, lds);
   if (groups < 0) return fail(PDA_ERR_HIP, "device query failed");
@@ -1357,8 +1418,8 @@ extern "C" {
       int32_t longest, float scale, int32_t window, float softcap,             \
       int32_t split_pages, void *workspace, size_t workspace_bytes,            \
       void *stream
-#define PDA_DECODE_ARGS                                                        \
-  queries, keys, values, nullptr, nullptr, tables, lengths, out, batch,        \
+#define PDA_DECODE_ARGS(BF16)                                                  \
+  queries, keys, values, nullptr, nullptr, BF16, tables, lengths, out, batch,  \
       q_heads, kv_heads, head_dim, page_size, table_stride, arena_rows,        \
       layout, longest, scale, window, softcap, split_pages, workspace,         \
       workspace_bytes, stream
@@ -1372,18 +1433,26 @@ extern "C" {
       int32_t split_pages, void *workspace, size_t workspace_bytes,            \
       void *stream
 #define PDA_DECODE_ARGS_Q8                                                     \
-  queries, keys, values, key_scales, value_scales, tables, lengths, out,       \
+  queries, keys, values, key_scales, value_scales, false, tables, lengths, out,\
       batch, q_heads, kv_heads, head_dim, page_size, table_stride, arena_rows, \
       layout, longest, scale, window, softcap, split_pages, workspace,         \
       workspace_bytes, stream
 
 int pda_paged_decode_attention(PDA_DECODE_PARAMS) {
-  return decode(kPassSplit | kPassMerge, PDA_DECODE_ARGS);
+  return decode(kPassSplit | kPassMerge, PDA_DECODE_ARGS(false));
 }
 
-int pda_decode_split(PDA_DECODE_PARAMS) { return decode(kPassSplit, PDA_DECODE_ARGS); }
+int pda_decode_split(PDA_DECODE_PARAMS) { return decode(kPassSplit, PDA_DECODE_ARGS(false)); }
 
-int pda_decode_merge(PDA_DECODE_PARAMS) { return decode(kPassMerge, PDA_DECODE_ARGS); }
+int pda_decode_merge(PDA_DECODE_PARAMS) { return decode(kPassMerge, PDA_DECODE_ARGS(false)); }
+
+int pda_paged_decode_attention_bf16(PDA_DECODE_PARAMS) {
+  return decode(kPassSplit | kPassMerge, PDA_DECODE_ARGS(true));
+}
+
+int pda_decode_split_bf16(PDA_DECODE_PARAMS) { return decode(kPassSplit, PDA_DECODE_ARGS(true)); }
+
+int pda_decode_merge_bf16(PDA_DECODE_PARAMS) { return decode(kPassMerge, PDA_DECODE_ARGS(true)); }
 
 int pda_paged_decode_attention_q8(PDA_DECODE_PARAMS_Q8) {
   if (!key_scales || !value_scales)

@@ -95,8 +95,12 @@ def paged_decode_attention(
                          "[pages, kv_heads, page_size, head_dim]")
     if q_heads % kv_heads:
         raise ValueError("query heads must be a multiple of kv heads")
-    kv_dtype = torch.int8 if q8 else torch.float16
-    for name, t, dtype in (("queries", queries, torch.float16), ("keys", keys, kv_dtype),
+    # bf16 queries select bf16 K/V and output (the model dtype of bf16
+    # models); 8-bit K/V take fp16 queries.
+    bf16 = queries.dtype == torch.bfloat16 and not q8
+    q_dtype = torch.bfloat16 if bf16 else torch.float16
+    kv_dtype = torch.int8 if q8 else q_dtype
+    for name, t, dtype in (("queries", queries, q_dtype), ("keys", keys, kv_dtype),
                            ("values", values, kv_dtype)):
         if t.dtype != dtype:
             raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
@@ -130,8 +134,10 @@ def paged_decode_attention(
                                 int(longest), int(window), int(split_pages))
     ws = workspace(device, need)
     stream = torch.cuda.current_stream(device).cuda_stream
+    if out.dtype != q_dtype or tuple(out.shape) != tuple(queries.shape) or not out.is_cuda:
+        raise ValueError("out must match the queries' shape and dtype")
     entry = {"both": "pda_paged_decode_attention", "split": "pda_decode_split",
-             "merge": "pda_decode_merge"}[passes] + ("_q8" if q8 else "")
+             "merge": "pda_decode_merge"}[passes] + ("_q8" if q8 else "_bf16" if bf16 else "")
     extra = (scales[0].data_ptr(), scales[1].data_ptr()) if q8 else ()
     rc = getattr(_lib.library(), entry)(
         queries.data_ptr(), keys.data_ptr(), values.data_ptr(), *extra, tables.data_ptr(),
