@@ -260,6 +260,18 @@ int pda_rope_append(const void* q, void* q_out, const void* k, const void* v,
                     int64_t arena_rows, int32_t layout, int32_t rope_dims,
                     const float* inv_freq, void* stream);
 
+/* bf16 models: pda_rope_append with q, q_out, k, v and both arenas in bf16.
+ * The rotation runs in float32 as in pda_rope_append and is rounded to bf16 to
+ * nearest even, the reference's `.astype(x.dtype)` for a bf16 model
+ * (portable.py:130-132); values are copied unchanged. Arguments as
+ * pda_rope_append. */
+int pda_rope_append_bf16(const void* q, void* q_out, const void* k, const void* v,
+                         void* k_arena, void* v_arena, const int32_t* positions,
+                         const int32_t* rows, int32_t n, int32_t q_heads,
+                         int32_t kv_heads, int32_t head_dim, int32_t page_size,
+                         int64_t arena_rows, int32_t layout, int32_t rope_dims,
+                         const float* inv_freq, void* stream);
+
 /* 8-bit K/V: pda_rope_append into int8 arenas. The rotated keys (rounded to
  * fp16 as the fp16 call writes them) and the values are quantized per (row,
  * kv head) as the reference's KVCache.write does for bits=8
@@ -343,6 +355,22 @@ int pda_paged_prefill_attention(const void* queries, const void* keys,
                                 const int32_t* images, int32_t num_images,
                                 int32_t splits, void* workspace,
                                 size_t workspace_bytes, void* stream);
+
+/* bf16 models: pda_paged_prefill_attention with queries, K/V arenas and
+ * output in bf16 (KVCache(dtype=bfloat16), paged_kv.py:156-166). Scores and
+ * the output accumulate in float32 on the bf16 matrix cores; the
+ * probabilities that weight V are rounded to bf16 and the output to bf16 to
+ * nearest even. Arguments and workspace as pda_paged_prefill_attention. */
+int pda_paged_prefill_attention_bf16(const void* queries, const void* keys,
+                                     const void* values, const int32_t* table,
+                                     int32_t table_len, int32_t start, int32_t count,
+                                     void* out, int32_t q_heads, int32_t kv_heads,
+                                     int32_t head_dim, int32_t page_size,
+                                     int64_t arena_rows, int32_t layout, float scale,
+                                     int32_t window, float softcap,
+                                     const int32_t* images, int32_t num_images,
+                                     int32_t splits, void* workspace,
+                                     size_t workspace_bytes, void* stream);
 
 /* Paged prefill attention over an 8-bit K/V cache. Replaces
  * PrefillBatch.attend's attention with KVCache(bits=8) (batches.py:84-132,

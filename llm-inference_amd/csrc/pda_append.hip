@@ -31,6 +31,7 @@
 namespace {
 
 typedef _Float16 f16;
+typedef __bf16 bf16;
 
 constexpr int kHeadsPerGroup = 4;  // heads of one token per workgroup, one wave each
 constexpr int kAppendThreads = 64 * kHeadsPerGroup;
@@ -79,7 +80,11 @@ __device__ __forceinline__ int64_t arena_index(const AppendParams& p, int64_t ro
 // 2 * half on are copied. Lane `lane` of the head's wave takes j = lane,
 // lane + 64, ...; the source elements are loaded before the angles are
 // computed, so their latency overlaps the position and frequency loads.
-__device__ __forceinline__ void rotate_head(const f16* src, f16* dst, float pos,
+// E: the element type of q, k and the arena (fp16, or bf16 for bf16 models);
+// the rotation runs in float32 and rounds once to E (portable.py:130-132,
+// `.astype(x.dtype)`).
+template <typename E>
+__device__ __forceinline__ void rotate_head(const E* src, E* dst, float pos,
                                             const float* inv_freq, int half, int d,
                                             int lane) {
   for (int j = lane; j < half; j += 64) {
@@ -87,8 +92,8 @@ __device__ __forceinline__ void rotate_head(const f16* src, f16* dst, float pos,
     const float x2 = (float)src[j + half];
     float s, c;
     sincosf(__fmul_rn(pos, inv_freq[j]), &s, &c);
-    dst[j] = (f16)__fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, s));
-    dst[j + half] = (f16)__fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, s));
+    dst[j] = (E)__fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, s));
+    dst[j + half] = (E)__fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, s));
   }
   for (int e = 2 * half + lane; e < d; e += 64) dst[e] = src[e];
 }
@@ -96,6 +101,7 @@ __device__ __forceinline__ void rotate_head(const f16* src, f16* dst, float pos,
 // One wave per head: workgroup (t, y) takes heads 4y .. 4y + 3 of token t,
 // query heads first, then kv heads. No LDS and no barrier: every wave
 // computes the angles it uses (sincosf with full range reduction).
+template <typename E>
 __global__ __launch_bounds__(kAppendThreads) void rope_append_kernel(const AppendParams p) {
   const int t = blockIdx.x;
   const int lane = threadIdx.x & 63;
@@ -104,17 +110,20 @@ __global__ __launch_bounds__(kAppendThreads) void rope_append_kernel(const Appen
   const float pos = p.half > 0 ? (float)p.positions[t] : 0.0f;
   if (h < p.hq) {
     const int64_t base = ((int64_t)t * p.hq + h) * p.d;
-    rotate_head(p.q + base, p.q_out + base, pos, p.inv_freq, p.half, p.d, lane);
+    rotate_head(reinterpret_cast<const E*>(p.q) + base, reinterpret_cast<E*>(p.q_out) + base,
+                pos, p.inv_freq, p.half, p.d, lane);
     return;
   }
   const int64_t row = p.rows[t];
   if (row < 0 || row >= p.arena_rows) return;  // rows outside the arena are skipped
   const int kh = h - p.hq;
   const int64_t base = ((int64_t)t * p.hkv + kh) * p.d;
-  rotate_head(p.k + base, static_cast<f16*>(p.k_arena) + arena_index(p, row, kh, 0), pos,
-              p.inv_freq, p.half, p.d, lane);
-  f16* const vdst = static_cast<f16*>(p.v_arena) + arena_index(p, row, kh, 0);
-  for (int e = lane; e < p.d; e += 64) vdst[e] = p.v[base + e];
+  rotate_head(reinterpret_cast<const E*>(p.k) + base,
+              static_cast<E*>(p.k_arena) + arena_index(p, row, kh, 0), pos, p.inv_freq,
+              p.half, p.d, lane);
+  E* const vdst = static_cast<E*>(p.v_arena) + arena_index(p, row, kh, 0);
+  const E* const vsrc = reinterpret_cast<const E*>(p.v) + base;
+  for (int e = lane; e < p.d; e += 64) vdst[e] = vsrc[e];
 }
 
 constexpr int kMaxPerLane = kMaxHeadDim / 64;  // elements of a row per lane
@@ -191,7 +200,7 @@ using pda_internal::fail;
 using pda_internal::ok;
 
 int rope_append(const void* q, void* q_out, const void* k, const void* v, void* k_arena,
-                void* v_arena, void* k_scale, void* v_scale, bool q8,
+                void* v_arena, void* k_scale, void* v_scale, bool q8, bool bf16_elems,
                 const int32_t* positions, const int32_t* rows, int32_t n, int32_t q_heads,
                 int32_t kv_heads, int32_t head_dim, int32_t page_size, int64_t arena_rows,
                 int32_t layout, int32_t rope_dims, const float* inv_freq, void* stream) {
@@ -253,8 +262,9 @@ int rope_append(const void* q, void* q_out, const void* k, const void* v, void* 
   prm.layout = layout;
   void* args[] = {&prm};
   const dim3 grid(n, (hq + hkv + kHeadsPerGroup - 1) / kHeadsPerGroup);
-  const void* fn = q8 ? reinterpret_cast<const void*>(rope_append_q8_kernel)
-                     : reinterpret_cast<const void*>(rope_append_kernel);
+  const void* fn = q8     ? reinterpret_cast<const void*>(rope_append_q8_kernel)
+                   : bf16_elems ? reinterpret_cast<const void*>(rope_append_kernel<bf16>)
+                          : reinterpret_cast<const void*>(rope_append_kernel<f16>);
   const hipError_t err = hipLaunchKernel(fn, grid, dim3(kAppendThreads), args, 0,
                                          static_cast<hipStream_t>(stream));
   if (err != hipSuccess)
@@ -272,9 +282,20 @@ int pda_rope_append(const void* q, void* q_out, const void* k, const void* v,
                     int32_t head_dim, int32_t page_size, int64_t arena_rows,
                     int32_t layout, int32_t rope_dims, const float* inv_freq,
                     void* stream) {
-  return rope_append(q, q_out, k, v, k_arena, v_arena, nullptr, nullptr, false, positions,
-                     rows, n, q_heads, kv_heads, head_dim, page_size, arena_rows, layout,
-                     rope_dims, inv_freq, stream);
+  return rope_append(q, q_out, k, v, k_arena, v_arena, nullptr, nullptr, false, false,
+                     positions, rows, n, q_heads, kv_heads, head_dim, page_size, arena_rows,
+                     layout, rope_dims, inv_freq, stream);
+}
+
+int pda_rope_append_bf16(const void* q, void* q_out, const void* k, const void* v,
+                         void* k_arena, void* v_arena, const int32_t* positions,
+                         const int32_t* rows, int32_t n, int32_t q_heads, int32_t kv_heads,
+                         int32_t head_dim, int32_t page_size, int64_t arena_rows,
+                         int32_t layout, int32_t rope_dims, const float* inv_freq,
+                         void* stream) {
+  return rope_append(q, q_out, k, v, k_arena, v_arena, nullptr, nullptr, false, true,
+                     positions, rows, n, q_heads, kv_heads, head_dim, page_size, arena_rows,
+                     layout, rope_dims, inv_freq, stream);
 }
 
 int pda_rope_append_q8(const void* q, void* q_out, const void* k, const void* v,
@@ -283,7 +304,7 @@ int pda_rope_append_q8(const void* q, void* q_out, const void* k, const void* v,
                        int32_t q_heads, int32_t kv_heads, int32_t head_dim,
                        int32_t page_size, int64_t arena_rows, int32_t layout,
                        int32_t rope_dims, const float* inv_freq, void* stream) {
-  return rope_append(q, q_out, k, v, k_arena, v_arena, key_scales, value_scales, true,
+  return rope_append(q, q_out, k, v, k_arena, v_arena, key_scales, value_scales, true, false,
                      positions, rows, n, q_heads, kv_heads, head_dim, page_size, arena_rows,
                      layout, rope_dims, inv_freq, stream);
 }

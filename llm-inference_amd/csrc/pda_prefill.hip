@@ -54,6 +54,9 @@ typedef _Float16 f16;
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16;
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
@@ -106,6 +109,26 @@ __device__ __forceinline__ f16x4 read_tr(const f16* p) {
   return __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p));
 }
 
+// One 32x32x16 matrix-core step on 16-bit operands held as fp16 bit patterns:
+// fp16, or bf16 (BF) for bf16 models.
+template <bool BF>
+__device__ __forceinline__ f32x16 mfma16(const f16x8& a, const f16x8& b, const f32x16& c) {
+  if constexpr (BF)
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// f32 -> the 16-bit element type (to nearest even), as an fp16 bit pattern.
+template <bool BF>
+__device__ __forceinline__ f16 round16(float x) {
+  if constexpr (BF)
+    return __builtin_bit_cast(f16, (bf16)x);
+  else
+    return (f16)x;
+}
+
 // Keys per tile: 64 (two 32-key blocks) where the registers allow it.
 template <int D>
 constexpr int blocks_per_tile() { return D <= 128 ? 2 : 1; }
@@ -114,8 +137,12 @@ constexpr int blocks_per_tile() { return D <= 128 ? 2 : 1; }
 // row to fp16(int8 x scale) on its way into LDS, the values the reference's
 // 8-bit gather hands to attention (paged_kv.py:285-292), and the rest of the
 // kernel is the fp16 one.
-template <int D, bool Q8>
+// BF: queries, K/V and output in bf16 (bf16 models); every 16-bit value is
+// moved as raw bits and only the matrix-core steps, the probabilities and the
+// output rounding differ.
+template <int D, bool Q8, bool BF>
 __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillParams p) {
+  static_assert(!(Q8 && BF), "8-bit K/V dequantizes to fp16");
   constexpr int KB = blocks_per_tile<D>();  // 32-key blocks per tile
   constexpr int kKeys = 32 * KB;            // keys per tile
   constexpr int kKRow = D + 8;    // K row in LDS (halves): 16-lane 16-byte reads hit distinct banks
@@ -349,7 +376,7 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
         s[kb] = f32x16{};
 #pragma unroll
         for (int c = 0; c < D / 16; ++c)
-          s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[c], qf[c], s[kb], 0, 0, 0);
+          s[kb] = mfma16<BF>(ka[c], qf[c], s[kb]);
       }
       const okword okm = *reinterpret_cast<const okword*>(s_ok[buf]);
       const bool edge = k0 + kKeys - 1 > wfirst || okm != (okword)~(okword)0 ||
@@ -414,11 +441,20 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
       for (int ks = 0; ks < 2 * KB; ++ks) {
 #pragma unroll
         for (int t2 = 0; t2 < 4; ++t2) {
-          const f16x2 ph = {(f16)__builtin_amdgcn_exp2f(fmaf(x[8 * ks + 2 * t2], c, -mu)),
-                            (f16)__builtin_amdgcn_exp2f(fmaf(x[8 * ks + 2 * t2 + 1], c, -mu))};
-          l = __builtin_amdgcn_fdot2(ph, f16x2{(f16)1.0f, (f16)1.0f}, l, false);
-          pb[ks][2 * t2] = ph[0];
-          pb[ks][2 * t2 + 1] = ph[1];
+          if constexpr (BF) {
+            const bf16x2 pp = {(bf16)__builtin_amdgcn_exp2f(fmaf(x[8 * ks + 2 * t2], c, -mu)),
+                               (bf16)__builtin_amdgcn_exp2f(fmaf(x[8 * ks + 2 * t2 + 1], c, -mu))};
+            l = __builtin_amdgcn_fdot2_f32_bf16(pp, bf16x2{(bf16)1.0f, (bf16)1.0f}, l, false);
+            const f16x2 ph = __builtin_bit_cast(f16x2, pp);
+            pb[ks][2 * t2] = ph[0];
+            pb[ks][2 * t2 + 1] = ph[1];
+          } else {
+            const f16x2 ph = {(f16)__builtin_amdgcn_exp2f(fmaf(x[8 * ks + 2 * t2], c, -mu)),
+                              (f16)__builtin_amdgcn_exp2f(fmaf(x[8 * ks + 2 * t2 + 1], c, -mu))};
+            l = __builtin_amdgcn_fdot2(ph, f16x2{(f16)1.0f, (f16)1.0f}, l, false);
+            pb[ks][2 * t2] = ph[0];
+            pb[ks][2 * t2 + 1] = ph[1];
+          }
         }
       }
       // O^T += V^T P^T. A operand of step ks for rows 32 b ..: keys
@@ -431,7 +467,7 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
           const f16x4 lo4 = read_tr(vp);
           const f16x4 hi4 = read_tr(vp + 8 * kVRow);
           const f16x8 a = {lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
-          o[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[ks], o[b], 0, 0, 0);
+          o[b] = mfma16<BF>(a, pb[ks], o[b]);
         }
       }
     }
@@ -464,7 +500,7 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
     for (int g = 0; g < 4; ++g) {
       f16x4 y;
 #pragma unroll
-      for (int t = 0; t < 4; ++t) y[t] = (f16)(o[b][4 * g + t] * inv);
+      for (int t = 0; t < 4; ++t) y[t] = round16<BF>(o[b][4 * g + t] * inv);
       *reinterpret_cast<f16x4*>(dst + 32 * b + 8 * g + 4 * hh) = y;
     }
   }
@@ -475,7 +511,7 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
 // sum_s w_s o_s / sum_s w_s l_s (0 when nothing was visible). The same LSE
 // merge as the reference's decode merge (metal_kernels.py:103-124), in the
 // log2 domain. One thread per 4 dims, D / 4 threads per (query, head).
-template <int D>
+template <int D, bool BF>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restrict__ part_o,
                                                             const float2* __restrict__ part_ml,
                                                             f16* __restrict__ out, int64_t pairs,
@@ -502,7 +538,8 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restr
     }
   }
   const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
-  f16x4 y = {(f16)(acc.x * inv), (f16)(acc.y * inv), (f16)(acc.z * inv), (f16)(acc.w * inv)};
+  f16x4 y = {round16<BF>(acc.x * inv), round16<BF>(acc.y * inv), round16<BF>(acc.z * inv),
+             round16<BF>(acc.w * inv)};
   *reinterpret_cast<f16x4*>(out + pair * D + d) = y;
 }
 
@@ -542,8 +579,23 @@ size_t prefill_workspace(int splits, int count, int q_heads, int head_dim) {
 using pda_internal::fail;
 using pda_internal::ok;
 
+template <bool Q8, bool BF>
+const void* prefill_kernel_for(int head_dim) {
+  return head_dim == 64    ? reinterpret_cast<const void*>(paged_prefill_kernel<64, Q8, BF>)
+         : head_dim == 128 ? reinterpret_cast<const void*>(paged_prefill_kernel<128, Q8, BF>)
+                           : reinterpret_cast<const void*>(paged_prefill_kernel<256, Q8, BF>);
+}
+
+template <bool BF>
+const void* merge_kernel_for(int head_dim) {
+  return head_dim == 64    ? reinterpret_cast<const void*>(prefill_merge_kernel<64, BF>)
+         : head_dim == 128 ? reinterpret_cast<const void*>(prefill_merge_kernel<128, BF>)
+                           : reinterpret_cast<const void*>(prefill_merge_kernel<256, BF>);
+}
+
 int prefill(const void* queries, const void* keys, const void* values, const void* key_scales,
-            const void* value_scales, bool q8, const int32_t* table, int32_t table_len,
+            const void* value_scales, bool q8, bool bf16_elems, const int32_t* table,
+            int32_t table_len,
             int32_t start, int32_t count, void* out, int32_t q_heads, int32_t kv_heads,
             int32_t head_dim, int32_t page_size, int64_t arena_rows, int32_t layout, float scale,
             int32_t window, float softcap, const int32_t* images, int32_t num_images,
@@ -641,13 +693,9 @@ int prefill(const void* queries, const void* keys, const void* values, const voi
   prm.cap_in = softcap > 0.0f ? 2.0f * kLog2e * scale / softcap : 0.0f;
   prm.cap_out = softcap * kLog2e;
   void* args[] = {&prm};
-  const void* fn =
-      q8 ? (head_dim == 64    ? reinterpret_cast<const void*>(paged_prefill_kernel<64, true>)
-            : head_dim == 128 ? reinterpret_cast<const void*>(paged_prefill_kernel<128, true>)
-                              : reinterpret_cast<const void*>(paged_prefill_kernel<256, true>))
-         : (head_dim == 64    ? reinterpret_cast<const void*>(paged_prefill_kernel<64, false>)
-            : head_dim == 128 ? reinterpret_cast<const void*>(paged_prefill_kernel<128, false>)
-                              : reinterpret_cast<const void*>(paged_prefill_kernel<256, false>));
+  const void* fn = q8 ? prefill_kernel_for<true, false>(head_dim)
+                  : bf16_elems ? prefill_kernel_for<false, true>(head_dim)
+                               : prefill_kernel_for<false, false>(head_dim);
   const hipStream_t hs = static_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)((int64_t)prm.tiles * q_heads * nsplit));
   hipError_t err = hipLaunchKernel(fn, grid, dim3(kThreads), args, 0, hs);
@@ -661,10 +709,8 @@ int prefill(const void* queries, const void* keys, const void* values, const voi
     f16* o16 = prm.out;
     int ns = nsplit;
     void* margs[] = {&po, &pml, &o16, (void*)&npairs, &ns};
-    const void* mfn =
-        head_dim == 64    ? reinterpret_cast<const void*>(prefill_merge_kernel<64>)
-        : head_dim == 128 ? reinterpret_cast<const void*>(prefill_merge_kernel<128>)
-                          : reinterpret_cast<const void*>(prefill_merge_kernel<256>);
+    const void* mfn = bf16_elems ? merge_kernel_for<true>(head_dim)
+                                 : merge_kernel_for<false>(head_dim);
     err = hipLaunchKernel(mfn, dim3((unsigned)((npairs + per_block - 1) / per_block)),
                           dim3(256), margs, 0, hs);
     if (err != hipSuccess)
@@ -699,9 +745,22 @@ int pda_paged_prefill_attention(const void* queries, const void* keys, const voi
                                 int32_t layout, float scale, int32_t window, float softcap,
                                 const int32_t* images, int32_t num_images, int32_t splits,
                                 void* workspace, size_t workspace_bytes, void* stream) {
-  return prefill(queries, keys, values, nullptr, nullptr, false, table, table_len, start, count,
-                 out, q_heads, kv_heads, head_dim, page_size, arena_rows, layout, scale, window,
-                 softcap, images, num_images, splits, workspace, workspace_bytes, stream);
+  return prefill(queries, keys, values, nullptr, nullptr, false, false, table, table_len, start,
+                 count, out, q_heads, kv_heads, head_dim, page_size, arena_rows, layout, scale,
+                 window, softcap, images, num_images, splits, workspace, workspace_bytes, stream);
+}
+
+int pda_paged_prefill_attention_bf16(const void* queries, const void* keys, const void* values,
+                                     const int32_t* table, int32_t table_len, int32_t start,
+                                     int32_t count, void* out, int32_t q_heads,
+                                     int32_t kv_heads, int32_t head_dim, int32_t page_size,
+                                     int64_t arena_rows, int32_t layout, float scale,
+                                     int32_t window, float softcap, const int32_t* images,
+                                     int32_t num_images, int32_t splits, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+  return prefill(queries, keys, values, nullptr, nullptr, false, true, table, table_len, start,
+                 count, out, q_heads, kv_heads, head_dim, page_size, arena_rows, layout, scale,
+                 window, softcap, images, num_images, splits, workspace, workspace_bytes, stream);
 }
 
 int pda_paged_prefill_attention_q8(const void* queries, const void* keys, const void* values,
@@ -712,9 +771,10 @@ int pda_paged_prefill_attention_q8(const void* queries, const void* keys, const 
                                    int32_t layout, float scale, int32_t window, float softcap,
                                    const int32_t* images, int32_t num_images, int32_t splits,
                                    void* workspace, size_t workspace_bytes, void* stream) {
-  return prefill(queries, keys, values, key_scales, value_scales, true, table, table_len, start,
-                 count, out, q_heads, kv_heads, head_dim, page_size, arena_rows, layout, scale,
-                 window, softcap, images, num_images, splits, workspace, workspace_bytes, stream);
+  return prefill(queries, keys, values, key_scales, value_scales, true, false, table, table_len,
+                 start, count, out, q_heads, kv_heads, head_dim, page_size, arena_rows, layout,
+                 scale, window, softcap, images, num_images, splits, workspace, workspace_bytes,
+                 stream);
 }
 
 }  // extern "C"

@@ -57,12 +57,14 @@ SIGNATURES["pda_rope_append"] = (
     ctypes.c_int,
     [c_void_p] * 8 + [c_int32] * 5 + [c_int64, c_int32, c_int32, c_void_p, c_void_p],
 )
+SIGNATURES["pda_rope_append_bf16"] = SIGNATURES["pda_rope_append"]
 _PREFILL_TAIL = [c_int64, c_int32, c_float, c_int32, c_float, c_void_p, c_int32, c_int32,
                  c_void_p, c_size_t, c_void_p]
 SIGNATURES["pda_paged_prefill_attention"] = (
     ctypes.c_int,
     [c_void_p] * 4 + [c_int32] * 3 + [c_void_p] + [c_int32] * 4 + _PREFILL_TAIL,
 )
+SIGNATURES["pda_paged_prefill_attention_bf16"] = SIGNATURES["pda_paged_prefill_attention"]
 SIGNATURES["pda_paged_prefill_attention_q8"] = (
     ctypes.c_int,
     [c_void_p] * 6 + [c_int32] * 3 + [c_void_p] + [c_int32] * 4 + _PREFILL_TAIL,

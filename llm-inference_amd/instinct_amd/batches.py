@@ -73,7 +73,7 @@ class DecodeBatch:
              freqs: Any = None) -> torch.Tensor:
         """Rotary embedding of ``[batch, heads, head_dim]`` at each
         sequence's position (batches.py:195-201, portable.py:88-132)."""
-        return rope(x.to(torch.float16).contiguous(), self.offsets, dims, base=base,
+        return rope(x.to(self.cache.compute_dtype).contiguous(), self.offsets, dims, base=base,
                     freqs=freqs)
 
     def rope_attend(self, layer: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
@@ -84,8 +84,9 @@ class DecodeBatch:
         backends/dense.py:99-102 and DecodeBatch.attend, batches.py:203-226)."""
         group = self.cache.layer_group[layer]
         cache = self.cache
-        q_rot = rope_append(q.to(torch.float16).contiguous(), k.to(torch.float16).contiguous(),
-                            v.to(torch.float16).contiguous(), cache.keys[layer],
+        dtype = cache.compute_dtype
+        q_rot = rope_append(q.to(dtype).contiguous(), k.to(dtype).contiguous(),
+                            v.to(dtype).contiguous(), cache.keys[layer],
                             cache.values[layer], self.offsets, self._write[group.name],
                             page_size=cache.page_size, dims=dims, base=base, freqs=freqs,
                             scales=cache.scales(layer))
@@ -104,7 +105,7 @@ class DecodeBatch:
                         softcap: float) -> torch.Tensor:
         group = self.cache.layer_group[layer]
         out = paged_decode_attention(
-            q.to(torch.float16).contiguous(),
+            q.to(self.cache.compute_dtype).contiguous(),
             self.cache.keys[layer],
             self.cache.values[layer],
             self._tables[group.name],
@@ -168,7 +169,7 @@ class PrefillBatch:
              freqs: Any = None) -> torch.Tensor:
         """Rotate ``[tokens, heads, head_dim]`` at the chunk's positions
         (batches.py:70-81)."""
-        return rope(x.to(torch.float16).contiguous(), self.offsets, dims, base=base,
+        return rope(x.to(self.cache.compute_dtype).contiguous(), self.offsets, dims, base=base,
                     freqs=freqs)
 
     def attend(self, layer: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
@@ -179,7 +180,8 @@ class PrefillBatch:
         group = self.cache.layer_group[layer]
         self.cache.write(layer, self._write[group.name], k, v)
         out = paged_prefill_attention(
-            q.to(torch.float16).contiguous(), self.cache.keys[layer], self.cache.values[layer],
+            q.to(self.cache.compute_dtype).contiguous(), self.cache.keys[layer],
+            self.cache.values[layer],
             self._tables[group.name], start=self.start, page_size=self.cache.page_size,
             scale=scale, window=group.window, softcap=softcap,
             scales=self.cache.scales(layer),

@@ -191,9 +191,10 @@ def rope_inv_freq(dims: int, *, base: float | None = None, freqs: Any = None,
     return table
 
 
-def _check_f16(name: str, t: torch.Tensor, dims: int) -> None:
-    if t.dtype != torch.float16:
-        raise TypeError(f"{name} must be float16, got {t.dtype}")
+def _check_f16(name: str, t: torch.Tensor, dims: int,
+               dtype: torch.dtype = torch.float16) -> None:
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {str(dtype).replace('torch.', '')}, got {t.dtype}")
     if not t.is_cuda:
         raise ValueError(f"{name} must be on a GPU")
     if not t.is_contiguous():
@@ -217,7 +218,7 @@ def _arena_geometry(keys: torch.Tensor, page_size: int) -> tuple[int, int, int, 
 
 def _launch_rope_append(q, q_out, k, v, keys, values, positions, rows, *, n, q_heads,
                         kv_heads, head_dim, page_size, arena_rows, layout, dims, table,
-                        device, scales=None) -> None:
+                        device, scales=None, bf16=False) -> None:
     stream = torch.cuda.current_stream(device).cuda_stream
     ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
     lib = _lib.library()
@@ -226,7 +227,8 @@ def _launch_rope_append(q, q_out, k, v, keys, values, positions, rows, *, n, q_h
             int(page_size), int(arena_rows), int(layout), int(dims), ptr(table),
             ctypes.c_void_p(stream))
     if scales is None:
-        rc = lib.pda_rope_append(*head, *tail)
+        entry = lib.pda_rope_append_bf16 if bf16 else lib.pda_rope_append
+        rc = entry(*head, *tail)
     else:
         rc = lib.pda_rope_append_q8(*head, ptr(scales[0]), ptr(scales[1]), *tail)
     _lib.check(rc)
@@ -253,21 +255,25 @@ def rope_append(q: torch.Tensor | None, k: torch.Tensor, v: torch.Tensor,
     (batches.py:203-207, paged_kv.py:278-283).
 
     ``q`` ``[n, q_heads, D]`` (or None), ``k``, ``v`` ``[n, kv_heads, D]``
-    fp16; ``keys``/``values`` one layer's arena in either layout;
+    fp16, or all bf16 (bf16 models: the rotation is rounded to bf16);
+    ``keys``/``values`` one layer's arena in either layout, of that dtype;
     ``positions`` and ``rows`` int32 ``[n]`` (rows outside the arena are not
     written). ``dims`` = 0 writes without rotation. Returns the rotated
     queries (``q_out``, new unless given; ``q_out`` may be ``q``).
 
     ``scales`` = (key_scales, value_scales) writes 8-bit K/V: ``keys`` and
     ``values`` are int8 arenas, the rotated keys and the values are quantized
-    per (row, kv head) as ``paged_kv.quantize`` does (paged_kv.py:50-55)."""
+    per (row, kv head) as ``paged_kv.quantize`` does (paged_kv.py:50-55);
+    the 8-bit write takes fp16 ``q``, ``k`` and ``v``."""
     n, kv_heads, head_dim = (int(x) for x in k.shape)
     layout, arena_rows, a_heads, a_dim = _arena_geometry(keys, page_size)
+    bf16 = k.dtype == torch.bfloat16 and scales is None
+    dtype = torch.bfloat16 if bf16 else torch.float16
     for name, t, d in (("k", k, 3), ("v", v, 3)):
-        _check_f16(name, t, d)
+        _check_f16(name, t, d, dtype)
     if scales is None:
         for name, t in (("keys", keys), ("values", values)):
-            _check_f16(name, t, keys.dim())
+            _check_f16(name, t, keys.dim(), dtype)
     else:
         scale_shape = ((arena_rows, kv_heads) if layout == _lib.PDA_LAYOUT_ROWS
                        else (arena_rows // page_size, kv_heads, page_size))
@@ -285,13 +291,13 @@ def rope_append(q: torch.Tensor | None, k: torch.Tensor, v: torch.Tensor,
         raise ValueError("k does not match the arena's kv_heads and head_dim")
     q_heads = 0
     if q is not None:
-        _check_f16("q", q, 3)
+        _check_f16("q", q, 3, dtype)
         if int(q.shape[0]) != n or int(q.shape[2]) != head_dim:
             raise ValueError("q must be [n, q_heads, head_dim]")
         q_heads = int(q.shape[1])
         if q_out is None:
             q_out = torch.empty_like(q)
-        _check_f16("q_out", q_out, 3)
+        _check_f16("q_out", q_out, 3, dtype)
         if q_out.shape != q.shape:
             raise ValueError("q_out must have q's shape")
     rows = _int32_vector("rows", rows, n)
@@ -305,15 +311,17 @@ def rope_append(q: torch.Tensor | None, k: torch.Tensor, v: torch.Tensor,
                         positions if dims else None, rows, n=n, q_heads=q_heads,
                         kv_heads=kv_heads, head_dim=head_dim, page_size=page_size,
                         arena_rows=arena_rows, layout=layout, dims=dims, table=table,
-                        device=k.device, scales=scales)
+                        device=k.device, scales=scales, bf16=bf16)
     return q_out
 
 
 def rope(x: torch.Tensor, positions: torch.Tensor, dims: int, *, base: float | None = None,
          freqs: Any = None, out: torch.Tensor | None = None) -> torch.Tensor:
     """``DecodeBatch.rope`` (batches.py:195-201): rotate ``[n, heads, D]`` by
-    one position per token (non-traditional RoPE, portable.py:88-132)."""
-    _check_f16("x", x, 3)
+    one position per token (non-traditional RoPE, portable.py:88-132);
+    ``x`` fp16 or bf16, the result in ``x``'s dtype."""
+    bf16 = x.dtype == torch.bfloat16
+    _check_f16("x", x, 3, torch.bfloat16 if bf16 else torch.float16)
     n, heads, head_dim = (int(s) for s in x.shape)
     if out is None:
         out = torch.empty_like(x)
@@ -321,7 +329,7 @@ def rope(x: torch.Tensor, positions: torch.Tensor, dims: int, *, base: float | N
     table = rope_inv_freq(dims, base=base, freqs=freqs, device=x.device)
     _launch_rope_append(x, out, None, None, None, None, positions, None, n=n, q_heads=heads,
                         kv_heads=0, head_dim=head_dim, page_size=0, arena_rows=0,
-                        layout=0, dims=dims, table=table, device=x.device)
+                        layout=0, dims=dims, table=table, device=x.device, bf16=bf16)
     return out
 
 
@@ -401,17 +409,20 @@ def paged_prefill_attention(queries: torch.Tensor, keys: torch.Tensor, values: t
     reference's gather does (paged_kv.py:285-292). ``images``: (at, length)
     spans of image tokens, or an int32 GPU tensor ``[n, 2]`` of [begin, end)
     positions; a query inside one also sees the span's later keys
-    (batches.py:107-118)."""
-    _check_f16("queries", queries, 3)
+    (batches.py:107-118). bf16 queries with bf16 arenas (bf16 models) give a
+    bf16 output; the 8-bit cache takes fp16 queries."""
+    q8 = scales is not None
+    bf16 = queries.dtype == torch.bfloat16 and not q8
+    dtype = torch.bfloat16 if bf16 else torch.float16
+    _check_f16("queries", queries, 3, dtype)
     count, q_heads, head_dim = (int(x) for x in queries.shape)
     layout, arena_rows, kv_heads, a_dim = _arena_geometry(keys, page_size)
-    q8 = scales is not None
     for name, t in (("keys", keys), ("values", values)):
         if q8:
             if t.dtype != torch.int8 or not t.is_cuda or not t.is_contiguous():
                 raise TypeError(f"{name} must be a contiguous int8 GPU tensor")
         else:
-            _check_f16(name, t, keys.dim())
+            _check_f16(name, t, keys.dim(), dtype)
     if q8:
         scale_shape = tuple(keys.shape[:-1])
         for name, t in zip(("key_scales", "value_scales"), scales):
@@ -431,7 +442,7 @@ def paged_prefill_attention(queries: torch.Tensor, keys: torch.Tensor, values: t
     if out is None:
         out = torch.empty_like(queries)
     else:
-        _check_f16("out", out, 3)
+        _check_f16("out", out, 3, dtype)
         if tuple(out.shape) != tuple(queries.shape):
             raise ValueError("out must have the queries' shape")
     if count == 0:
@@ -441,7 +452,7 @@ def paged_prefill_attention(queries: torch.Tensor, keys: torch.Tensor, values: t
     ws = workspace(queries.device, need) if need else None
     stream = torch.cuda.current_stream(queries.device).cuda_stream
     spans = image_spans(images, queries.device)
-    entry = "pda_paged_prefill_attention" + ("_q8" if q8 else "")
+    entry = "pda_paged_prefill_attention" + ("_q8" if q8 else "_bf16" if bf16 else "")
     extra = (scales[0].data_ptr(), scales[1].data_ptr()) if q8 else ()
     rc = getattr(_lib.library(), entry)(
         queries.data_ptr(), keys.data_ptr(), values.data_ptr(), *extra, table.data_ptr(),

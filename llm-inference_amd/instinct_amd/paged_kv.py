@@ -159,6 +159,8 @@ class KVCache:
             raise ValueError(f"layout must be one of {LAYOUTS}")
         if bits not in (8, 16):
             raise ValueError("K/V is stored in 16 or 8 bits")
+        if dtype not in (torch.float16, torch.bfloat16):
+            raise ValueError("the model dtype is float16 or bfloat16")
         self.layout = layout
         self.bits = bits
         self.storage = torch.int8 if bits == 8 else dtype
@@ -185,6 +187,13 @@ class KVCache:
                     for store in (self.key_scales, self.value_scales):
                         store[layer] = torch.zeros(shape[:-1], dtype=torch.float16,
                                                    device=self.device)
+
+    @property
+    def compute_dtype(self) -> torch.dtype:
+        """The element type the kernels take for queries and new K/V: the
+        model dtype at 16 bits; fp16 at 8 bits, whose kernels dequantize to
+        fp16."""
+        return self.dtype if self.bits == 16 else torch.float16
 
     @property
     def _stores(self) -> tuple[dict[int, torch.Tensor], ...]:
@@ -238,7 +247,8 @@ class KVCache:
         if not arena.is_cuda:
             raise ValueError("KVCache.write runs on the GPU; the arenas are on the CPU")
         kv_write(arena, self.values[layer], rows.to(device=arena.device, dtype=torch.int32),
-                 keys.to(self.dtype).contiguous(), values.to(self.dtype).contiguous(),
+                 keys.to(self.compute_dtype).contiguous(),
+                 values.to(self.compute_dtype).contiguous(),
                  page_size=self.page_size, scales=self.scales(layer))
 
     def _pick(self, store: torch.Tensor, rows: torch.Tensor) -> torch.Tensor:

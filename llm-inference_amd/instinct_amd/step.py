@@ -32,7 +32,8 @@ class DecodeStepGraph:
     ``len(arenas)`` layers.
 
     ``arenas``: per layer ``(keys, values)`` or ``(keys, values, key_scales,
-    value_scales)`` (8-bit); all layers share ``seq_tables``
+    value_scales)`` (8-bit); bf16 arenas take bf16 q/k/v and give bf16
+    outputs, fp16 and 8-bit arenas fp16 ones; all layers share ``seq_tables``
     (``[num_slots, stride]`` int32 resident page lists), the page size, the
     window and the head shape. ``dims``/``base``/``freqs``: the rotary
     embedding (``dims`` = 0: none)."""
@@ -52,7 +53,8 @@ class DecodeStepGraph:
                        softcap=softcap)
         self.rope = dict(dims=dims, base=base, freqs=freqs)
         i32 = dict(dtype=torch.int32, device=dev)
-        f16 = dict(dtype=torch.float16, device=dev)
+        dtype = torch.bfloat16 if keys.dtype == torch.bfloat16 else torch.float16
+        f16 = dict(dtype=dtype, device=dev)
         # Step inputs, written before every replay.
         self.slots = torch.zeros(batch, **i32)
         self.positions = torch.zeros(batch, **i32)

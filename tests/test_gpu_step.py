@@ -49,11 +49,11 @@ def test_device_packing_matches_the_host_packing(gpu):
     assert lb[3].item() == width * P + 4
 
 
-def setup(gpu, layout, bits, layers=2, batch=6):
+def setup(gpu, layout, bits, layers=2, batch=6, dtype=torch.float16):
     page, heads, hq, d = 16, 4, 28, 128
     groups = [KVGroup("full", tuple(range(layers)), kv_heads=heads, head_dim=d)]
     cache = KVCache(groups, page_size=page, capacities={"full": 1024}, device=gpu,
-                    layout=layout, bits=bits)
+                    layout=layout, bits=bits, dtype=dtype)
     gen = torch.Generator(device=gpu).manual_seed(1)
     for layer in range(layers):
         if bits == 16:
@@ -73,11 +73,15 @@ def setup(gpu, layout, bits, layers=2, batch=6):
     return cache, start, slot_lists, seq_tables, width, hq
 
 
-@pytest.mark.parametrize("layout,bits", [("pages", 16), ("rows", 16), ("pages", 8)])
-def test_graph_replays_match_eager_steps(gpu, layout, bits):
+@pytest.mark.parametrize("layout,bits,dtype", [
+    ("pages", 16, torch.float16), ("rows", 16, torch.float16), ("pages", 8, torch.float16),
+    ("pages", 16, torch.bfloat16)])
+def test_graph_replays_match_eager_steps(gpu, layout, bits, dtype):
     layers, batch = 2, 6
-    cache_g, start, slot_lists, seq_tables, width, hq = setup(gpu, layout, bits, layers, batch)
-    cache_e, *_ = setup(gpu, layout, bits, layers, batch)
+    cache_g, start, slot_lists, seq_tables, width, hq = setup(gpu, layout, bits, layers, batch,
+                                                              dtype)
+    cache_e, *_ = setup(gpu, layout, bits, layers, batch, dtype)
+    work = cache_g.compute_dtype
     arenas = [(cache_g.keys[l], cache_g.values[l]) + (cache_g.scales(l) or ())
               for l in range(layers)]
     step = DecodeStepGraph(arenas, seq_tables, batch=batch, q_heads=hq, page_size=16,
@@ -87,9 +91,9 @@ def test_graph_replays_match_eager_steps(gpu, layout, bits):
     gen = torch.Generator(device=gpu).manual_seed(2)
 
     def inputs(t):
-        return [(torch.randn((batch, hq, 128), generator=gen, device=gpu).half(),
-                 torch.randn((batch, 4, 128), generator=gen, device=gpu).half(),
-                 torch.randn((batch, 4, 128), generator=gen, device=gpu).half())
+        return [(torch.randn((batch, hq, 128), generator=gen, device=gpu).to(work),
+                 torch.randn((batch, 4, 128), generator=gen, device=gpu).to(work),
+                 torch.randn((batch, 4, 128), generator=gen, device=gpu).to(work))
                 for _ in range(layers)]
 
     for t in range(4):
@@ -113,9 +117,11 @@ def test_graph_replays_match_eager_steps(gpu, layout, bits):
             want = batch_e.rope_attend(layer, q, k, v, dims=128, base=1e6, scale=128 ** -0.5)
             torch.cuda.synchronize()
             got = step.out[layer].reshape(batch, -1)
+            assert got.dtype == want.dtype == work
             d = (got.float() - want.float()).abs()
             print(f"step {t} layer {layer}: max={d.max().item():.3e}", flush=True)
-            assert d.max().item() <= MAX_ABS and d.mean().item() <= MEAN_ABS
+            bar = 8 if work == torch.bfloat16 else 1  # bf16: the eps ratio 2^-7 / 2^-10
+            assert d.max().item() <= bar * MAX_ABS and d.mean().item() <= bar * MEAN_ABS
             assert torch.equal(cache_g.keys[layer], cache_e.keys[layer])
             assert torch.equal(cache_g.values[layer], cache_e.values[layer])
         # Eager work of the program between replays.

@@ -152,6 +152,23 @@ def test_unknown_layout_is_rejected():
         small_cache("columns")
 
 
+def test_model_dtype_and_kernel_dtype():
+    """The arenas hold the model dtype (fp16 or bf16) at 16 bits and int8 at
+    8 bits; the kernels take the model dtype at 16 bits and fp16 at 8."""
+    groups = [KVGroup("full", (0,), kv_heads=2, head_dim=8)]
+
+    def make(**kw):
+        return KVCache(groups, page_size=4, capacities={"full": 2}, device="cpu", **kw)
+
+    bf = make(dtype=torch.bfloat16)
+    assert bf.keys[0].dtype == bf.compute_dtype == torch.bfloat16
+    q8 = make(dtype=torch.bfloat16, bits=8)
+    assert q8.keys[0].dtype == torch.int8 and q8.compute_dtype == torch.float16
+    assert make().compute_dtype == torch.float16
+    with pytest.raises(ValueError, match="dtype"):
+        make(dtype=torch.float32)
+
+
 def test_decode_batch_packs_tables_and_lengths():
     cache = small_cache()
     positions = np.array([0, 5, 9])
