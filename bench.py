@@ -58,6 +58,9 @@ def parse():
                          "per layer, eager and as one captured HIP graph")
     ap.add_argument("--kv-bits", type=int, choices=[16, 8], default=16,
                     help="K/V storage: fp16, or int8 with a scale per (row, kv head)")
+    ap.add_argument("--dtype", choices=["f16", "bf16"], default="f16",
+                    help="model dtype of queries, K/V and outputs at 16 bits (bf16: the "
+                         "reference's bf16 models)")
     ap.add_argument("--prefill", default="4096@0,512@32256",
                     help="prefill chunks to time, TOKENS@START comma-separated ('' = skip): "
                          "one sequence at the workload's heads, causal; the reference prefills "
@@ -107,9 +110,9 @@ def append_inputs(w):
 
     dev = w.q.device
     gen = torch.Generator(device=dev).manual_seed(7)
-    q = torch.randn(w.q.shape, generator=gen, device=dev).half()
-    k = torch.randn((w.batch, w.kv_heads, w.head_dim), generator=gen, device=dev).half()
-    v = torch.randn((w.batch, w.kv_heads, w.head_dim), generator=gen, device=dev).half()
+    q = torch.randn(w.q.shape, generator=gen, device=dev).to(w.q.dtype)
+    k = torch.randn((w.batch, w.kv_heads, w.head_dim), generator=gen, device=dev).to(w.q.dtype)
+    v = torch.randn((w.batch, w.kv_heads, w.head_dim), generator=gen, device=dev).to(w.q.dtype)
     positions = (w.lengths - 1).clamp(min=0).to(torch.int32)
     pages = w.tables.long().gather(1, (positions.long() // w.page_size)[:, None])[:, 0]
     rows = (pages * w.page_size + positions.long() % w.page_size).to(torch.int32)
@@ -267,13 +270,14 @@ def prefill_leg(w, tokens, steps, start=0):
     P, hq, hkv, d = w.page_size, w.q_heads, w.kv_heads, w.head_dim
     pages = (start + tokens + P - 1) // P
     gen = torch.Generator(device=dev).manual_seed(11)
-    keys = torch.randn((pages * P, hkv, d), generator=gen, device=dev).half()
-    values = torch.randn((pages * P, hkv, d), generator=gen, device=dev).half()
+    dtype = w.q.dtype
+    keys = torch.randn((pages * P, hkv, d), generator=gen, device=dev).to(dtype)
+    values = torch.randn((pages * P, hkv, d), generator=gen, device=dev).to(dtype)
     if w.layout == "pages":
         keys, values = rows_to_pages(keys, P), rows_to_pages(values, P)
     table = torch.as_tensor(np.random.default_rng(11).permutation(pages).astype(np.int32),
                             device=dev)
-    q = torch.randn((tokens, hq, d), generator=gen, device=dev).half()
+    q = torch.randn((tokens, hq, d), generator=gen, device=dev).to(dtype)
     out = torch.empty_like(q)
 
     def call():
@@ -290,7 +294,9 @@ def prefill_leg(w, tokens, steps, start=0):
     flops = 4.0 * d * hq * seen.sum()
     med = statistics.median(ms)
     tflops = flops / (med * 1e-3) / 1e12
-    return {"kernel": f"paged_prefill_kernel<{d}> (pda_paged_prefill_attention)",
+    bf16 = dtype == torch.bfloat16
+    return {"kernel": f"paged_prefill_kernel<{d},false,{str(bf16).lower()}> "
+                      f"(pda_paged_prefill_attention{'_bf16' if bf16 else ''})",
             "tokens": tokens, "start": start, "key_ranges": splits, "q_heads": hq,
             "kv_heads": hkv, "head_dim": d,
             "us_median": round(med * 1e3, 2), "flops": flops,
@@ -369,7 +375,15 @@ def main():
 
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
+    bf16 = args.dtype == "bf16"
+    if bf16 and args.kv_bits == 8:
+        print("bench.py: the 8-bit cache takes fp16 queries (--dtype f16)", file=sys.stderr)
+        sys.exit(2)
     w = workloads.CONFIGS[args.config](device=device).to_layout(args.layout)
+    if bf16:
+        # The same seeded values rounded to bf16: a bf16 model's cache.
+        w.q, w.keys, w.values = w.q.bfloat16(), w.keys.bfloat16(), w.values.bfloat16()
+        torch.cuda.empty_cache()
     kv_bytes = w.kv_bytes()
     fp16_bytes = kv_bytes
     scales = None
@@ -430,7 +444,7 @@ def main():
     waves, _ = _lib.plan(w.batch, w.q_heads, w.kv_heads, w.head_dim, w.page_size,
                          int(w.tables.shape[1]), w.longest, w.window, args.split_pages)
     traffic = None
-    if TRAFFIC_FILE.exists() and args.config == 2 and args.kv_bits == 16:
+    if TRAFFIC_FILE.exists() and args.config == 2 and args.kv_bits == 16 and not bf16:
         traffic = json.loads(TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
     line = {
         "metric": METRIC,
@@ -443,7 +457,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16" if args.kv_bits == 16 else "i8 K/V, f16 math",
+        "dtype": ("bf16" if bf16 else "f16") if args.kv_bits == 16 else "i8 K/V, f16 math",
         "data": "synthetic (seeded N(0,1) K/V/Q, random page permutation)",
         "config": {
             "workload": w.name,
@@ -467,7 +481,8 @@ def main():
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
             "kernel": f"paged_decode_kernel<{w.head_dim},{min(8, w.q_heads // w.kv_heads)},"
-                      f"{str(args.kv_bits == 8).lower()}> (split pass; events around it alone)",
+                      f"{str(args.kv_bits == 8).lower()},{str(bf16).lower()}> "
+                      "(split pass; events around it alone)",
             "us_mean": round(split_mean * 1e3, 2),
             "call_us_mean": round(statistics.fmean(ms) * 1e3, 2),
         },
@@ -478,7 +493,8 @@ def main():
         # Keys per second in fp16 terms: the fp16 bytes of the same rows / time.
         line["fp16_equivalent_GB_per_s"] = round(fp16_bytes / (med * 1e-3) / 1e9, 2)
     line["wall_s_timed_loop"] = round(wall, 3)
-    if not args.no_cpu and args.kv_bits == 16:
+    # The CPU baselines time the fp16 oracle; a bf16 run has none.
+    if not args.no_cpu and args.kv_bits == 16 and not bf16:
         line["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
 
     # The step before the attention call: RoPE of the new queries and keys and
@@ -502,7 +518,8 @@ def main():
     (step_ms,), _ = time_calls([append_and_call], args.steps, flushing)
     app_med = statistics.median(app_ms)
     line["append"] = {
-        "kernel": ("rope_append_kernel (pda_rope_append: RoPE of q and k, K/V write)"
+        "kernel": (f"rope_append_kernel<{'bf16' if bf16 else 'f16'}> (pda_rope_append"
+                   f"{'_bf16' if bf16 else ''}: RoPE of q and k, K/V write)"
                    if args.kv_bits == 16 else
                    "rope_append_q8_kernel (pda_rope_append_q8: RoPE, quantized K/V write)"),
         "tokens": w.batch,
@@ -510,7 +527,7 @@ def main():
         "bytes": abytes,
         "GB_per_s": round(abytes / (app_med * 1e-3) / 1e9, 2),
     }
-    if not args.no_cpu and args.kv_bits == 16:
+    if not args.no_cpu and args.kv_bits == 16 and not bf16:
         line["append"]["cpu_baseline"] = append_cpu_baseline(w, 2.0)
     line["layer_step_us"] = round(statistics.median(step_ms) * 1e3, 2)
     if args.step_layers > 0:
@@ -520,7 +537,7 @@ def main():
         for case in args.prefill.split(","):
             tokens, start = (int(x) for x in case.split("@"))
             leg = prefill_leg(w, tokens, args.steps, start=start)
-            if not args.no_cpu:
+            if not args.no_cpu and not bf16:
                 leg["cpu_baseline"] = prefill_cpu_baseline(w, tokens, start, 6.0)
             line["prefill"].append(leg)
     print(json.dumps(line), flush=True)
