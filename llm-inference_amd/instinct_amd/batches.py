@@ -73,7 +73,7 @@ class DecodeBatch:
              freqs: Any = None) -> torch.Tensor:
         """Rotary embedding of ``[batch, heads, head_dim]`` at each
         sequence's position (batches.py:195-201, portable.py:88-132)."""
-        return rope(x.to(self.cache.compute_dtype).contiguous(), self.offsets, dims, base=base,
+        return rope(x.to(self.cache.dtype).contiguous(), self.offsets, dims, base=base,
                     freqs=freqs)
 
     def rope_attend(self, layer: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
@@ -81,10 +81,17 @@ class DecodeBatch:
                     softcap: float = 0.0) -> torch.Tensor:
         """``attend(layer, rope(q), rope(k), v)`` with the rotation of q and k
         and the K/V write in one launch (the model calls of
-        backends/dense.py:99-102 and DecodeBatch.attend, batches.py:203-226)."""
+        backends/dense.py:99-102 and DecodeBatch.attend, batches.py:203-226).
+        A bf16 model over an 8-bit cache takes the three steps apart: its
+        rotated keys are rounded to bf16 before they are quantized, as the
+        reference's are, while the fused 8-bit write rounds them to fp16."""
         group = self.cache.layer_group[layer]
         cache = self.cache
         dtype = cache.compute_dtype
+        if dtype != cache.dtype:
+            rot = dict(base=base, freqs=freqs)
+            return self.attend(layer, self.rope(q, dims, **rot), self.rope(k, dims, **rot), v,
+                               scale=scale, softcap=softcap)
         q_rot = rope_append(q.to(dtype).contiguous(), k.to(dtype).contiguous(),
                             v.to(dtype).contiguous(), cache.keys[layer],
                             cache.values[layer], self.offsets, self._write[group.name],
@@ -117,7 +124,7 @@ class DecodeBatch:
             softcap=softcap,
             scales=self.cache.scales(layer),
         )
-        return out.reshape(self.count, -1)
+        return out.reshape(self.count, -1).to(self.cache.dtype)
 
 
 class PrefillBatch:
@@ -169,7 +176,7 @@ class PrefillBatch:
              freqs: Any = None) -> torch.Tensor:
         """Rotate ``[tokens, heads, head_dim]`` at the chunk's positions
         (batches.py:70-81)."""
-        return rope(x.to(self.cache.compute_dtype).contiguous(), self.offsets, dims, base=base,
+        return rope(x.to(self.cache.dtype).contiguous(), self.offsets, dims, base=base,
                     freqs=freqs)
 
     def attend(self, layer: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
@@ -186,4 +193,4 @@ class PrefillBatch:
             scale=scale, window=group.window, softcap=softcap,
             scales=self.cache.scales(layer),
             images=self._spans if self._spans is not None else ())
-        return out.reshape(self.count, -1)
+        return out.reshape(self.count, -1).to(self.cache.dtype)

@@ -360,3 +360,73 @@ def test_bf16_cache_prefill_then_decode(gpu, layout):
         err_max, err_mean = pa.error_stats(out.view(1, hq, d).float().cpu().numpy(), want)
         print(f"bf16 decode step {t} {layout}: max_abs={err_max:.3e}")
         assert err_max <= MAX_ABS and err_mean <= MEAN_ABS
+
+
+def test_bf16_model_over_8bit_cache(gpu):
+    """KVCache(dtype=bfloat16, bits=8): the kernels take fp16 (bf16 -> fp16
+    is exact in fp16's range), rope runs in bf16, rope_attend rounds the
+    rotated keys to bf16 before quantizing them (the reference's order,
+    paged_kv.py:50-55,278-283), and attention outputs come back in bf16. The
+    oracle: the reference's quantization of the bf16 rotated keys and of the
+    values, attention over the dequantized rows."""
+    from instinct_amd.batches import DecodeBatch, PrefillBatch
+    from instinct_amd.paged_kv import KVCache, KVGroup, pages_to_rows
+    from oracle import kv8
+
+    page, hq, hkv, d = 16, 14, 2, 128
+    groups = [KVGroup("full", (0,), kv_heads=hkv, head_dim=d)]
+    cache = KVCache(groups, page_size=page, capacities={"full": 64}, device=gpu,
+                    dtype=torch.bfloat16, bits=8)
+    assert cache.keys[0].dtype == torch.int8 and cache.compute_dtype == torch.float16
+    n = 200
+    table = np.array([cache.pools["full"].allocate(reserved=False) for _ in range(16)])
+    gen = torch.Generator(device=gpu).manual_seed(9)
+    q = torch.randn((n + 2, hq, d), generator=gen, device=gpu).bfloat16()
+    k = torch.randn((n + 2, hkv, d), generator=gen, device=gpu).bfloat16()
+    v = torch.randn((n + 2, hkv, d), generator=gen, device=gpu).bfloat16()
+
+    def arena():
+        keys, values = pages_to_rows(cache.keys[0]), pages_to_rows(cache.values[0])
+        k_s = cache.key_scales[0].permute(0, 2, 1).reshape(-1, hkv)
+        v_s = cache.value_scales[0].permute(0, 2, 1).reshape(-1, hkv)
+        f = lambda t: t.cpu().numpy()  # noqa: E731
+        return f(keys), f(values), f(k_s), f(v_s)
+
+    chunk = PrefillBatch(cache, torch.zeros(n, device=gpu), start=0, tables={"full": table})
+    q_rot, k_rot = chunk.rope(q[:n], d, base=1e6), chunk.rope(k[:n], d, base=1e6)
+    assert q_rot.dtype == k_rot.dtype == torch.bfloat16
+    out = chunk.attend(0, q_rot, k_rot, v[:n], scale=d ** -0.5)
+    torch.cuda.synchronize()
+    assert out.dtype == torch.bfloat16
+    kq, vq, ks, vs = arena()
+    rows = np.concatenate([table[p // page] * page + np.arange(page) for p in range(0, n, page)])[:n]
+    want_kq, want_ks = kv8.quantize(k_rot.float().cpu().numpy())
+    np.testing.assert_array_equal(ks[rows], want_ks)
+    np.testing.assert_array_equal(kq[rows], want_kq)
+    want = pa.paged_prefill_dense(q_rot.float().cpu().numpy(), kv8.gather_dequantize(kq, ks),
+                                  kv8.gather_dequantize(vq, vs), table, start=0,
+                                  page_size=page, scale=d ** -0.5)
+    err_max, err_mean = pa.error_stats(out.view(n, hq, d).float().cpu().numpy(), want)
+    print(f"bf16 model, 8-bit cache, prefill: max_abs={err_max:.3e} mean_abs={err_mean:.3e}")
+    assert err_max <= MAX_ABS and err_mean <= MEAN_ABS
+    for t in (n, n + 1):
+        step = DecodeBatch(cache, torch.zeros(1, device=gpu), positions=np.array([t]),
+                           tables={"full": [table]})
+        out = step.rope_attend(0, q[t:t + 1], k[t:t + 1], v[t:t + 1], dims=d, base=1e6,
+                               scale=d ** -0.5)
+        torch.cuda.synchronize()
+        assert out.dtype == torch.bfloat16
+        kq, vq, ks, vs = arena()
+        row = table[t // page] * page + t % page
+        k_rot = step.rope(k[t:t + 1], d, base=1e6)
+        want_kq, want_ks = kv8.quantize(k_rot.float().cpu().numpy())
+        np.testing.assert_array_equal(kq[row], want_kq[0])
+        np.testing.assert_array_equal(ks[row], want_ks[0])
+        q_rot = step.rope(q[t:t + 1], d, base=1e6).float().cpu().numpy()
+        want = pa.paged_decode_dense(q_rot, kv8.gather_dequantize(kq, ks),
+                                     kv8.gather_dequantize(vq, vs),
+                                     table[None].astype(np.int32), np.array([t + 1], np.int32),
+                                     page_size=page, scale=d ** -0.5)
+        err_max, err_mean = pa.error_stats(out.view(1, hq, d).float().cpu().numpy(), want)
+        print(f"bf16 model, 8-bit cache, decode step {t}: max_abs={err_max:.3e}")
+        assert err_max <= MAX_ABS and err_mean <= MEAN_ABS
