@@ -65,6 +65,13 @@ def parse():
                     help="prefill chunks to time, TOKENS@START comma-separated ('' = skip): "
                          "one sequence at the workload's heads, causal; the reference prefills "
                          "512-token chunks (mlx_engine.py:74)")
+    ap.add_argument("--prefill-wide", default="4096@0,4096@28672,4096@258048",
+                    help="prefill chunks at 512-wide heads, TOKENS@START ('' = skip): the "
+                         "global layers of the reference's Gemma 4 (gemma4.py:49-66), whose "
+                         "4096-token chunks at 256K context the reference names as its "
+                         "prefill bottleneck (docs/benchmarks.md:102-105, roadmap.md:36)")
+    ap.add_argument("--wide-heads", default="16/2",
+                    help="query/kv heads of the 512-wide legs (a representative shape)")
     ap.add_argument("--no-flush", action="store_true", help="skip the flushed pass")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="approximate CPU time budget of the CPU-baseline sample")
@@ -540,6 +547,23 @@ def main():
             if not args.no_cpu and not bf16:
                 leg["cpu_baseline"] = prefill_cpu_baseline(w, tokens, start, 6.0)
             line["prefill"].append(leg)
+    if args.prefill_wide and args.kv_bits == 16:
+        from types import SimpleNamespace
+
+        hq, hkv = (int(x) for x in args.wide_heads.split("/"))
+        wide = SimpleNamespace(q=w.q[:1], page_size=w.page_size, q_heads=hq, kv_heads=hkv,
+                               head_dim=512, scale=512 ** -0.5, window=0, softcap=0.0,
+                               layout=w.layout)
+        line["prefill_wide"] = []
+        for case in args.prefill_wide.split(","):
+            tokens, start = (int(x) for x in case.split("@"))
+            leg = prefill_leg(wide, tokens, min(args.steps, 10), start=start)
+            # The float32 oracle gathers the whole prefix per call: only the
+            # shorter prefixes are sampled on the CPU.
+            if not args.no_cpu and not bf16 and start + tokens <= 65536:
+                leg["cpu_baseline"] = prefill_cpu_baseline(wide, tokens, start, 6.0)
+            line["prefill_wide"].append(leg)
+            torch.cuda.empty_cache()
     print(json.dumps(line), flush=True)
 
 

@@ -65,7 +65,12 @@ constexpr float kLog2e = 1.44269504088896340736f;
 constexpr float kSlack = 8.0f;
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kQueries = 32 * kWaves;  // queries per workgroup
+// Waves that split the head dim: at D = 512 the query fragments and output
+// accumulators of 32 queries do not fit one wave's registers, so the four
+// waves of a workgroup share 32 queries, each holding 128 dims of Q and O.
+constexpr int slices_for(int d) { return d > 256 ? 4 : 1; }
+// Queries per workgroup: 32 per wave, or 32 shared by the slices.
+constexpr int queries_for(int d) { return 32 * kWaves / slices_for(d); }
 constexpr int kXcds = 8;
 
 struct PrefillParams {
@@ -90,7 +95,7 @@ struct PrefillParams {
   int32_t table_len;
   int32_t start;
   int32_t count;
-  int32_t tiles;       // query tiles = ceil(count / kQueries)
+  int32_t tiles;       // query tiles = ceil(count / queries per workgroup)
   int32_t splits;      // key ranges per (query tile, head)
   int32_t page_step;   // keys per tile / page_size when that divides, else 0
   int32_t hq;
@@ -145,6 +150,9 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
   static_assert(!(Q8 && BF), "8-bit K/V dequantizes to fp16");
   constexpr int KB = blocks_per_tile<D>();  // 32-key blocks per tile
   constexpr int kKeys = 32 * KB;            // keys per tile
+  constexpr int kSlices = slices_for(D);    // waves sharing one query block
+  constexpr int kDW = D / kSlices;          // head dims per wave
+  constexpr int kQ = queries_for(D);        // queries per workgroup
   constexpr int kKRow = D + 8;    // K row in LDS (halves): 16-lane 16-byte reads hit distinct banks
   constexpr int kVRow = D + 32;   // V row: the 4 rows of a transposed read hit distinct banks
   constexpr int kTpk = kThreads / kKeys;               // gather threads per key
@@ -156,12 +164,17 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
   __shared__ __align__(16) f16 s_k[2][kKeys * kKRow];
   __shared__ __align__(16) f16 s_v[2][kKeys * kVRow];
   __shared__ __align__(8) okbits s_ok[2][kWaves];  // usable-key bits of the tile
+  // D = 512: each wave's partial scores (over its dims), summed by all the
+  // waves of the query block.
+  __shared__ __align__(16) float4 s_x[kSlices > 1 ? kWaves * 4 * KB : 1][64];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = uniform(tid >> 6);
   const int n = lane & 31;   // query column of this lane
   const int hh = lane >> 5;  // which half of the key rows this lane holds
+  const int qb = w / kSlices;       // this wave's 32-query block
+  const int sl = w - qb * kSlices;  // and its head dims: [sl kDW, (sl + 1) kDW)
 
   // Work item. Logical order: query tiles from the last (most keys) to the
   // first, then key range, then kv head, then the G query heads of that kv
@@ -181,30 +194,31 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
   const int split = (run / p.hkv) % p.splits;
   const int tile = p.tiles - 1 - run / p.hkv / p.splits;
 
-  const int q0 = tile * kQueries;
-  const int q1 = min(q0 + kQueries, p.count);
-  const int qi = q0 + 32 * w + n;  // this lane's query (may be past count)
+  const int q0 = tile * kQ;
+  const int q1 = min(q0 + kQ, p.count);
+  const int qi = q0 + 32 * qb + n;  // this lane's query (may be past count)
   const bool q_live = qi < p.count;
   const int qpos = p.start + qi;
-  const int wq0 = q0 + 32 * w;
+  const int wq0 = q0 + 32 * qb;
   const bool wave_live = wq0 < p.count;
   const int wfirst = p.start + wq0;
   const int wlast = p.start + min(wq0 + 31, p.count - 1);
 
-  // Query fragments (B operand of S^T = K Q^T): dims 16 c + 8 hh .. + 7.
-  f16x8 qf[D / 16];
+  // Query fragments (B operand of S^T = K Q^T): dims 16 c + 8 hh .. + 7 of
+  // the wave's slice.
+  f16x8 qf[kDW / 16];
   {
-    const f16* qp = p.q + ((int64_t)(q_live ? qi : 0) * p.hq + h) * D + 8 * hh;
+    const f16* qp = p.q + ((int64_t)(q_live ? qi : 0) * p.hq + h) * D + sl * kDW + 8 * hh;
 #pragma unroll
-    for (int c = 0; c < D / 16; ++c) {
+    for (int c = 0; c < kDW / 16; ++c) {
       const f16x8 x = *reinterpret_cast<const f16x8*>(qp + 16 * c);
       qf[c] = q_live ? x : f16x8{};
     }
   }
 
-  f32x16 o[D / 32];
+  f32x16 o[kDW / 32];
 #pragma unroll
-  for (int b = 0; b < D / 32; ++b) o[b] = f32x16{};
+  for (int b = 0; b < kDW / 32; ++b) o[b] = f32x16{};
   float m = -INFINITY, l = 0.0f;
 
   // Keys this workgroup needs: from the first visible key of its first query
@@ -341,8 +355,9 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
   // Lane part of the transposed V read: group g = lane / 16 reads dims
   // 16 (g % 2) + 4 (s % 4) of key 4 (g / 2) + s / 4, s = lane % 16.
   const int g16 = lane >> 4, s16 = lane & 15;
-  const int v_lane = (4 * (g16 >> 1) + (s16 >> 2)) * kVRow + 16 * (g16 & 1) + 4 * (s16 & 3);
-  const int k_lane = n * kKRow + 8 * hh;
+  const int v_lane =
+      (4 * (g16 >> 1) + (s16 >> 2)) * kVRow + 16 * (g16 & 1) + 4 * (s16 & 3) + sl * kDW;
+  const int k_lane = n * kKRow + 8 * hh + sl * kDW;
   const int qlo = p.window > 0 ? qpos - p.window : INT32_MIN;  // keys > qlo are in the window
   const float c = p.softcap <= 0.0f && p.scale_log2 > 0.0f ? p.scale_log2 : 1.0f;
 
@@ -362,16 +377,16 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
 
     const bool work = wave_live && k0 <= wave_last &&
                       (p.window <= 0 || wave_img || k0 + kKeys - 1 > wfirst - p.window);
+    const f16* sk = s_k[buf];
+    const f16* sv = s_v[buf];
+    // S^T per 32-key block kb: lane holds keys 32 kb + 8 (v / 4) + 4 hh + v % 4.
+    f32x16 s[KB];
     if (work) {
-      const f16* sk = s_k[buf];
-      const f16* sv = s_v[buf];
-      // S^T per 32-key block kb: lane holds keys 32 kb + 8 (v / 4) + 4 hh + v % 4.
-      f32x16 s[KB];
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
-        f16x8 ka[D / 16];
+        f16x8 ka[kDW / 16];
 #pragma unroll
-        for (int c = 0; c < D / 16; ++c)
+        for (int c = 0; c < kDW / 16; ++c)
           ka[c] = *reinterpret_cast<const f16x8*>(sk + k_lane + 32 * kb * kKRow + 16 * c);
         s[kb] = f32x16{};
         // Raised wave priority while this wave issues matrix-core work: the
@@ -380,10 +395,43 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
         // the MFMA phase of the other (2-4% on config 2's chunks).
         __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-        for (int c = 0; c < D / 16; ++c)
+        for (int c = 0; c < kDW / 16; ++c)
           s[kb] = mfma16<BF>(ka[c], qf[c], s[kb]);
         __builtin_amdgcn_s_setprio(0);
       }
+    }
+    if constexpr (kSlices > 1) {
+      // Sum the slices' partial scores in slice order, so that every wave of
+      // the block holds the same scores, maximum, sum and probabilities.
+      // `work` is the same for all of them (it depends on the queries only).
+      if (work) {
+#pragma unroll
+        for (int i = 0; i < 4 * KB; ++i)
+          s_x[w * 4 * KB + i][lane] = make_float4(s[i / 4][4 * (i % 4)], s[i / 4][4 * (i % 4) + 1],
+                                                  s[i / 4][4 * (i % 4) + 2],
+                                                  s[i / 4][4 * (i % 4) + 3]);
+      }
+      __syncthreads();
+      if (work) {
+#pragma unroll
+        for (int i = 0; i < 4 * KB; ++i) {
+          float4 acc = s_x[qb * kSlices * 4 * KB + i][lane];
+#pragma unroll
+          for (int j = 1; j < kSlices; ++j) {
+            const float4 y = s_x[(qb * kSlices + j) * 4 * KB + i][lane];
+            acc.x += y.x;
+            acc.y += y.y;
+            acc.z += y.z;
+            acc.w += y.w;
+          }
+          s[i / 4][4 * (i % 4)] = acc.x;
+          s[i / 4][4 * (i % 4) + 1] = acc.y;
+          s[i / 4][4 * (i % 4) + 2] = acc.z;
+          s[i / 4][4 * (i % 4) + 3] = acc.w;
+        }
+      }
+    }
+    if (work) {
       const okword okm = *reinterpret_cast<const okword*>(s_ok[buf]);
       const bool edge = k0 + kKeys - 1 > wfirst || okm != (okword)~(okword)0 ||
                         (p.window > 0 && k0 <= wlast - p.window);
@@ -434,7 +482,7 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
         m = top;
         l *= f;
 #pragma unroll
-        for (int b = 0; b < D / 32; ++b)
+        for (int b = 0; b < kDW / 32; ++b)
 #pragma unroll
           for (int v = 0; v < 16; ++v) o[b][v] *= f;
       }
@@ -467,7 +515,7 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
       // 16 ks + 4 hh + 0..3 (first read) and + 8 (second read).
       __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-      for (int b = 0; b < D / 32; ++b) {
+      for (int b = 0; b < kDW / 32; ++b) {
 #pragma unroll
         for (int ks = 0; ks < 2 * KB; ++ks) {
           const f16* vp = sv + v_lane + 16 * ks * kVRow + 32 * b;
@@ -489,21 +537,21 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
     // Unnormalised partial and its (max, sum) for the merge; an empty or
     // fully masked range leaves m = -inf, l = 0 and zeros.
     const int64_t at = ((int64_t)split * p.count + qi) * p.hq + h;
-    float* dst = p.part_o + at * D;
+    float* dst = p.part_o + at * D + sl * kDW;
 #pragma unroll
-    for (int b = 0; b < D / 32; ++b)
+    for (int b = 0; b < kDW / 32; ++b)
 #pragma unroll
       for (int g = 0; g < 4; ++g)
         *reinterpret_cast<float4*>(dst + 32 * b + 8 * g + 4 * hh) =
             make_float4(o[b][4 * g], o[b][4 * g + 1], o[b][4 * g + 2], o[b][4 * g + 3]);
-    if (hh == 0) p.part_ml[at] = make_float2(m, l);
+    if (hh == 0 && sl == 0) p.part_ml[at] = make_float2(m, l);
     return;
   }
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-  f16* dst = p.out + ((int64_t)qi * p.hq + h) * D;
-  // O^T rows: element 32 b + 8 (v / 4) + 4 hh + v % 4 of query n.
+  f16* dst = p.out + ((int64_t)qi * p.hq + h) * D + sl * kDW;
+  // O^T rows: element 32 b + 8 (v / 4) + 4 hh + v % 4 of query n (of the slice).
 #pragma unroll
-  for (int b = 0; b < D / 32; ++b) {
+  for (int b = 0; b < kDW / 32; ++b) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       f16x4 y;
@@ -562,13 +610,14 @@ constexpr int kMaxSplits = 64;
 // forces a count.
 int prefill_splits(int start, int count, int q_heads, int head_dim, int window, int request) {
   if (request > 0) return request < kMaxSplits ? request : kMaxSplits;
-  const int64_t wgs = (int64_t)(count + kQueries - 1) / kQueries * q_heads;
+  const int queries = queries_for(head_dim);
+  const int64_t wgs = (int64_t)(count + queries - 1) / queries * q_heads;
   const int occupancy = head_dim == 64 ? 3 : head_dim == 128 ? 2 : 1;
   const int64_t slots = (int64_t)kCus * occupancy;
   if (wgs * 2 > slots) return 1;
   const int keys = 32 * (head_dim <= 128 ? 2 : 1);
   int64_t span = (int64_t)start + count;
-  if (window > 0 && span > (int64_t)window + kQueries) span = (int64_t)window + kQueries;
+  if (window > 0 && span > (int64_t)window + queries) span = (int64_t)window + queries;
   const int64_t by_keys = (span + keys - 1) / keys / 8;
   int64_t s = slots / wgs;
   if (s > by_keys) s = by_keys;
@@ -591,14 +640,16 @@ template <bool Q8, bool BF>
 const void* prefill_kernel_for(int head_dim) {
   return head_dim == 64    ? reinterpret_cast<const void*>(paged_prefill_kernel<64, Q8, BF>)
          : head_dim == 128 ? reinterpret_cast<const void*>(paged_prefill_kernel<128, Q8, BF>)
-                           : reinterpret_cast<const void*>(paged_prefill_kernel<256, Q8, BF>);
+         : head_dim == 256 ? reinterpret_cast<const void*>(paged_prefill_kernel<256, Q8, BF>)
+                           : reinterpret_cast<const void*>(paged_prefill_kernel<512, Q8, BF>);
 }
 
 template <bool BF>
 const void* merge_kernel_for(int head_dim) {
   return head_dim == 64    ? reinterpret_cast<const void*>(prefill_merge_kernel<64, BF>)
          : head_dim == 128 ? reinterpret_cast<const void*>(prefill_merge_kernel<128, BF>)
-                           : reinterpret_cast<const void*>(prefill_merge_kernel<256, BF>);
+         : head_dim == 256 ? reinterpret_cast<const void*>(prefill_merge_kernel<256, BF>)
+                           : reinterpret_cast<const void*>(prefill_merge_kernel<512, BF>);
 }
 
 int prefill(const void* queries, const void* keys, const void* values, const void* key_scales,
@@ -616,8 +667,8 @@ int prefill(const void* queries, const void* keys, const void* values, const voi
                 count, start, q_heads, kv_heads, page_size, table_len, window, splits);
   if (q_heads % kv_heads)
     return fail(PDA_ERR_HEAD_RATIO, "query heads must be a multiple of kv heads");
-  if (head_dim != 64 && head_dim != 128 && head_dim != 256)
-    return fail(PDA_ERR_HEAD_DIM, "head_dim %d has no prefill kernel (64, 128, 256)",
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256 && head_dim != 512)
+    return fail(PDA_ERR_HEAD_DIM, "head_dim %d has no prefill kernel (64, 128, 256, 512)",
                 head_dim);
   if (count == 0) return ok();
   if (table_len == 0)
@@ -647,7 +698,8 @@ int prefill(const void* queries, const void* keys, const void* values, const voi
     return fail(PDA_ERR_ALIGNMENT, "fp16 scale arenas must be 2-byte aligned");
   if ((uintptr_t)table & 3) return fail(PDA_ERR_ALIGNMENT, "the table must be 4-byte aligned");
   const int nsplit = prefill_splits(start, count, q_heads, head_dim, window, splits);
-  if ((int64_t)((count + kQueries - 1) / kQueries) * q_heads * nsplit > INT32_MAX)
+  const int per_wg = queries_for(head_dim);
+  if ((int64_t)((count + per_wg - 1) / per_wg) * q_heads * nsplit > INT32_MAX)
     return fail(PDA_ERR_INVALID_ARGUMENT, "query tiles x query heads x splits exceeds 2^31");
   const size_t need = prefill_workspace(nsplit, count, q_heads, head_dim);
   if (need > 0 && (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 255)))
@@ -688,7 +740,7 @@ int prefill(const void* queries, const void* keys, const void* values, const voi
   prm.table_len = table_len;
   prm.start = start;
   prm.count = count;
-  prm.tiles = (count + kQueries - 1) / kQueries;
+  prm.tiles = (count + per_wg - 1) / per_wg;
   prm.splits = nsplit;
   const int tile_keys = head_dim <= 128 ? 64 : 32;
   prm.page_step = tile_keys % page_size == 0 ? tile_keys / page_size : 0;
@@ -737,8 +789,8 @@ int pda_prefill_workspace_bytes(int32_t start, int32_t count, int32_t q_heads,
   if (count < 0 || start < 0 || q_heads <= 0 || window < 0 || splits < 0 || !bytes)
     return fail(PDA_ERR_INVALID_ARGUMENT, "count=%d start=%d q_heads=%d window=%d splits=%d",
                 count, start, q_heads, window, splits);
-  if (head_dim != 64 && head_dim != 128 && head_dim != 256)
-    return fail(PDA_ERR_HEAD_DIM, "head_dim %d has no prefill kernel (64, 128, 256)",
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256 && head_dim != 512)
+    return fail(PDA_ERR_HEAD_DIM, "head_dim %d has no prefill kernel (64, 128, 256, 512)",
                 head_dim);
   const int s = count == 0 ? 1 : prefill_splits(start, count, q_heads, head_dim, window, splits);
   if (splits_used) *splits_used = s;

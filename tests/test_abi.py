@@ -235,6 +235,11 @@ def test_prefill_split_plan():
     assert _lib.prefill_workspace_bytes(0, 0, 8, 64, splits=3) == (1, 0)
     with pytest.raises(_lib.PdaError):
         _lib.prefill_workspace_bytes(0, 10, 8, 96)
+    # 512-wide heads: 32 queries per workgroup, one workgroup per CU. A
+    # 64-token chunk at 8 heads is 16 workgroups; 16 ranges fill the 256 CUs.
+    assert _lib.prefill_workspace_bytes(6000, 64, 8, 512) == (
+        16, 16 * 64 * 8 * 512 * 4 + 16 * 64 * 8 * 8)
+    assert _lib.prefill_workspace_bytes(0, 4096, 16, 512) == (1, 0)
 
 
 def test_prefill_q8_validation():

@@ -430,3 +430,11 @@ def test_bf16_model_over_8bit_cache(gpu):
         err_max, err_mean = pa.error_stats(out.view(1, hq, d).float().cpu().numpy(), want)
         print(f"bf16 model, 8-bit cache, decode step {t}: max_abs={err_max:.3e}")
         assert err_max <= MAX_ABS and err_mean <= MEAN_ABS
+
+
+@pytest.mark.parametrize("layout", ["pages", "rows"])
+def test_prefill_head_dim_512(gpu, layout):
+    c = prefill_case(gpu, hq=8, hkv=2, d=512, start=900, count=130, layout=layout, seed=90)
+    check_prefill(c, scale=512 ** -0.5, what=f"bf16 prefill D512 {layout}")
+    check_prefill(c, scale=512 ** -0.5, splits=3, window=500,
+                  what=f"bf16 prefill D512 3 ranges, window {layout}")

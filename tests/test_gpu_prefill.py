@@ -327,3 +327,59 @@ def test_image_span_at_every_position(gpu):
             worst = max(worst, err)
             assert err <= MAX_ABS, (a, n, err)
     print(f"image spans at every position: worst max_abs={worst:.3e}")
+
+
+# --- 512-wide heads (Gemma 4's global layers): four waves split the head dim --
+
+@pytest.mark.parametrize("layout", ["pages", "rows"])
+@pytest.mark.parametrize("hq,hkv,start,count", [
+    (16, 2, 0, 300), (8, 1, 700, 65), (4, 4, 31, 1), (16, 2, 4000, 96)])
+def test_head_dim_512(gpu, layout, hq, hkv, start, count):
+    c = case(gpu, hq=hq, hkv=hkv, d=512, start=start, count=count, layout=layout,
+             seed=hq + start + count)
+    check(c, scale=512 ** -0.5, what=f"D512 {hq}/{hkv} @{start}+{count} {layout}")
+
+
+def test_head_dim_512_ranges_window_softcap_images(gpu):
+    c = case(gpu, hq=8, hkv=2, d=512, start=1500, count=200, page=32, seed=77, released=(0, 3))
+    check(c, scale=512 ** -0.5, window=300, softcap=50.0, what="D512 window+softcap")
+    for splits in (2, 5):
+        check(c, scale=512 ** -0.5, window=300, splits=splits,
+              what=f"D512 window, {splits} ranges")
+    c = case(gpu, hq=8, hkv=2, d=512, start=100, count=180, seed=78)
+    check(c, scale=512 ** -0.5, images=[(110, 7), (150, 70), (270, 10)],
+          what="D512 image spans")
+    check(c, scale=512 ** -0.5, splits=3, images=[(150, 70)], what="D512 images, 3 ranges")
+
+
+def test_head_dim_512_long_prefix_splits_automatically(gpu):
+    from instinct_amd import _lib
+
+    assert _lib.prefill_workspace_bytes(6000, 64, 8, 512)[0] > 1
+    c = case(gpu, hq=8, hkv=1, d=512, start=6000, count=64, seed=79)
+    check(c, scale=512 ** -0.5, what="D512 64@6000 auto split")
+
+
+@pytest.mark.parametrize("layout", ["pages", "rows"])
+def test_head_dim_512_8bit_cache(gpu, layout):
+    page, hq, hkv, d, start, count = 16, 8, 2, 512, 300, 140
+    c = case(gpu, hq=hq, hkv=hkv, d=d, start=start, count=count, seed=80, layout="rows")
+    q, k16, v16, table = c["t"]
+    s8 = []
+    for x in (k16, v16):
+        scale = (x.float().abs().amax(-1).clamp(min=1e-4) / 127.0).half()
+        s8.append((scale, (x.float() / scale.float()[..., None]).round().clamp(-127, 127)
+                   .to(torch.int8)))
+    (ks, kq), (vs, vq) = s8
+    want = pa.paged_prefill_dense(c["q"], kv8.gather_dequantize(kq.cpu().numpy(), ks.cpu().numpy()),
+                                  kv8.gather_dequantize(vq.cpu().numpy(), vs.cpu().numpy()),
+                                  c["table"], start=start, page_size=page, scale=d ** -0.5)
+    if layout == "pages":
+        kq, vq = rows_to_pages(kq, page), rows_to_pages(vq, page)
+        ks, vs = scales_to_pages(ks, page), scales_to_pages(vs, page)
+    got = paged_prefill_attention(q, kq, vq, table, start=start, page_size=page,
+                                  scale=d ** -0.5, scales=(ks, vs))
+    torch.cuda.synchronize()
+    err_max, err_mean = pa.error_stats(got.float().cpu().numpy(), want)
+    print(f"D512 8-bit {layout}: max_abs={err_max:.3e} mean_abs={err_mean:.3e}", flush=True)
+    assert err_max <= MAX_ABS and err_mean <= MEAN_ABS
