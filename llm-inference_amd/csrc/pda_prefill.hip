@@ -63,14 +63,15 @@ typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 constexpr float kLog2e = 1.44269504088896340736f;
 constexpr float kSlack = 8.0f;
-constexpr int kWaves = 4;
-constexpr int kThreads = 64 * kWaves;
+constexpr int kWaves = 4;  // waves per workgroup (D <= 256)
 // Waves that split the head dim: at D = 512 the query fragments and output
-// accumulators of 32 queries do not fit one wave's registers, so the four
-// waves of a workgroup share 32 queries, each holding 128 dims of Q and O.
+// accumulators of 32 queries do not fit one wave's registers, so four waves
+// share 32 queries, each holding 128 dims of Q and O; a D = 512 workgroup has
+// eight waves (two such query blocks).
 constexpr int slices_for(int d) { return d > 256 ? 4 : 1; }
-// Queries per workgroup: 32 per wave, or 32 shared by the slices.
-constexpr int queries_for(int d) { return 32 * kWaves / slices_for(d); }
+constexpr int waves_for(int d) { return d > 256 ? 2 * kWaves : kWaves; }
+// Queries per workgroup: 32 per query block.
+constexpr int queries_for(int d) { return 32 * waves_for(d) / slices_for(d); }
 constexpr int kXcds = 8;
 
 struct PrefillParams {
@@ -146,27 +147,34 @@ constexpr int blocks_per_tile() { return D <= 128 ? 2 : 1; }
 // moved as raw bits and only the matrix-core steps, the probabilities and the
 // output rounding differ.
 template <int D, bool Q8, bool BF>
-__global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillParams p) {
+__global__ __launch_bounds__(64 * waves_for(D)) void paged_prefill_kernel(const PrefillParams p) {
   static_assert(!(Q8 && BF), "8-bit K/V dequantizes to fp16");
   constexpr int KB = blocks_per_tile<D>();  // 32-key blocks per tile
   constexpr int kKeys = 32 * KB;            // keys per tile
   constexpr int kSlices = slices_for(D);    // waves sharing one query block
   constexpr int kDW = D / kSlices;          // head dims per wave
   constexpr int kQ = queries_for(D);        // queries per workgroup
+  constexpr int kW = waves_for(D);          // waves per workgroup
+  constexpr int kT = 64 * kW;               // threads per workgroup
+  // D = 512: one V tile in LDS (the partials take the second one's room); V
+  // of tile t + 1 is stored at the top of iteration t + 1, after every wave
+  // is done with V of tile t.
+  constexpr bool kOneV = kSlices > 1;
   constexpr int kKRow = D + 8;    // K row in LDS (halves): 16-lane 16-byte reads hit distinct banks
   constexpr int kVRow = D + 32;   // V row: the 4 rows of a transposed read hit distinct banks
-  constexpr int kTpk = kThreads / kKeys;               // gather threads per key
+  constexpr int kTpk = kT / kKeys;                     // gather threads per key
   constexpr int kPieces = D / 8 / kTpk;                // 16-byte pieces per thread and tile
   constexpr int kKeysPerWave = 64 / kTpk;              // keys one wave gathers
   static_assert(kPieces >= 1 && kPieces * kTpk * 8 == D, "tile shape");
   typedef typename std::conditional<kKeysPerWave == 16, uint16_t, uint8_t>::type okbits;
   typedef typename std::conditional<KB == 2, uint64_t, uint32_t>::type okword;
+  static_assert(kKeysPerWave * kW == kKeys, "usable-key bits");
   __shared__ __align__(16) f16 s_k[2][kKeys * kKRow];
-  __shared__ __align__(16) f16 s_v[2][kKeys * kVRow];
-  __shared__ __align__(8) okbits s_ok[2][kWaves];  // usable-key bits of the tile
+  __shared__ __align__(16) f16 s_v[kOneV ? 1 : 2][kKeys * kVRow];
+  __shared__ __align__(8) okbits s_ok[2][kW];  // usable-key bits of the tile
   // D = 512: each wave's partial scores (over its dims), summed by all the
   // waves of the query block.
-  __shared__ __align__(16) float4 s_x[kSlices > 1 ? kWaves * 4 * KB : 1][64];
+  __shared__ __align__(16) float4 s_x[kSlices > 1 ? kW * 4 * KB : 1][64];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -325,23 +333,41 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
       return x;
     }
   };
+  auto stash_v = [&](int vbuf) {
+    f16* vd = s_v[vbuf] + gk * kVRow + gp * 8;
+    if (__ballot(gok) == ~0ull) {
+#pragma unroll
+      for (int i = 0; i < kPieces; ++i)
+        *reinterpret_cast<f16x8*>(vd + 8 * kTpk * i) = as_f16(vr[i], vsc);
+    } else {
+#pragma unroll
+      for (int i = 0; i < kPieces; ++i)
+        *reinterpret_cast<f16x8*>(vd + 8 * kTpk * i) = gok ? as_f16(vr[i], vsc) : f16x8{};
+    }
+  };
   auto stash = [&](int buf) {
     // Unusable keys are stored as zeros (their weight is 0; zero V keeps
     // 0 * V finite whatever the arena holds there).
     f16* kd = s_k[buf] + gk * kKRow + gp * 8;
-    f16* vd = s_v[buf] + gk * kVRow + gp * 8;
     const uint64_t bits = __ballot(gok);
-    if (bits == ~0ull) {  // wave-uniform: the usual case stores without selects
+    if constexpr (kOneV) {
 #pragma unroll
-      for (int i = 0; i < kPieces; ++i) {
-        *reinterpret_cast<f16x8*>(kd + 8 * kTpk * i) = as_f16(kr[i], ksc);
-        *reinterpret_cast<f16x8*>(vd + 8 * kTpk * i) = as_f16(vr[i], vsc);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < kPieces; ++i) {
+      for (int i = 0; i < kPieces; ++i)
         *reinterpret_cast<f16x8*>(kd + 8 * kTpk * i) = gok ? as_f16(kr[i], ksc) : f16x8{};
-        *reinterpret_cast<f16x8*>(vd + 8 * kTpk * i) = gok ? as_f16(vr[i], vsc) : f16x8{};
+    } else {
+      f16* vd = s_v[buf] + gk * kVRow + gp * 8;
+      if (bits == ~0ull) {  // wave-uniform: the usual case stores without selects
+#pragma unroll
+        for (int i = 0; i < kPieces; ++i) {
+          *reinterpret_cast<f16x8*>(kd + 8 * kTpk * i) = as_f16(kr[i], ksc);
+          *reinterpret_cast<f16x8*>(vd + 8 * kTpk * i) = as_f16(vr[i], vsc);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < kPieces; ++i) {
+          *reinterpret_cast<f16x8*>(kd + 8 * kTpk * i) = gok ? as_f16(kr[i], ksc) : f16x8{};
+          *reinterpret_cast<f16x8*>(vd + 8 * kTpk * i) = gok ? as_f16(vr[i], vsc) : f16x8{};
+        }
       }
     }
     if (lane == 0) {
@@ -367,18 +393,24 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
   lookup(page1, in1, r1, s1);
   fetch(page0, in0, r0, s0);
   stash(0);
+  if constexpr (kOneV) stash_v(0);
   __syncthreads();
   for (int t = t_begin; t < t_end; ++t) {
     const int buf = (t - t_begin) & 1;
     const int k0 = kbase + t * kKeys;
     const bool more = t + 1 < t_end;
+    // V of this tile, staged in the previous iteration (every wave finished
+    // that tile's V at its closing barrier; the score exchange's barrier
+    // below publishes these stores before any wave reads them).
+    if constexpr (kOneV)
+      if (t > t_begin) stash_v(0);
     if (more) fetch(page1, in1, r1, s1);
     lookup(page1, in1, r1, s1);
 
     const bool work = wave_live && k0 <= wave_last &&
                       (p.window <= 0 || wave_img || k0 + kKeys - 1 > wfirst - p.window);
     const f16* sk = s_k[buf];
-    const f16* sv = s_v[buf];
+    const f16* sv = s_v[kOneV ? 0 : buf];
     // S^T per 32-key block kb: lane holds keys 32 kb + 8 (v / 4) + 4 hh + v % 4.
     f32x16 s[KB];
     if (work) {
@@ -432,7 +464,16 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(const PrefillPa
       }
     }
     if (work) {
-      const okword okm = *reinterpret_cast<const okword*>(s_ok[buf]);
+      okword okm;
+      if constexpr (kKeysPerWave == 4) {
+        // Eight waves of four keys: one nibble per byte, packed to 32 bits.
+        uint64_t x = *reinterpret_cast<const uint64_t*>(s_ok[buf]) & 0x0F0F0F0F0F0F0F0Full;
+        x = (x | (x >> 4)) & 0x00FF00FF00FF00FFull;
+        x = (x | (x >> 8)) & 0x0000FFFF0000FFFFull;
+        okm = (okword)(x | (x >> 16));
+      } else {
+        okm = *reinterpret_cast<const okword*>(s_ok[buf]);
+      }
       const bool edge = k0 + kKeys - 1 > wfirst || okm != (okword)~(okword)0 ||
                         (p.window > 0 && k0 <= wlast - p.window);
       // x = score in units that exp2(x * c - m) turns into the weight: the
@@ -758,7 +799,7 @@ int prefill(const void* queries, const void* keys, const void* values, const voi
                                : prefill_kernel_for<false, false>(head_dim);
   const hipStream_t hs = static_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)((int64_t)prm.tiles * q_heads * nsplit));
-  hipError_t err = hipLaunchKernel(fn, grid, dim3(kThreads), args, 0, hs);
+  hipError_t err = hipLaunchKernel(fn, grid, dim3(64 * waves_for(head_dim)), args, 0, hs);
   if (err != hipSuccess)
     return fail(PDA_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(err));
   if (nsplit > 1) {
