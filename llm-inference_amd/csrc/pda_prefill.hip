@@ -172,9 +172,10 @@ __global__ __launch_bounds__(64 * waves_for(D)) void paged_prefill_kernel(const 
   __shared__ __align__(16) f16 s_k[2][kKeys * kKRow];
   __shared__ __align__(16) f16 s_v[kOneV ? 1 : 2][kKeys * kVRow];
   __shared__ __align__(8) okbits s_ok[2][kW];  // usable-key bits of the tile
-  // D = 512: each wave's partial scores (over its dims), summed by all the
-  // waves of the query block.
+  // D = 512: each wave's partial scores (over its dims), and the sums of
+  // the query block's partials, one entry group per wave.
   __shared__ __align__(16) float4 s_x[kSlices > 1 ? kW * 4 * KB : 1][64];
+  __shared__ __align__(16) float4 s_y[kSlices > 1 ? kW * KB : 1][64];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -436,6 +437,7 @@ __global__ __launch_bounds__(64 * waves_for(D)) void paged_prefill_kernel(const 
       // Sum the slices' partial scores in slice order, so that every wave of
       // the block holds the same scores, maximum, sum and probabilities.
       // `work` is the same for all of them (it depends on the queries only).
+      // Reduce-scatter then gather: 12 adds per lane instead of 48.
       if (work) {
 #pragma unroll
         for (int i = 0; i < 4 * KB; ++i)
@@ -444,9 +446,13 @@ __global__ __launch_bounds__(64 * waves_for(D)) void paged_prefill_kernel(const 
                                                   s[i / 4][4 * (i % 4) + 3]);
       }
       __syncthreads();
+      // Reduce-scatter: slice sl sums entry group sl (and sl + 4 ...) of the
+      // four partials in slice order, then every wave reads the four sums.
+      static_assert(kSlices == 4, "one entry group per slice");
       if (work) {
 #pragma unroll
-        for (int i = 0; i < 4 * KB; ++i) {
+        for (int r = 0; r < KB; ++r) {
+          const int i = 4 * r + sl;
           float4 acc = s_x[qb * kSlices * 4 * KB + i][lane];
 #pragma unroll
           for (int j = 1; j < kSlices; ++j) {
@@ -456,6 +462,14 @@ __global__ __launch_bounds__(64 * waves_for(D)) void paged_prefill_kernel(const 
             acc.z += y.z;
             acc.w += y.w;
           }
+          s_y[w * KB + r][lane] = acc;
+        }
+      }
+      __syncthreads();
+      if (work) {
+#pragma unroll
+        for (int i = 0; i < 4 * KB; ++i) {
+          const float4 acc = s_y[(qb * kSlices + (i % 4)) * KB + i / 4][lane];
           s[i / 4][4 * (i % 4)] = acc.x;
           s[i / 4][4 * (i % 4) + 1] = acc.y;
           s[i / 4][4 * (i % 4) + 2] = acc.z;
