@@ -67,7 +67,9 @@ constexpr int kWaves = 4;  // waves per workgroup (D <= 256)
 // Waves that split the head dim: at D = 512 the query fragments and output
 // accumulators of 32 queries do not fit one wave's registers, so four waves
 // share 32 queries, each holding 128 dims of Q and O; a D = 512 workgroup has
-// eight waves (two such query blocks).
+// eight waves (two such query blocks). (Split the same way, D = 256 runs two
+// waves per SIMD instead of one but was 2-5% slower: the score exchange
+// costs more than the second wave hides.)
 constexpr int slices_for(int d) { return d > 256 ? 4 : 1; }
 constexpr int waves_for(int d) { return d > 256 ? 2 * kWaves : kWaves; }
 // Queries per workgroup: 32 per query block.
@@ -159,7 +161,10 @@ __global__ __launch_bounds__(64 * waves_for(D)) void paged_prefill_kernel(const 
   // D = 512: one V tile in LDS (the partials take the second one's room); V
   // of tile t + 1 is stored at the top of iteration t + 1, after every wave
   // is done with V of tile t.
-  constexpr bool kOneV = kSlices > 1;
+  constexpr bool kOneV = D > 256;
+  constexpr int kGroups = 4 * KB;             // float4 groups of a lane's scores
+  constexpr int kPer = kGroups / kSlices;     // groups each slice sums
+  static_assert(kPer * kSlices == kGroups, "score groups per slice");
   constexpr int kKRow = D + 8;    // K row in LDS (halves): 16-lane 16-byte reads hit distinct banks
   constexpr int kVRow = D + 32;   // V row: the 4 rows of a transposed read hit distinct banks
   constexpr int kTpk = kT / kKeys;                     // gather threads per key
@@ -173,9 +178,9 @@ __global__ __launch_bounds__(64 * waves_for(D)) void paged_prefill_kernel(const 
   __shared__ __align__(16) f16 s_v[kOneV ? 1 : 2][kKeys * kVRow];
   __shared__ __align__(8) okbits s_ok[2][kW];  // usable-key bits of the tile
   // D = 512: each wave's partial scores (over its dims), and the sums of
-  // the query block's partials, one entry group per wave.
-  __shared__ __align__(16) float4 s_x[kSlices > 1 ? kW * 4 * KB : 1][64];
-  __shared__ __align__(16) float4 s_y[kSlices > 1 ? kW * KB : 1][64];
+  // the query block's partials, kPer groups per wave.
+  __shared__ __align__(16) float4 s_x[kSlices > 1 ? kW * kGroups : 1][64];
+  __shared__ __align__(16) float4 s_y[kSlices > 1 ? kW * kPer : 1][64];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -437,39 +442,38 @@ __global__ __launch_bounds__(64 * waves_for(D)) void paged_prefill_kernel(const 
       // Sum the slices' partial scores in slice order, so that every wave of
       // the block holds the same scores, maximum, sum and probabilities.
       // `work` is the same for all of them (it depends on the queries only).
-      // Reduce-scatter then gather: 12 adds per lane instead of 48.
+      // Reduce-scatter then gather: 12 adds per lane instead of 48. Slice sl
+      // sums groups [sl kPer, (sl + 1) kPer) of the block's partials in
+      // slice order; then every wave reads all the sums.
       if (work) {
 #pragma unroll
-        for (int i = 0; i < 4 * KB; ++i)
-          s_x[w * 4 * KB + i][lane] = make_float4(s[i / 4][4 * (i % 4)], s[i / 4][4 * (i % 4) + 1],
-                                                  s[i / 4][4 * (i % 4) + 2],
-                                                  s[i / 4][4 * (i % 4) + 3]);
+        for (int i = 0; i < kGroups; ++i)
+          s_x[w * kGroups + i][lane] = make_float4(s[i / 4][4 * (i % 4)], s[i / 4][4 * (i % 4) + 1],
+                                                   s[i / 4][4 * (i % 4) + 2],
+                                                   s[i / 4][4 * (i % 4) + 3]);
       }
       __syncthreads();
-      // Reduce-scatter: slice sl sums entry group sl (and sl + 4 ...) of the
-      // four partials in slice order, then every wave reads the four sums.
-      static_assert(kSlices == 4, "one entry group per slice");
       if (work) {
 #pragma unroll
-        for (int r = 0; r < KB; ++r) {
-          const int i = 4 * r + sl;
-          float4 acc = s_x[qb * kSlices * 4 * KB + i][lane];
+        for (int r = 0; r < kPer; ++r) {
+          const int i = sl * kPer + r;
+          float4 acc = s_x[qb * kSlices * kGroups + i][lane];
 #pragma unroll
           for (int j = 1; j < kSlices; ++j) {
-            const float4 y = s_x[(qb * kSlices + j) * 4 * KB + i][lane];
+            const float4 y = s_x[(qb * kSlices + j) * kGroups + i][lane];
             acc.x += y.x;
             acc.y += y.y;
             acc.z += y.z;
             acc.w += y.w;
           }
-          s_y[w * KB + r][lane] = acc;
+          s_y[w * kPer + r][lane] = acc;
         }
       }
       __syncthreads();
       if (work) {
 #pragma unroll
-        for (int i = 0; i < 4 * KB; ++i) {
-          const float4 acc = s_y[(qb * kSlices + (i % 4)) * KB + i / 4][lane];
+        for (int i = 0; i < kGroups; ++i) {
+          const float4 acc = s_y[(qb * kSlices + i / kPer) * kPer + i % kPer][lane];
           s[i / 4][4 * (i % 4)] = acc.x;
           s[i / 4][4 * (i % 4) + 1] = acc.y;
           s[i / 4][4 * (i % 4) + 2] = acc.z;
