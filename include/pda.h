@@ -340,7 +340,7 @@ int pda_prefill_workspace_bytes(int32_t start, int32_t count, int32_t q_heads,
  * num_images is 0) lists image-token spans [begin, end) of positions: a
  * query inside a span also sees every key of that span up to the chunk's
  * end, whatever the causal limit and the window (batches.py:107-118).
- * head_dim in {64, 128, 256, 512} (512: the 512-wide heads of Gemma 4's
+ * head_dim in {64, 96, 128, 256, 512} (512: the 512-wide heads of Gemma 4's
  * global layers, docs/roadmap.md:36). With more than one key range
  * (see pda_prefill_workspace_bytes; results do not depend on `splits`
  * beyond fp32 rounding) the ranges' partials go to `workspace` (256-byte

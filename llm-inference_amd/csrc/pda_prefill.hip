@@ -166,7 +166,9 @@ __global__ __launch_bounds__(64 * waves_for(D)) void paged_prefill_kernel(const 
   constexpr int kPer = kGroups / kSlices;     // groups each slice sums
   static_assert(kPer * kSlices == kGroups, "score groups per slice");
   constexpr int kKRow = D + 8;    // K row in LDS (halves): 16-lane 16-byte reads hit distinct banks
-  constexpr int kVRow = D + 32;   // V row: the 4 rows of a transposed read hit distinct banks
+  // V row: the 4 rows of a transposed read hit distinct banks (a row is 16
+  // banks past the previous one modulo 64).
+  constexpr int kVRow = D % 64 == 32 ? D + 64 : D + 32;
   constexpr int kTpk = kT / kKeys;                     // gather threads per key
   constexpr int kPieces = D / 8 / kTpk;                // 16-byte pieces per thread and tile
   constexpr int kKeysPerWave = 64 / kTpk;              // keys one wave gathers
@@ -632,6 +634,8 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restr
                                                             f16* __restrict__ out, int64_t pairs,
                                                             int splits) {
   constexpr int kT = D / 4;
+  // 256 / kT pairs per block; at D = 96 the last 16 threads have none.
+  if (threadIdx.x >= 256 / kT * kT) return;
   const int64_t pair = (int64_t)blockIdx.x * (256 / kT) + threadIdx.x / kT;
   if (pair >= pairs) return;
   const int d = 4 * (threadIdx.x % kT);
@@ -671,7 +675,7 @@ int prefill_splits(int start, int count, int q_heads, int head_dim, int window, 
   if (request > 0) return request < kMaxSplits ? request : kMaxSplits;
   const int queries = queries_for(head_dim);
   const int64_t wgs = (int64_t)(count + queries - 1) / queries * q_heads;
-  const int occupancy = head_dim == 64 ? 3 : head_dim == 128 ? 2 : 1;
+  const int occupancy = head_dim == 64 ? 3 : head_dim <= 128 ? 2 : 1;
   const int64_t slots = (int64_t)kCus * occupancy;
   if (wgs * 2 > slots) return 1;
   const int keys = 32 * (head_dim <= 128 ? 2 : 1);
@@ -698,6 +702,7 @@ using pda_internal::ok;
 template <bool Q8, bool BF>
 const void* prefill_kernel_for(int head_dim) {
   return head_dim == 64    ? reinterpret_cast<const void*>(paged_prefill_kernel<64, Q8, BF>)
+         : head_dim == 96  ? reinterpret_cast<const void*>(paged_prefill_kernel<96, Q8, BF>)
          : head_dim == 128 ? reinterpret_cast<const void*>(paged_prefill_kernel<128, Q8, BF>)
          : head_dim == 256 ? reinterpret_cast<const void*>(paged_prefill_kernel<256, Q8, BF>)
                            : reinterpret_cast<const void*>(paged_prefill_kernel<512, Q8, BF>);
@@ -706,6 +711,7 @@ const void* prefill_kernel_for(int head_dim) {
 template <bool BF>
 const void* merge_kernel_for(int head_dim) {
   return head_dim == 64    ? reinterpret_cast<const void*>(prefill_merge_kernel<64, BF>)
+         : head_dim == 96  ? reinterpret_cast<const void*>(prefill_merge_kernel<96, BF>)
          : head_dim == 128 ? reinterpret_cast<const void*>(prefill_merge_kernel<128, BF>)
          : head_dim == 256 ? reinterpret_cast<const void*>(prefill_merge_kernel<256, BF>)
                            : reinterpret_cast<const void*>(prefill_merge_kernel<512, BF>);
@@ -726,8 +732,9 @@ int prefill(const void* queries, const void* keys, const void* values, const voi
                 count, start, q_heads, kv_heads, page_size, table_len, window, splits);
   if (q_heads % kv_heads)
     return fail(PDA_ERR_HEAD_RATIO, "query heads must be a multiple of kv heads");
-  if (head_dim != 64 && head_dim != 128 && head_dim != 256 && head_dim != 512)
-    return fail(PDA_ERR_HEAD_DIM, "head_dim %d has no prefill kernel (64, 128, 256, 512)",
+  if (head_dim != 64 && head_dim != 96 && head_dim != 128 && head_dim != 256 &&
+      head_dim != 512)
+    return fail(PDA_ERR_HEAD_DIM, "head_dim %d has no prefill kernel (64, 96, 128, 256, 512)",
                 head_dim);
   if (count == 0) return ok();
   if (table_len == 0)
@@ -848,8 +855,9 @@ int pda_prefill_workspace_bytes(int32_t start, int32_t count, int32_t q_heads,
   if (count < 0 || start < 0 || q_heads <= 0 || window < 0 || splits < 0 || !bytes)
     return fail(PDA_ERR_INVALID_ARGUMENT, "count=%d start=%d q_heads=%d window=%d splits=%d",
                 count, start, q_heads, window, splits);
-  if (head_dim != 64 && head_dim != 128 && head_dim != 256 && head_dim != 512)
-    return fail(PDA_ERR_HEAD_DIM, "head_dim %d has no prefill kernel (64, 128, 256, 512)",
+  if (head_dim != 64 && head_dim != 96 && head_dim != 128 && head_dim != 256 &&
+      head_dim != 512)
+    return fail(PDA_ERR_HEAD_DIM, "head_dim %d has no prefill kernel (64, 96, 128, 256, 512)",
                 head_dim);
   const int s = count == 0 ? 1 : prefill_splits(start, count, q_heads, head_dim, window, splits);
   if (splits_used) *splits_used = s;

@@ -191,7 +191,7 @@ def prefill(**overrides):
     (dict(splits=4, workspace=FAKE, workspace_bytes=1 << 20), _lib.PDA_ERR_WORKSPACE),
     (dict(splits=4, workspace=FAKE + 16, workspace_bytes=1 << 30), _lib.PDA_ERR_WORKSPACE),
     (dict(q_heads=30), _lib.PDA_ERR_HEAD_RATIO),
-    (dict(head_dim=96), _lib.PDA_ERR_HEAD_DIM),
+    (dict(head_dim=80), _lib.PDA_ERR_HEAD_DIM),
     (dict(start=(1 << 31) - 100), _lib.PDA_ERR_TOO_LONG),
     (dict(out=None), _lib.PDA_ERR_INVALID_ARGUMENT),
     (dict(table=None), _lib.PDA_ERR_INVALID_ARGUMENT),
@@ -234,11 +234,12 @@ def test_prefill_split_plan():
     assert _lib.prefill_workspace_bytes(0, 100, 8, 64, splits=500)[0] == 64
     assert _lib.prefill_workspace_bytes(0, 0, 8, 64, splits=3) == (1, 0)
     with pytest.raises(_lib.PdaError):
-        _lib.prefill_workspace_bytes(0, 10, 8, 96)
-    # 512-wide heads: 32 queries per workgroup, one workgroup per CU. A
-    # 64-token chunk at 8 heads is 16 workgroups; 16 ranges fill the 256 CUs.
+        _lib.prefill_workspace_bytes(0, 10, 8, 80)
+    # 512-wide heads: 64 queries per workgroup, one workgroup per CU. A
+    # 64-token chunk at 8 heads is 8 workgroups; 32 ranges would fill the
+    # 256 CUs, but a range keeps at least 8 key tiles: 6064 keys / 32 / 8 = 23.
     assert _lib.prefill_workspace_bytes(6000, 64, 8, 512) == (
-        16, 16 * 64 * 8 * 512 * 4 + 16 * 64 * 8 * 8)
+        23, 23 * 64 * 8 * 512 * 4 + ((23 * 64 * 8 * 8 + 255) // 256) * 256)
     assert _lib.prefill_workspace_bytes(0, 4096, 16, 512) == (1, 0)
 
 

@@ -438,3 +438,9 @@ def test_prefill_head_dim_512(gpu, layout):
     check_prefill(c, scale=512 ** -0.5, what=f"bf16 prefill D512 {layout}")
     check_prefill(c, scale=512 ** -0.5, splits=3, window=500,
                   what=f"bf16 prefill D512 3 ranges, window {layout}")
+
+
+def test_prefill_head_dim_96(gpu):
+    c = prefill_case(gpu, hq=32, hkv=8, d=96, start=700, count=200, seed=96)
+    check_prefill(c, scale=96 ** -0.5, what="bf16 prefill D96")
+    check_prefill(c, scale=96 ** -0.5, splits=4, what="bf16 prefill D96, 4 ranges")

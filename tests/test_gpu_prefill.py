@@ -383,3 +383,15 @@ def test_head_dim_512_8bit_cache(gpu, layout):
     err_max, err_mean = pa.error_stats(got.float().cpu().numpy(), want)
     print(f"D512 8-bit {layout}: max_abs={err_max:.3e} mean_abs={err_mean:.3e}", flush=True)
     assert err_max <= MAX_ABS and err_mean <= MEAN_ABS
+
+
+@pytest.mark.parametrize("layout", ["pages", "rows"])
+@pytest.mark.parametrize("start,count,splits", [(0, 300, 0), (900, 130, 3), (4000, 64, 0)])
+def test_head_dim_96(gpu, layout, start, count, splits):
+    """96-wide heads (padded V rows, a merge block with idle threads)."""
+    c = case(gpu, hq=32, hkv=8, d=96, start=start, count=count, layout=layout,
+             seed=start + count)
+    check(c, scale=96 ** -0.5, splits=splits,
+          what=f"D96 @{start}+{count} s{splits} {layout}")
+    check(c, scale=96 ** -0.5, window=200, softcap=30.0, images=[(start + 5, 20)],
+          what=f"D96 window+softcap+image {layout}")
