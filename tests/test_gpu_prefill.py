@@ -101,10 +101,12 @@ def test_forced_key_ranges(gpu, splits):
     check(c, scale=128 ** -0.5, splits=splits, what=f"splits {splits}")
 
 
-@pytest.mark.parametrize("d", [64, 256])
+@pytest.mark.parametrize("d", [64, 96, 256, 512])
 def test_forced_key_ranges_head_dims(gpu, d):
     c = case(gpu, hq=8, hkv=2, d=d, start=500, count=200, seed=d)
     check(c, scale=d ** -0.5, splits=3, what=f"D{d} splits 3")
+    # More ranges than key tiles: empty ranges leave m = -inf partials.
+    check(c, scale=d ** -0.5, splits=64, what=f"D{d} splits 64")
 
 
 def test_key_ranges_with_window_and_released_pages(gpu):
