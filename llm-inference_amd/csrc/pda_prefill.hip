@@ -43,6 +43,7 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <algorithm>
 #include <type_traits>
 
 #include "pda.h"
@@ -669,19 +670,24 @@ constexpr int kMaxSplits = 64;
 // every workgroup slot of the GPU (CUs x the kernel's occupancy) its work,
 // else as many as fit the slots in one round: the ranges of a chunk over a
 // long prefix are all alike, so a partly filled second round would cost a
-// whole range's time. Each range holds at least 8 key tiles. `request` > 0
-// forces a count.
+// whole range's time. One exception: a causal chunk that fills at most one
+// round and whose first query tile sees at most half the keys of its last
+// (a prompt from position 0) takes 2 ranges, so that the halves of its
+// longest tiles run beside its short ones. Each range holds at least 8 key
+// tiles. `request` > 0 forces a count.
 int prefill_splits(int start, int count, int q_heads, int head_dim, int window, int request) {
   if (request > 0) return request < kMaxSplits ? request : kMaxSplits;
   const int queries = queries_for(head_dim);
   const int64_t wgs = (int64_t)(count + queries - 1) / queries * q_heads;
   const int occupancy = head_dim == 64 ? 3 : head_dim <= 128 ? 2 : 1;
   const int64_t slots = (int64_t)kCus * occupancy;
-  if (wgs * 2 > slots) return 1;
   const int keys = 32 * (head_dim <= 128 ? 2 : 1);
-  int64_t span = (int64_t)start + count;
-  if (window > 0 && span > (int64_t)window + queries) span = (int64_t)window + queries;
+  // Keys seen by the chunk's first and last query tiles.
+  const int64_t cap = window > 0 ? (int64_t)window + queries : INT64_MAX;
+  const int64_t first = std::min<int64_t>((int64_t)start + std::min(count, queries), cap);
+  const int64_t span = std::min<int64_t>((int64_t)start + count, cap);
   const int64_t by_keys = (span + keys - 1) / keys / 8;
+  if (wgs * 2 > slots) return wgs <= slots && 2 * first <= span && by_keys >= 2 ? 2 : 1;
   int64_t s = slots / wgs;
   if (s > by_keys) s = by_keys;
   if (s > kMaxSplits) s = kMaxSplits;

@@ -241,6 +241,13 @@ def test_prefill_split_plan():
     assert _lib.prefill_workspace_bytes(6000, 64, 8, 512) == (
         23, 23 * 64 * 8 * 512 * 4 + ((23 * 64 * 8 * 8 + 255) // 256) * 256)
     assert _lib.prefill_workspace_bytes(0, 4096, 16, 512) == (1, 0)
+    # A prompt from position 0 that fills at most one round: its tiles' key
+    # counts differ up to 32x, and 2 ranges let the long tiles' halves run
+    # beside the short ones.
+    assert _lib.prefill_workspace_bytes(0, 4096, 14, 64)[0] == 2
+    assert _lib.prefill_workspace_bytes(0, 2048, 16, 256)[0] == 2
+    assert _lib.prefill_workspace_bytes(0, 2048, 16, 512)[0] == 1  # two rounds
+    assert _lib.prefill_workspace_bytes(0, 4096, 14, 64, window=256)[0] == 1  # tiles alike
 
 
 def test_prefill_q8_validation():
