@@ -397,3 +397,67 @@ def test_head_dim_96(gpu, layout, start, count, splits):
           what=f"D96 @{start}+{count} s{splits} {layout}")
     check(c, scale=96 ** -0.5, window=200, softcap=30.0, images=[(start + 5, 20)],
           what=f"D96 window+softcap+image {layout}")
+
+
+@pytest.mark.parametrize("layout", ["pages", "rows"])
+def test_global_layer_512_wide_quarter_rotation(gpu, layout):
+    """A Gemma 4 global layer end to end (gemma4.py:49-75): 512-wide heads
+    whose first quarter of dims is rotated. PrefillBatch in two chunks (the
+    model's rope, then attend), then two DecodeBatch.rope_attend steps, each
+    against the RoPE oracle and the attention oracle over the arena the
+    kernels wrote."""
+    from instinct_amd.batches import DecodeBatch
+    from oracle import rope_append as ra
+
+    page, hq, hkv, d, dims, base = 16, 8, 2, 512, 128, 1e6
+    groups = [KVGroup("full", (0,), kv_heads=hkv, head_dim=d)]
+    cache = KVCache(groups, page_size=page, capacities={"full": 32}, device=gpu, layout=layout)
+    n = 200
+    table = np.array([cache.pools["full"].allocate(reserved=False) for _ in range(16)])
+    gen = torch.Generator(device=gpu).manual_seed(12)
+    q = torch.randn((n + 2, hq, d), generator=gen, device=gpu).half()
+    k = torch.randn((n + 2, hkv, d), generator=gen, device=gpu).half()
+    v = torch.randn((n + 2, hkv, d), generator=gen, device=gpu).half()
+    inverse = ra.inv_freq(dims, base=base)
+
+    def arena():
+        keys, values = cache.keys[0], cache.values[0]
+        if layout == "pages":
+            keys, values = pages_to_rows(keys), pages_to_rows(values)
+        return keys.cpu().numpy(), values.cpu().numpy()
+
+    outs, q_rots = [], []
+    for a, b in ((0, 120), (120, n)):
+        chunk = PrefillBatch(cache, torch.zeros(b - a, device=gpu), start=a,
+                             tables={"full": table})
+        q_rot = chunk.rope(q[a:b], dims, base=base)
+        k_rot = chunk.rope(k[a:b], dims, base=base)
+        pos = np.arange(a, b, dtype=np.int32)
+        np.testing.assert_array_equal(
+            k_rot.cpu().numpy()[..., dims:], k[a:b].cpu().numpy()[..., dims:])
+        assert np.abs(q_rot.cpu().numpy().astype(np.float64)
+                      - ra.rope(q[a:b].cpu().numpy(), pos, dims, inverse)).max() <= 2e-3
+        q_rots.append(q_rot)
+        outs.append(chunk.attend(0, q_rot, k_rot, v[a:b], scale=d ** -0.5))
+    torch.cuda.synchronize()
+    keys, values = arena()
+    want = pa.paged_prefill_dense(torch.cat(q_rots).cpu().numpy(), keys, values, table,
+                                  start=0, page_size=page, scale=d ** -0.5)
+    err_max, err_mean = pa.error_stats(torch.cat(outs).view(n, hq, d).float().cpu().numpy(),
+                                       want)
+    print(f"D512 global layer prefill {layout}: max_abs={err_max:.3e} mean_abs={err_mean:.3e}")
+    assert err_max <= MAX_ABS and err_mean <= MEAN_ABS
+    for t in (n, n + 1):
+        step = DecodeBatch(cache, torch.zeros(1, device=gpu), positions=np.array([t]),
+                           tables={"full": [table]})
+        out = step.rope_attend(0, q[t:t + 1], k[t:t + 1], v[t:t + 1], dims=dims, base=base,
+                               scale=d ** -0.5)
+        torch.cuda.synchronize()
+        keys, values = arena()
+        q_rot = ra.rope(q[t:t + 1].cpu().numpy(), np.array([t], np.int32), dims, inverse)
+        want = pa.paged_decode_dense(q_rot, keys, values, table[None].astype(np.int32),
+                                     np.array([t + 1], np.int32), page_size=page,
+                                     scale=d ** -0.5)
+        err_max, err_mean = pa.error_stats(out.view(1, hq, d).float().cpu().numpy(), want)
+        print(f"D512 global layer decode step {t} {layout}: max_abs={err_max:.3e}")
+        assert err_max <= MAX_ABS and err_mean <= MEAN_ABS
