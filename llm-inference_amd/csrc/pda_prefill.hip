@@ -12,11 +12,15 @@
 //
 // MI355X design (a flash-attention tile loop on the matrix cores):
 //  * Workgroup = 4 waves = one query head and 128 queries (32 per wave).
-//    Keys are streamed in tiles of 32 through LDS, K and V rows gathered from
-//    the pages of the sequence's table (either arena layout). The LDS holds
-//    two tiles: the loads of tile t + 1 are issued into registers before the
-//    math of tile t and stored to the other half after it, one barrier per
-//    tile.
+//    Keys are streamed in tiles of 64 (32 at D >= 256) through LDS, K and V
+//    rows gathered from the pages of the sequence's table (either arena
+//    layout). The LDS holds two tiles: the loads of tile t + 1 are issued
+//    into registers before the math of tile t and stored to the other half
+//    after it, one barrier per tile.
+//  * D = 512: eight waves, two blocks of 32 queries; the four waves of a
+//    block split the head dim (128 dims of Q and O each) and sum their
+//    partial scores through LDS, so every wave of the block holds the same
+//    scores and probabilities (see slices_for).
 //  * Each wave computes S^T = K Q^T for its 32 queries with
 //    v_mfma_f32_32x32x16_f16 (D / 16 instructions per key tile), Q held in
 //    registers. In that product's accumulator a lane holds 16 keys of one
