@@ -191,8 +191,10 @@ def rope_inv_freq(dims: int, *, base: float | None = None, freqs: Any = None,
     return table
 
 
-def _check_f16(name: str, t: torch.Tensor, dims: int,
-               dtype: torch.dtype = torch.float16) -> None:
+def _check_half(name: str, t: torch.Tensor, dims: int,
+                dtype: torch.dtype = torch.float16) -> None:
+    """A contiguous GPU tensor of ``dims`` dimensions in a 16-bit float type
+    (fp16, or bf16 where the caller asks for it)."""
     if t.dtype != dtype:
         raise TypeError(f"{name} must be {str(dtype).replace('torch.', '')}, got {t.dtype}")
     if not t.is_cuda:
@@ -270,10 +272,10 @@ def rope_append(q: torch.Tensor | None, k: torch.Tensor, v: torch.Tensor,
     bf16 = k.dtype == torch.bfloat16 and scales is None
     dtype = torch.bfloat16 if bf16 else torch.float16
     for name, t, d in (("k", k, 3), ("v", v, 3)):
-        _check_f16(name, t, d, dtype)
+        _check_half(name, t, d, dtype)
     if scales is None:
         for name, t in (("keys", keys), ("values", values)):
-            _check_f16(name, t, keys.dim(), dtype)
+            _check_half(name, t, keys.dim(), dtype)
     else:
         scale_shape = ((arena_rows, kv_heads) if layout == _lib.PDA_LAYOUT_ROWS
                        else (arena_rows // page_size, kv_heads, page_size))
@@ -291,13 +293,13 @@ def rope_append(q: torch.Tensor | None, k: torch.Tensor, v: torch.Tensor,
         raise ValueError("k does not match the arena's kv_heads and head_dim")
     q_heads = 0
     if q is not None:
-        _check_f16("q", q, 3, dtype)
+        _check_half("q", q, 3, dtype)
         if int(q.shape[0]) != n or int(q.shape[2]) != head_dim:
             raise ValueError("q must be [n, q_heads, head_dim]")
         q_heads = int(q.shape[1])
         if q_out is None:
             q_out = torch.empty_like(q)
-        _check_f16("q_out", q_out, 3, dtype)
+        _check_half("q_out", q_out, 3, dtype)
         if q_out.shape != q.shape:
             raise ValueError("q_out must have q's shape")
     rows = _int32_vector("rows", rows, n)
@@ -321,7 +323,7 @@ def rope(x: torch.Tensor, positions: torch.Tensor, dims: int, *, base: float | N
     one position per token (non-traditional RoPE, portable.py:88-132);
     ``x`` fp16 or bf16, the result in ``x``'s dtype."""
     bf16 = x.dtype == torch.bfloat16
-    _check_f16("x", x, 3, torch.bfloat16 if bf16 else torch.float16)
+    _check_half("x", x, 3, torch.bfloat16 if bf16 else torch.float16)
     n, heads, head_dim = (int(s) for s in x.shape)
     if out is None:
         out = torch.empty_like(x)
@@ -414,7 +416,7 @@ def paged_prefill_attention(queries: torch.Tensor, keys: torch.Tensor, values: t
     q8 = scales is not None
     bf16 = queries.dtype == torch.bfloat16 and not q8
     dtype = torch.bfloat16 if bf16 else torch.float16
-    _check_f16("queries", queries, 3, dtype)
+    _check_half("queries", queries, 3, dtype)
     count, q_heads, head_dim = (int(x) for x in queries.shape)
     layout, arena_rows, kv_heads, a_dim = _arena_geometry(keys, page_size)
     for name, t in (("keys", keys), ("values", values)):
@@ -422,7 +424,7 @@ def paged_prefill_attention(queries: torch.Tensor, keys: torch.Tensor, values: t
             if t.dtype != torch.int8 or not t.is_cuda or not t.is_contiguous():
                 raise TypeError(f"{name} must be a contiguous int8 GPU tensor")
         else:
-            _check_f16(name, t, keys.dim(), dtype)
+            _check_half(name, t, keys.dim(), dtype)
     if q8:
         scale_shape = tuple(keys.shape[:-1])
         for name, t in zip(("key_scales", "value_scales"), scales):
@@ -442,7 +444,7 @@ def paged_prefill_attention(queries: torch.Tensor, keys: torch.Tensor, values: t
     if out is None:
         out = torch.empty_like(queries)
     else:
-        _check_f16("out", out, 3, dtype)
+        _check_half("out", out, 3, dtype)
         if tuple(out.shape) != tuple(queries.shape):
             raise ValueError("out must have the queries' shape")
     if count == 0:
