@@ -37,12 +37,20 @@ from . import _lib
 _workspaces: dict[tuple[int, int], torch.Tensor] = {}
 
 
-def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """A cached, 256-byte aligned device workspace of at least ``nbytes``,
-    grown on demand and shared by calls of any shape (it holds nothing
-    between calls)."""
+def stream_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """A cached, 256-byte aligned device workspace of at least ``nbytes`` for
+    the current stream of ``device``, grown on demand and shared by calls of
+    any shape on that stream (it holds nothing between calls, and calls on
+    one stream never overlap). Calls on different streams get different
+    buffers.
+
+    Growing replaces the stream's buffer; the caching allocator only reuses
+    the old one for work ordered after the replacement on the same stream.
+    Code that records a workspace address for later (a captured graph) must
+    pass a workspace it owns instead (``workspace=`` of the calls), as
+    :class:`instinct_amd.step.DecodeStepGraph` does."""
     index = device.index if device.index is not None else torch.cuda.current_device()
-    key = (index, 0)
+    key = (index, int(torch.cuda.current_stream(index).cuda_stream))
     buf = _workspaces.get(key)
     if buf is None or buf.numel() < nbytes:
         size = max(nbytes, 1 << 20)
@@ -51,6 +59,28 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
         buf = torch.empty(size, dtype=torch.uint8, device=device)
         _workspaces[key] = buf
     return buf
+
+
+def _given_workspace(ws: torch.Tensor, device: torch.device, nbytes: int) -> torch.Tensor:
+    """A caller's workspace: a contiguous uint8 tensor on ``device``, 256-byte
+    aligned, of at least ``nbytes``."""
+    if ws.dtype != torch.uint8 or not ws.is_contiguous() or ws.device != device:
+        raise ValueError("workspace must be a contiguous uint8 tensor on the queries' device")
+    if ws.numel() < nbytes:
+        raise ValueError(f"workspace of {nbytes} bytes needed, {ws.numel()} given")
+    if ws.data_ptr() % 256:
+        raise ValueError("workspace must be 256-byte aligned")
+    return ws
+
+
+def decode_workspace_bytes(queries_shape: tuple[int, int, int], keys: torch.Tensor, *,
+                           page_size: int, table_width: int, longest: int, window: int = 0,
+                           split_pages: int = 0) -> int:
+    """Bytes of workspace :func:`paged_decode_attention` needs for this shape
+    (``pda_workspace_bytes``)."""
+    batch, q_heads, head_dim = (int(n) for n in queries_shape)
+    return _lib.workspace_bytes(batch, q_heads, int(keys.shape[1]), head_dim, int(page_size),
+                                int(table_width), int(longest), int(window), int(split_pages))
 
 
 def paged_decode_attention(
@@ -69,12 +99,15 @@ def paged_decode_attention(
     split_pages: int = 0,
     out: torch.Tensor | None = None,
     passes: str = "both",
+    workspace: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Attention for one new token per sequence over its paged keys
     (metal_kernels.py:164-186). ``split_pages`` is the fewest pages a wave
     reads before the batch is spread over fewer waves (0 = default); the
     result does not depend on it. ``passes`` = "split" or "merge" launches
     one of the two kernels only (the output is complete after the merge).
+    ``workspace``: a uint8 device tensor the caller owns (at least
+    :func:`decode_workspace_bytes`), else the stream's cached one.
 
     ``scales`` = (key_scales, value_scales) selects 8-bit K/V
     (metal_kernels.py:134-141): ``keys``/``values`` are int8 arenas and the
@@ -132,7 +165,8 @@ def paged_decode_attention(
     stride = int(tables.shape[1])
     need = _lib.workspace_bytes(batch, q_heads, kv_heads, head_dim, page_size, stride,
                                 int(longest), int(window), int(split_pages))
-    ws = workspace(device, need)
+    ws = (stream_workspace(device, need) if workspace is None
+          else _given_workspace(workspace, device, need))
     stream = torch.cuda.current_stream(device).cuda_stream
     if out.dtype != q_dtype or tuple(out.shape) != tuple(queries.shape) or not out.is_cuda:
         raise ValueError("out must match the queries' shape and dtype")
@@ -398,7 +432,8 @@ def paged_prefill_attention(queries: torch.Tensor, keys: torch.Tensor, values: t
                             table: torch.Tensor, *, start: int, page_size: int, scale: float,
                             window: int = 0, softcap: float = 0.0, splits: int = 0,
                             scales: tuple[Any, Any] | None = None, images: Any = (),
-                            out: torch.Tensor | None = None) -> torch.Tensor:
+                            out: torch.Tensor | None = None,
+                            workspace: torch.Tensor | None = None) -> torch.Tensor:
     """Attention of one prompt chunk (``PrefillBatch.attend``,
     batches.py:84-132): ``queries`` ``[count, q_heads, D]`` at positions
     ``start ..`` over the sequence's keys in the arena (either layout, the
@@ -412,7 +447,9 @@ def paged_prefill_attention(queries: torch.Tensor, keys: torch.Tensor, values: t
     spans of image tokens, or an int32 GPU tensor ``[n, 2]`` of [begin, end)
     positions; a query inside one also sees the span's later keys
     (batches.py:107-118). bf16 queries with bf16 arenas (bf16 models) give a
-    bf16 output; the 8-bit cache takes fp16 queries."""
+    bf16 output; the 8-bit cache takes fp16 queries. ``workspace``: a uint8
+    device tensor the caller owns (at least the ``pda_prefill_workspace_bytes``
+    of the call), else the stream's cached one."""
     q8 = scales is not None
     bf16 = queries.dtype == torch.bfloat16 and not q8
     dtype = torch.bfloat16 if bf16 else torch.float16
@@ -451,7 +488,10 @@ def paged_prefill_attention(queries: torch.Tensor, keys: torch.Tensor, values: t
         return out
     _, need = _lib.prefill_workspace_bytes(int(start), count, q_heads, head_dim, int(window),
                                            int(splits))
-    ws = workspace(queries.device, need) if need else None
+    ws = None
+    if need:
+        ws = (stream_workspace(queries.device, need) if workspace is None
+              else _given_workspace(workspace, queries.device, need))
     stream = torch.cuda.current_stream(queries.device).cuda_stream
     spans = image_spans(images, queries.device)
     entry = "pda_paged_prefill_attention" + ("_q8" if q8 else "_bf16" if bf16 else "")

@@ -21,7 +21,6 @@ reallocates.
 
 from __future__ import annotations
 
-import heapq
 from collections.abc import Iterable, Sequence
 from dataclasses import dataclass
 
@@ -50,7 +49,9 @@ def pages_to_rows(arena: torch.Tensor) -> torch.Tensor:
 
 @dataclass(frozen=True)
 class KVGroup:
-    """Attention layers that share a K/V shape and window (paged_kv.py:34-47)."""
+    """A set of attention layers whose K/V arenas share one shape, one window
+    and one page pool. The fields are the reference's group description
+    (paged_kv.py:34-47), so an engine hands its groups over unchanged."""
 
     name: str
     layers: tuple[int, ...]
@@ -59,81 +60,151 @@ class KVGroup:
     window: int = 0  # 0 for full attention
 
     def bytes_per_token(self, bits: int = 16) -> int:
-        row = self.head_dim * bits // 8 + (2 if bits == 8 else 0)
-        return 2 * len(self.layers) * self.kv_heads * row
+        """HBM bytes one token costs over the group's layers: a K and a V row
+        per kv head, plus one fp16 scale per row at 8 bits."""
+        per_head = self.head_dim * bits // 8 + (2 if bits == 8 else 0)
+        return len(self.layers) * 2 * self.kv_heads * per_head
+
+
+_WORD = 64
 
 
 class PagePool:
-    """Physical page ids with reference counts and reservations
-    (paged_kv.py:79-153): the lowest free id is handed out first, so the arena
-    only has to cover the high-water mark; ``retain``/``release`` let several
-    tables hold one page (prefix sharing)."""
+    """Physical page ids of one group: reference counts, reservations, and
+    the lowest free id handed out first, so the arena only has to cover the
+    high-water mark (the reference's contract, paged_kv.py:79-153).
+
+    Design: the free pages are a bitmap of 64-bit words (bit set = free),
+    and a Python integer summarises it (bit w set = word w holds a free
+    page), so the lowest free id is two lowest-set-bit steps away whatever
+    the capacity. Reference counts live in an int32 vector; :meth:`retain`
+    and :meth:`release` take whole page lists (a shared prefix of 128
+    pages, the pages a window trim drops) and update them with a few vector
+    operations. Both check the whole list before changing anything, so a
+    bad id leaves the pool as it was. Negative ids (released table entries,
+    mlx_engine.py:349-372) are ignored."""
 
     def __init__(self, capacity: int) -> None:
         if capacity <= 0:
             raise ValueError("a page pool needs at least one page")
-        self.capacity = capacity
-        self._free = list(range(capacity))
-        self._refs = np.zeros(capacity, dtype=np.int32)
+        self.capacity = int(capacity)
+        words = -(-self.capacity // _WORD)
+        self._bits = np.full(words, np.iinfo(np.uint64).max, dtype=np.uint64)
+        tail = self.capacity - (words - 1) * _WORD
+        if tail < _WORD:
+            self._bits[-1] = np.uint64((1 << tail) - 1)
+        self._summary = (1 << words) - 1
+        self._refs = np.zeros(self.capacity, dtype=np.int32)
+        self._free_count = self.capacity
         self.reserved = 0
         self.high_water = 0
 
+    # Counts -------------------------------------------------------------
     @property
     def free(self) -> int:
-        return len(self._free)
+        """Pages no table holds."""
+        return self._free_count
 
     @property
     def available(self) -> int:
-        return len(self._free) - self.reserved
+        """Free pages not promised to a reservation."""
+        return self._free_count - self.reserved
 
     @property
     def used(self) -> int:
-        return self.capacity - len(self._free)
+        return self.capacity - self._free_count
 
+    def refcount(self, page: int) -> int:
+        return int(self._refs[page])
+
+    def shared(self, page: int) -> bool:
+        """More than one table holds the page (copy-on-write needed)."""
+        return bool(self._refs[page] > 1)
+
+    # Reservations --------------------------------------------------------
     def reserve(self, count: int) -> bool:
+        """Promise ``count`` free pages to a request; False if they are not there."""
+        if count < 0:
+            raise ValueError("cannot reserve a negative page count")
         if count > self.available:
             return False
         self.reserved += count
         return True
 
     def unreserve(self, count: int) -> None:
-        if not 0 <= count <= self.reserved:
-            raise RuntimeError("released more pages than were reserved")
+        if count < 0 or count > self.reserved:
+            raise RuntimeError(f"cannot return {count} of {self.reserved} reserved pages")
         self.reserved -= count
 
-    def allocate(self, *, reserved: bool) -> int:
-        """Take one page, from the caller's reservation if ``reserved``."""
+    # Allocation -------------------------------------------------------------
+    def _take(self, count: int) -> list[int]:
+        pages: list[int] = []
+        while len(pages) < count:
+            w = (self._summary & -self._summary).bit_length() - 1
+            word = int(self._bits[w])
+            base = w * _WORD
+            while word and len(pages) < count:
+                low = word & -word
+                pages.append(base + low.bit_length() - 1)
+                word ^= low
+            self._bits[w] = np.uint64(word)
+            if not word:
+                self._summary &= ~(1 << w)
+        return pages
+
+    def allocate_many(self, count: int, *, reserved: bool) -> np.ndarray:
+        """The ``count`` lowest free ids, each with one reference; drawn from
+        the caller's reservation if ``reserved``."""
+        if count < 0:
+            raise ValueError("cannot allocate a negative page count")
         if reserved:
-            self.unreserve(1)
-        elif self.available <= 0:
-            raise RuntimeError("the K/V page pool is exhausted")
-        page = heapq.heappop(self._free)
-        self._refs[page] = 1
-        self.high_water = max(self.high_water, page + 1)
-        return page
+            self.unreserve(count)
+        elif count > self.available:
+            raise RuntimeError(f"the K/V page pool is exhausted ({count} pages asked, "
+                               f"{self.available} available)")
+        pages = np.asarray(self._take(count), dtype=np.int64)
+        self._refs[pages] = 1
+        self._free_count -= count
+        if count:
+            self.high_water = max(self.high_water, int(pages[-1]) + 1)
+        return pages
+
+    def allocate(self, *, reserved: bool) -> int:
+        """The lowest free id, with one reference."""
+        return int(self.allocate_many(1, reserved=reserved)[0])
+
+    # Sharing -----------------------------------------------------------------
+    def _held(self, pages: Iterable[int]) -> tuple[np.ndarray, np.ndarray]:
+        ids = np.asarray(list(pages) if not isinstance(pages, np.ndarray) else pages,
+                         dtype=np.int64).ravel()
+        ids = ids[ids >= 0]
+        if ids.size and int(ids.max()) >= self.capacity:
+            raise RuntimeError(f"page {int(ids.max())} is outside a pool of {self.capacity}")
+        unique, counts = np.unique(ids, return_counts=True)
+        return unique, counts.astype(np.int32)
 
     def retain(self, pages: Iterable[int]) -> None:
-        for page in pages:
-            if page >= 0:
-                if self._refs[page] <= 0:
-                    raise RuntimeError("retained a page that isn't allocated")
-                self._refs[page] += 1
+        """One more reference to each listed page (a table that now shares it)."""
+        unique, counts = self._held(pages)
+        if np.any(self._refs[unique] <= 0):
+            raise RuntimeError("cannot share a page that is not allocated")
+        self._refs[unique] += counts
 
     def release(self, pages: Iterable[int]) -> None:
-        for page in pages:
-            if page < 0:
-                continue
-            if self._refs[page] <= 0:
-                raise RuntimeError("released a page that isn't allocated")
-            self._refs[page] -= 1
-            if self._refs[page] == 0:
-                heapq.heappush(self._free, page)
-
-    def shared(self, page: int) -> bool:
-        return bool(self._refs[page] > 1)
-
-    def held_only_by(self, counts: np.ndarray) -> int:
-        return int(np.count_nonzero((counts > 0) & (self._refs == counts)))
+        """Drop one reference per listed occurrence; pages left with none
+        become free."""
+        unique, counts = self._held(pages)
+        if np.any(self._refs[unique] < counts):
+            raise RuntimeError("cannot release a page more often than it is held")
+        self._refs[unique] -= counts
+        freed = unique[self._refs[unique] == 0]
+        if freed.size:
+            words = freed // _WORD
+            masks = np.left_shift(np.uint64(1), (freed % _WORD).astype(np.uint64))
+            np.bitwise_or.at(self._bits, words, masks)
+            for w in np.unique(words).tolist():
+                self._summary |= 1 << w
+            self._free_count += int(freed.size)
 
 
 class KVCache:

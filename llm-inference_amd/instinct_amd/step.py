@@ -24,7 +24,8 @@ from typing import Any
 
 import torch
 
-from .hip_kernels import pack_decode_step, paged_decode_attention, rope_append
+from .hip_kernels import (decode_workspace_bytes, pack_decode_step, paged_decode_attention,
+                          rope_append)
 
 
 class DecodeStepGraph:
@@ -68,6 +69,12 @@ class DecodeStepGraph:
         self.rows = torch.zeros(batch, **i32)
         self.q_rot = [torch.zeros_like(q) for q in self.q]
         self.out = [torch.zeros_like(q) for q in self.q]
+        # The decode calls' workspace, owned by this object: a captured graph
+        # holds its address, so it must live as long as the graph and never
+        # be shared with calls outside it (whose workspace may be replaced).
+        need = decode_workspace_bytes((batch, q_heads, head_dim), keys, page_size=page_size,
+                                      table_width=width, longest=longest, window=window)
+        self.workspace = torch.empty(need, dtype=torch.uint8, device=dev)
         self.graph: torch.cuda.CUDAGraph | None = None
 
     def run(self) -> None:
@@ -82,11 +89,14 @@ class DecodeStepGraph:
                         self.positions, self.rows, q_out=self.q_rot[layer], scales=scales,
                         page_size=self.page_size, **self.rope)
             paged_decode_attention(self.q_rot[layer], keys, values, self.tables, self.lengths,
-                                   out=self.out[layer], scales=scales, **self.kw)
+                                   out=self.out[layer], scales=scales,
+                                   workspace=self.workspace, **self.kw)
 
     def capture(self) -> None:
-        """Capture :meth:`run` (after one eager run that sizes and allocates
-        the decode workspace outside the capture)."""
+        """Capture :meth:`run` (after one eager run outside the capture).
+        Every buffer the graph touches belongs to this object or to the
+        caller (arenas, resident tables), so nothing it recorded is freed
+        while the object lives."""
         self.run()
         torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()

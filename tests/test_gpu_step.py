@@ -126,3 +126,86 @@ def test_graph_replays_match_eager_steps(gpu, layout, bits, dtype):
             assert torch.equal(cache_g.values[layer], cache_e.values[layer])
         # Eager work of the program between replays.
         torch.ones(1 << 20, device=gpu).sum().item()
+
+
+def test_graph_keeps_its_workspace_when_the_stream_cache_grows(gpu):
+    """A captured step records its decode workspace's address. Calls outside
+    the graph on the same stream may grow (replace) the stream's cached
+    workspace, e.g. a prefill chunk over a long prefix, and the allocator may
+    hand the old buffer to new tensors. The graph owns its workspace, so a
+    replay after that writes nothing into those tensors and still matches
+    the eager step."""
+    layers, batch = 2, 6
+    cache_g, start, slot_lists, seq_tables, width, hq = setup(gpu, "pages", 16, layers, batch)
+    cache_e, *_ = setup(gpu, "pages", 16, layers, batch)
+    arenas = [(cache_g.keys[l], cache_g.values[l]) for l in range(layers)]
+    # An eager decode call first, so the stream's cache holds a decode-sized buffer.
+    q0 = torch.randn((batch, hq, 128), device=gpu, dtype=torch.float16)
+    t0 = torch.as_tensor(np.array(slot_lists, dtype=np.int32), device=gpu)
+    l0 = torch.as_tensor(start.astype(np.int32) + 1, device=gpu)
+    hip_kernels.paged_decode_attention(q0, cache_g.keys[0], cache_g.values[0], t0, l0,
+                                       page_size=16, longest=int(l0.max()), scale=0.1)
+    torch.cuda.synchronize()
+    step = DecodeStepGraph(arenas, seq_tables, batch=batch, q_heads=hq, page_size=16,
+                           width=width, scale=128 ** -0.5, longest=int(start.max()) + 8,
+                           dims=128, base=1e6)
+    slots = np.arange(batch, dtype=np.int32)
+    gen = torch.Generator(device=gpu).manual_seed(5)
+
+    def load_step(t):
+        positions = (start + t).astype(np.int32)
+        step.slots.copy_(torch.as_tensor(slots, device=gpu))
+        step.positions.copy_(torch.as_tensor(positions, device=gpu))
+        qkv = []
+        for layer in range(layers):
+            q = torch.randn((batch, hq, 128), generator=gen, device=gpu).half()
+            k = torch.randn((batch, 4, 128), generator=gen, device=gpu).half()
+            v = torch.randn((batch, 4, 128), generator=gen, device=gpu).half()
+            step.q[layer].copy_(q)
+            step.k[layer].copy_(k)
+            step.v[layer].copy_(v)
+            qkv.append((q, k, v))
+        return positions, qkv
+
+    def check(positions, qkv):
+        batch_e = DecodeBatch(cache_e, torch.zeros(batch, device=gpu), positions=positions,
+                              tables={"full": [np.array(slot_lists[s]) for s in slots]})
+        for layer, (q, k, v) in enumerate(qkv):
+            want = batch_e.rope_attend(layer, q, k, v, dims=128, base=1e6, scale=128 ** -0.5)
+            torch.cuda.synchronize()
+            d = (step.out[layer].reshape(batch, -1).float() - want.float()).abs()
+            assert d.max().item() <= MAX_ABS and d.mean().item() <= MEAN_ABS
+
+    positions, qkv = load_step(0)
+    step.capture()
+    torch.cuda.synchronize()
+    check(positions, qkv)
+    before = hip_kernels.stream_workspace(gpu, 0)
+    old_bytes, old_ptr = before.numel(), before.data_ptr()
+    del before
+    # A 512-token prefill chunk over a 32256-token prefix: its key ranges
+    # need a workspace larger than the decode call's, so the stream's cached
+    # buffer is replaced (and the old one returned to the allocator).
+    P, hkv, d, pos0, count = 16, 4, 128, 32256, 512
+    pages = (pos0 + count) // P
+    pk = torch.randn((pages, hkv, P, d), device=gpu, dtype=torch.float16)
+    pv = torch.randn_like(pk)
+    table = torch.as_tensor(np.random.default_rng(3).permutation(pages).astype(np.int32),
+                            device=gpu)
+    pq = torch.randn((count, hq, d), device=gpu, dtype=torch.float16)
+    hip_kernels.paged_prefill_attention(pq, pk, pv, table, start=pos0, page_size=P,
+                                        scale=d ** -0.5)
+    torch.cuda.synchronize()
+    grown = hip_kernels.stream_workspace(gpu, 0)
+    assert grown.numel() > old_bytes and grown.data_ptr() != old_ptr
+    del grown
+    # New tensors that may take the old buffer's memory, holding a pattern.
+    sentinels = [torch.full((old_bytes // 4,), 7.0, device=gpu) for _ in range(3)]
+    torch.cuda.synchronize()
+    for t in (1, 2):
+        positions, qkv = load_step(t)
+        step.replay()
+        torch.cuda.synchronize()
+        check(positions, qkv)
+        for s in sentinels:
+            assert bool((s == 7.0).all()), "a replay wrote into memory it does not own"

@@ -1,7 +1,8 @@
 """Page pool, arena and table conventions that feed the kernel (CPU only).
 
-PagePool invariants follow the reference's tests/test_paged_kv.py (lowest
-free page first, reservations, refcounted sharing, random traffic), and the
+PagePool is checked against a brute-force model of its contract (lowest free
+id first, reference counts, reservations; paged_kv.py:79-153) and on the
+engine's sharing and window-trim patterns (mlx_engine.py:315-372), plus the
 block arithmetic of its C++ KVBlockPool test (tests/host_tests.cpp:66-90:
 15/16/17 tokens need 1/1/2 pages of 16).
 """
@@ -18,63 +19,159 @@ from instinct_amd.paged_kv import (LAYOUTS, KVCache, KVGroup, PagePool, pages_to
                                   rows_to_pages)
 
 
-def test_lowest_free_page_first_keeps_the_arena_compact():
-    pool = PagePool(8)
-    pages = [pool.allocate(reserved=False) for _ in range(3)]
-    assert pages == [0, 1, 2] and pool.high_water == 3
-    pool.release([1])
-    assert pool.allocate(reserved=False) == 1
-    assert pool.high_water == 3
+class PoolModel:
+    """Brute-force model of the pool's contract: a refcount per id, the
+    lowest id with no reference comes first, reservations only count."""
+
+    def __init__(self, capacity):
+        self.refs = [0] * capacity
+        self.reserved = 0
+        self.high_water = 0
+
+    @property
+    def free(self):
+        return self.refs.count(0)
+
+    def allocate(self, count):
+        got = [i for i, r in enumerate(self.refs) if r == 0][:count]
+        for i in got:
+            self.refs[i] = 1
+        if got:
+            self.high_water = max(self.high_water, got[-1] + 1)
+        return got
 
 
-def test_reservations_hold_pages_for_their_owner():
-    pool = PagePool(4)
-    assert pool.reserve(3)
-    assert pool.available == 1 and not pool.reserve(2)
-    pool.allocate(reserved=True)
-    assert pool.reserved == 2 and pool.free == 3 and pool.available == 1
-    pool.allocate(reserved=False)
-    with pytest.raises(RuntimeError, match="exhausted"):
-        pool.allocate(reserved=False)
-    pool.unreserve(2)
-    assert pool.available == 2
+def agrees(pool, model):
+    assert pool.free == model.free
+    assert pool.used == pool.capacity - model.free
+    assert pool.reserved == model.reserved
+    assert pool.available == model.free - model.reserved >= 0
+    assert pool.high_water == model.high_water
+    assert [pool.refcount(i) for i in range(pool.capacity)] == model.refs
+
+
+@pytest.mark.parametrize("capacity,seed", [(1, 0), (63, 1), (64, 2), (65, 3), (200, 4),
+                                           (1000, 5)])
+def test_pool_follows_the_brute_force_model(capacity, seed):
+    """Every operation of a long random sequence, including multi-page
+    allocations across 64-id word boundaries, repeated ids and released
+    (negative) table entries, against the model."""
+    rng = random.Random(seed)
+    pool, model = PagePool(capacity), PoolModel(capacity)
+    held = []  # one entry per reference
+    for _ in range(1500):
+        op = rng.random()
+        if op < 0.3:
+            n = rng.randint(0, 5) if rng.random() < 0.8 else rng.randint(0, 80)
+            use_reserve = rng.random() < 0.3 and model.reserved >= n
+            if not use_reserve and n > model.free - model.reserved:
+                with pytest.raises(RuntimeError, match="exhausted"):
+                    pool.allocate_many(n, reserved=False)
+                continue
+            got = pool.allocate_many(n, reserved=use_reserve)
+            if use_reserve:
+                model.reserved -= n
+            assert got.tolist() == model.allocate(n)
+            held += got.tolist()
+        elif op < 0.45 and held:
+            pages = [rng.choice(held) for _ in range(rng.randint(1, 4))] + [-1]
+            pool.retain(pages)
+            for page in pages:
+                if page >= 0:
+                    model.refs[page] += 1
+                    held.append(page)
+        elif op < 0.75 and held:
+            pages = [held.pop(rng.randrange(len(held))) for _ in range(min(len(held),
+                                                                           rng.randint(1, 6)))]
+            pool.release(pages + [-1, -7])
+            for page in pages:
+                model.refs[page] -= 1
+        elif op < 0.85:
+            n = rng.randint(0, 6)
+            ok = pool.reserve(n)
+            assert ok == (n <= model.free - model.reserved)
+            model.reserved += n if ok else 0
+        elif model.reserved:
+            n = rng.randint(0, model.reserved)
+            pool.unreserve(n)
+            model.reserved -= n
+        agrees(pool, model)
+    pool.release(held)
+    assert pool.free == capacity and pool.used == 0
+
+
+def test_lowest_free_id_comes_back_first_so_the_arena_stays_compact():
+    pool = PagePool(300)
+    first = pool.allocate_many(200, reserved=False)
+    assert first.tolist() == list(range(200)) and pool.high_water == 200
+    pool.release([199, 3, 130, 64])
+    assert pool.allocate_many(3, reserved=False).tolist() == [3, 64, 130]
+    assert pool.allocate(reserved=False) == 199
+    assert pool.allocate(reserved=False) == 200 and pool.high_water == 201
+
+
+def test_errors_leave_the_pool_unchanged():
+    pool = PagePool(10)
+    a, b = pool.allocate(reserved=False), pool.allocate(reserved=False)
+    pool.retain([a])
+    snapshot = [pool.refcount(i) for i in range(10)], pool.free
+    with pytest.raises(RuntimeError):
+        pool.release([a, b, b])          # b is held once
+    with pytest.raises(RuntimeError):
+        pool.retain([a, 7])              # 7 is free
+    with pytest.raises(RuntimeError):
+        pool.release([a, 10])            # outside the pool
+    assert ([pool.refcount(i) for i in range(10)], pool.free) == snapshot
     with pytest.raises(RuntimeError):
         pool.unreserve(1)
+    with pytest.raises(ValueError):
+        PagePool(0)
+    assert pool.shared(a) and not pool.shared(b)
 
 
-def test_shared_pages_return_only_after_the_last_reference():
-    pool = PagePool(2)
-    page = pool.allocate(reserved=False)
-    pool.retain([page, -1])
-    assert pool.shared(page)
-    pool.release([page])
-    assert pool.free == 1 and not pool.shared(page)
-    pool.release([page, -1])
-    assert pool.free == 2
-    with pytest.raises(RuntimeError):
-        pool.release([page])
-    with pytest.raises(RuntimeError):
-        pool.retain([page])
+def test_reserved_pages_stay_available_to_their_owner_only():
+    pool = PagePool(6)
+    assert pool.reserve(4) and pool.available == 2
+    assert not pool.reserve(3)
+    pool.allocate_many(2, reserved=False)
+    with pytest.raises(RuntimeError, match="exhausted"):
+        pool.allocate(reserved=False)
+    assert pool.allocate_many(4, reserved=True).tolist() == [2, 3, 4, 5]
+    assert pool.reserved == 0 and pool.free == 0
 
 
-@pytest.mark.parametrize("seed", range(5))
-def test_random_traffic_never_loses_or_duplicates_pages(seed):
-    rng = random.Random(seed)
-    pool = PagePool(32)
-    held = []
-    for _ in range(500):
-        action = rng.random()
-        if action < 0.5 and pool.available:
-            held.append(pool.allocate(reserved=False))
-        elif action < 0.7 and held:
-            page = rng.choice(held)
-            pool.retain([page])
-            held.append(page)
-        elif held:
-            pool.release([held.pop(rng.randrange(len(held)))])
-        assert pool.free + len(set(held)) == pool.capacity
-    pool.release(held)
-    assert pool.free == pool.capacity
+def test_shared_prefix_and_window_trim():
+    """The engine's table producers on one pool (mlx_engine.py:315-372): a
+    second request attaches to a 4-page prefix (retain all, copy the
+    partial last page into a fresh one); a windowed sequence releases the
+    pages that fall before (len - W + 1) // P and marks them -1. Pages come
+    free only when their last holder lets go, and a windowed sequence holds
+    at most ceil(W / P) + 1 pages however long it grows."""
+    P, W = 16, 40
+    pool = PagePool(64)
+    first = pool.allocate_many(4, reserved=False).tolist()
+    second = list(first)
+    pool.retain(second)
+    tail = pool.allocate(reserved=False)          # copy-on-write of the last page
+    pool.release([second[-1]])
+    second[-1] = tail
+    assert [pool.refcount(p) for p in first] == [2, 2, 2, 1]
+    pool.release(first)
+    assert pool.free == 64 - 4 and all(pool.refcount(p) == 1 for p in second)
+    pool.release(second)
+    assert pool.free == 64
+    table = []
+    for length in range(1, 400):
+        if (length - 1) // P >= len(table):
+            table.append(pool.allocate(reserved=False))
+        drop = (length - W + 1) // P
+        gone = [i for i in range(min(drop, len(table))) if table[i] >= 0]
+        pool.release([table[i] for i in gone])
+        for i in gone:
+            table[i] = -1
+        assert sum(p >= 0 for p in table) <= math.ceil(W / P) + 1
+        assert pool.used == sum(p >= 0 for p in table)
+    assert pool.high_water <= math.ceil(W / P) + 2
 
 
 def test_group_sizes():
