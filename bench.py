@@ -40,7 +40,7 @@ for _p in (ROOT, ROOT / "llm-inference_amd"):
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 matrix cores, published
 METRIC = "decode-attention effective K/V GB/s (% of HBM peak) + µs/layer-step"
-TRAFFIC_FILE = ROOT / "profiles" / "traffic_config2.json"
+TRAFFIC_FILE = ROOT / "profiles" / "decode_traffic.json"
 SPIN_CYCLES = 2_000_000  # torch.cuda._sleep before each timed call
 
 
@@ -50,7 +50,17 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
+    ap.add_argument("--batch", type=int, default=0,
+                    help="config 3: sequences (1, 2 or 4; default 1)")
+    ap.add_argument("--context", type=int, default=0,
+                    help="config 3: tokens per sequence (32768 or 131072; default 32768)")
     ap.add_argument("--split-pages", type=int, default=0)
+    ap.add_argument("--deterministic", action="store_true",
+                    help="fixed split points (PDA_DECODE_FIXED_SPLIT): bitwise reproducible")
+    ap.add_argument("--latency-configs", default="1",
+                    help="other configs timed in the same run, comma-separated ('' = none): "
+                         "GPU call time (flushed) beside the CPU baseline on the same "
+                         "workload; BASELINE pairs config 1 with the CPU path")
     ap.add_argument("--layout", choices=["pages", "rows"], default="pages",
                     help="K/V arena layout: page tiles (MI355X) or the reference's rows")
     ap.add_argument("--step-layers", type=int, default=28,
@@ -312,6 +322,44 @@ def prefill_leg(w, tokens, steps, start=0):
             "tokens_per_s": round(tokens / (med * 1e-3), 1)}
 
 
+def config_leg(cfg, args, flush):
+    """Another BASELINE config in the same run: the whole call (split and
+    merge) timed with HIP events around it, caches flushed between calls,
+    and the same CPU baseline as the headline leg on that workload."""
+    import torch
+
+    from instinct_amd import workloads
+    from instinct_amd.hip_kernels import decode_kernel_names, paged_decode_attention
+
+    device = torch.device("cuda:0")
+    w = workloads.CONFIGS[cfg](device=device).to_layout(args.layout)
+    out = torch.empty_like(w.q)
+
+    def call():
+        paged_decode_attention(w.q, w.keys, w.values, w.tables, w.lengths,
+                               page_size=w.page_size, longest=w.longest, scale=w.scale,
+                               window=w.window, softcap=w.softcap, out=out,
+                               deterministic=args.deterministic)
+
+    for _ in range(args.warmup):
+        call()
+    (ms,), _ = time_calls([call], args.steps, flush)
+    med = statistics.median(ms)
+    kv_bytes = w.kv_bytes()
+    names = decode_kernel_names(w.q_heads, w.kv_heads, w.head_dim)
+    leg = {"workload": w.name, "batch": w.batch, "q_heads": w.q_heads,
+           "kv_heads": w.kv_heads, "head_dim": w.head_dim, "kv_bytes": kv_bytes,
+           "kernel": f"{names['split']} + {names['merge']}",
+           "us_median": round(med * 1e3, 2), "us_mean": round(statistics.fmean(ms) * 1e3, 2),
+           "GB_per_s": round(kv_bytes / (med * 1e-3) / 1e9, 2),
+           "pct_hbm_peak": round(100 * kv_bytes / (med * 1e-3) / 1e9 / HBM_PEAK_GBS, 2)}
+    if not args.no_cpu:
+        leg["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds / 2)
+    del w, out
+    torch.cuda.empty_cache()
+    return leg
+
+
 def cpu_baseline(w, budget_s):
     """Oracle's C++ split-K restatement on a sample of sequences of the same
     workload, all host cores; returns the dict for the JSON line."""
@@ -378,7 +426,7 @@ def main():
         return
 
     from instinct_amd import _lib, workloads
-    from instinct_amd.hip_kernels import paged_decode_attention
+    from instinct_amd.hip_kernels import decode_kernel_names, paged_decode_attention
 
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
@@ -386,7 +434,13 @@ def main():
     if bf16 and args.kv_bits == 8:
         print("bench.py: the 8-bit cache takes fp16 queries (--dtype f16)", file=sys.stderr)
         sys.exit(2)
-    w = workloads.CONFIGS[args.config](device=device).to_layout(args.layout)
+    cfg_kw = {}
+    if args.config == 3:
+        cfg_kw = dict(batch=args.batch or 1, length=args.context or 32768)
+    elif args.batch or args.context:
+        print("bench.py: --batch/--context choose among config 3's points", file=sys.stderr)
+        sys.exit(2)
+    w = workloads.CONFIGS[args.config](device=device, **cfg_kw).to_layout(args.layout)
     if bf16:
         # The same seeded values rounded to bf16: a bf16 model's cache.
         w.q, w.keys, w.values = w.q.bfloat16(), w.keys.bfloat16(), w.values.bfloat16()
@@ -415,7 +469,7 @@ def main():
                                page_size=w.page_size, longest=w.longest, scale=w.scale,
                                window=w.window, softcap=w.softcap,
                                split_pages=args.split_pages, out=out, passes=passes,
-                               scales=scales)
+                               scales=scales, deterministic=args.deterministic)
 
     def split():
         call("split")
@@ -436,23 +490,29 @@ def main():
         flush_buf.fill_(1)
         read_buf.sum()
 
-    # The metric: whole calls (split + merge, one C-ABI call). The roofline:
-    # the split kernel alone, from a second loop that issues the two passes
-    # separately so an event can sit between them.
+    # The metric and the roofline: whole calls (split + merge, one C-ABI
+    # call), HIP events on the kernels' stream. A second loop issues the two
+    # passes separately (an event between them) to show where the time goes.
     flushing = None if args.no_flush else flush
     (call_ms,), wall = time_calls([call], args.steps, flushing)
-    (split_ms, _), _ = time_calls([split, merge], args.steps, flushing)
+    (split_ms, merge_ms), _ = time_calls([split, merge], args.steps, flushing)
     (call_w,), _ = time_calls([call], args.steps)
     ms = call_ms
     med = statistics.median(ms)
     value = kv_bytes / (med * 1e-3) / 1e9
+    call_mean = statistics.fmean(ms)
     split_mean = statistics.fmean(split_ms)
-    achieved = kv_bytes / (split_mean * 1e-3) / 1e9
+    achieved = kv_bytes / (call_mean * 1e-3) / 1e9
     waves, _ = _lib.plan(w.batch, w.q_heads, w.kv_heads, w.head_dim, w.page_size,
                          int(w.tables.shape[1]), w.longest, w.window, args.split_pages)
+    names = decode_kernel_names(w.q_heads, w.kv_heads, w.head_dim, bits=args.kv_bits,
+                                bf16=bf16)
+    traffic_key = (f"{w.name}/{w.layout}/{'bf16' if bf16 else 'f16'}/kv{args.kv_bits}"
+                   f"{'/fixed' if args.deterministic else ''}")
     traffic = None
-    if TRAFFIC_FILE.exists() and args.config == 2 and args.kv_bits == 16 and not bf16:
-        traffic = json.loads(TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
+    if TRAFFIC_FILE.exists():
+        traffic = json.loads(TRAFFIC_FILE.read_text()).get(traffic_key, {}).get(
+            "hbm_bytes_per_call")
     line = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -473,6 +533,7 @@ def main():
             "layout": w.layout, "kv_bits": args.kv_bits,
             "longest": w.longest, "kv_bytes": kv_bytes,
             "split_pages": args.split_pages, "stream_waves_max": waves,
+            "fixed_split": args.deterministic,
             "cache": "warm (no flush)" if args.no_flush else "flushed (1 GiB write + 1 GiB read between calls)",
         },
         "us_per_layer_step": round(med * 1e3, 2),
@@ -487,11 +548,13 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "kernel": f"paged_decode_kernel<{w.head_dim},{min(8, w.q_heads // w.kv_heads)},"
-                      f"{str(args.kv_bits == 8).lower()},{str(bf16).lower()}> "
-                      "(split pass; events around it alone)",
-            "us_mean": round(split_mean * 1e3, 2),
-            "call_us_mean": round(statistics.fmean(ms) * 1e3, 2),
+            "traffic_source": f"{TRAFFIC_FILE.relative_to(ROOT)}[{traffic_key}]",
+            "kernel": f"{names['split']} + {names['merge']} (one call: split and merge, "
+                      "events around both)",
+            "us_mean": round(call_mean * 1e3, 2),
+            "split_us_mean": round(split_mean * 1e3, 2),
+            "merge_us_mean": round(statistics.fmean(merge_ms) * 1e3, 2),
+            "head_groups_per_kv_head": names["head_groups_per_kv_head"],
         },
     }
     if w.meta.get("sharers") is not None:
@@ -503,6 +566,10 @@ def main():
     # The CPU baselines time the fp16 oracle; a bf16 run has none.
     if not args.no_cpu and args.kv_bits == 16 and not bf16:
         line["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
+    others = [int(c) for c in args.latency_configs.split(",") if c.strip()]
+    if args.kv_bits == 16 and not bf16:
+        line["other_configs"] = {str(c): config_leg(c, args, flushing)
+                                 for c in others if c != args.config}
 
     # The step before the attention call: RoPE of the new queries and keys and
     # the K/V append (one launch), timed alone and followed by the call (one

@@ -59,12 +59,16 @@ extern "C" {
 #define PDA_OK 0
 #define PDA_ERR_INVALID_ARGUMENT (-1) /* null pointer, non-positive size, ... */
 #define PDA_ERR_HEAD_RATIO (-2)       /* q_heads is not a multiple of kv_heads */
-#define PDA_ERR_HEAD_DIM (-3)         /* head_dim has no compiled kernel      */
-#define PDA_ERR_PAGE_SIZE (-4)        /* page_size not a multiple of the step */
+#define PDA_ERR_HEAD_DIM (-3)         /* head_dim odd, or above 512           */
+#define PDA_ERR_PAGE_SIZE (-4)        /* (no longer returned: any page size)  */
 #define PDA_ERR_WORKSPACE (-5)        /* workspace missing or too small       */
 #define PDA_ERR_ALIGNMENT (-6)        /* fp16 buffers must be 16-byte aligned */
 #define PDA_ERR_TOO_LONG (-7)         /* context beyond the split planner     */
 #define PDA_ERR_HIP (-8)              /* a HIP runtime call failed            */
+
+/* Flags of the decode calls (the `flags` argument, 0 = none). */
+#define PDA_DECODE_FIXED_SPLIT 1 /* fixed split points: bitwise reproducible
+                                    output (see pda_paged_decode_attention) */
 
 /* K/V arena layouts (the `layout` argument of the decode calls). */
 #define PDA_LAYOUT_ROWS 0  /* [rows, kv_heads, head_dim], the reference's   */
@@ -107,10 +111,21 @@ int pda_plan(int32_t batch, int32_t q_heads, int32_t kv_heads,
  * attention. `longest` is the host-side largest length, as in the reference
  * (a planning hint only: results never depend on it, and lengths above it
  * stay correct). `split_pages` is the fewest pages a wave reads before the
- * stream is spread over fewer waves (0 = 1; results do not depend on it).
- * `arena_rows` is the row count of the keys/values arenas (pages x
- * page_size) and `layout` is PDA_LAYOUT_ROWS or PDA_LAYOUT_PAGES (the reference
- * has one layout, rows); batch <= 8184.
+ * stream is spread over fewer waves (0 = 1; results do not depend on it
+ * beyond rounding). `arena_rows` is the row count of the keys/values arenas
+ * (pages x page_size) and `layout` is PDA_LAYOUT_ROWS or PDA_LAYOUT_PAGES (the
+ * reference has one layout, rows); batch <= 8184. Like the reference op
+ * (its IN_HEAD guard and PAGE template, metal_kernels.py:28-30,204), any even
+ * head_dim up to 512 and any page_size are accepted: head dims 64, 80, 96,
+ * 128, 256, 512 run tuned kernels, the others a generic one.
+ * `flags`: 0, or PDA_DECODE_FIXED_SPLIT. Without it the two waves that share
+ * a stretch of pages split it wherever their shared counter runs out (the
+ * faster wave takes more), so where a sequence is cut, and the rounding of
+ * its partial results, can differ between two calls on the same inputs
+ * (within the parity bar). With it the split points are fixed by the
+ * shapes, the lengths and the device's CU count, and repeated calls give
+ * bitwise-identical output, as the reference's fixed split ranges do
+ * (metal_kernels.py:32-36).
  * Launches a split kernel and a merge kernel on `stream`; calls that share a
  * workspace must not overlap. */
 int pda_paged_decode_attention(const void* queries, const void* keys,
@@ -122,7 +137,7 @@ int pda_paged_decode_attention(const void* queries, const void* keys,
                                int64_t arena_rows, int32_t layout,
                                int32_t longest, float scale, int32_t window,
                                float softcap,
-                               int32_t split_pages, void* workspace,
+                               int32_t split_pages, int32_t flags, void* workspace,
                                size_t workspace_bytes, void* stream);
 
 /* The two passes of pda_paged_decode_attention, for callers that schedule or
@@ -136,7 +151,7 @@ int pda_decode_split(const void* queries, const void* keys, const void* values,
                      int32_t head_dim, int32_t page_size, int32_t table_stride,
                      int64_t arena_rows, int32_t layout, int32_t longest,
                      float scale, int32_t window, float softcap,
-                     int32_t split_pages,
+                     int32_t split_pages, int32_t flags,
                      void* workspace, size_t workspace_bytes, void* stream);
 int pda_decode_merge(const void* queries, const void* keys, const void* values,
                      const int32_t* tables, const int32_t* lengths, void* out,
@@ -144,7 +159,7 @@ int pda_decode_merge(const void* queries, const void* keys, const void* values,
                      int32_t head_dim, int32_t page_size, int32_t table_stride,
                      int64_t arena_rows, int32_t layout, int32_t longest,
                      float scale, int32_t window, float softcap,
-                     int32_t split_pages,
+                     int32_t split_pages, int32_t flags,
                      void* workspace, size_t workspace_bytes, void* stream);
 
 /* bf16: the same calls with queries, K/V arenas and output in bf16, the
@@ -162,7 +177,7 @@ int pda_paged_decode_attention_bf16(const void* queries, const void* keys,
                                     int64_t arena_rows, int32_t layout,
                                     int32_t longest, float scale,
                                     int32_t window, float softcap,
-                                    int32_t split_pages, void* workspace,
+                                    int32_t split_pages, int32_t flags, void* workspace,
                                     size_t workspace_bytes, void* stream);
 int pda_decode_split_bf16(const void* queries, const void* keys, const void* values,
                           const int32_t* tables, const int32_t* lengths, void* out,
@@ -170,7 +185,7 @@ int pda_decode_split_bf16(const void* queries, const void* keys, const void* val
                           int32_t head_dim, int32_t page_size, int32_t table_stride,
                           int64_t arena_rows, int32_t layout, int32_t longest,
                           float scale, int32_t window, float softcap,
-                          int32_t split_pages,
+                          int32_t split_pages, int32_t flags,
                           void* workspace, size_t workspace_bytes, void* stream);
 int pda_decode_merge_bf16(const void* queries, const void* keys, const void* values,
                           const int32_t* tables, const int32_t* lengths, void* out,
@@ -178,7 +193,7 @@ int pda_decode_merge_bf16(const void* queries, const void* keys, const void* val
                           int32_t head_dim, int32_t page_size, int32_t table_stride,
                           int64_t arena_rows, int32_t layout, int32_t longest,
                           float scale, int32_t window, float softcap,
-                          int32_t split_pages,
+                          int32_t split_pages, int32_t flags,
                           void* workspace, size_t workspace_bytes, void* stream);
 
 /* 8-bit K/V: pda_paged_decode_attention over int8 arenas with one fp16 scale
@@ -194,10 +209,10 @@ int pda_decode_merge_bf16(const void* queries, const void* keys, const void* val
  *   key_scales, value_scales  fp16, [arena_rows, kv_heads] beside a row
  *                 arena, [arena_rows / page_size, kv_heads, page_size] beside
  *                 a page-tile arena
- * head_dim in {64, 128, 256, 512}; every other argument as for the fp16
- * call, which shares the workspace sizing (pda_workspace_bytes). The split
- * and merge passes exist as for fp16; merge with the _q8 entry after a _q8
- * split. */
+ * Any even head_dim up to 512 (64, 128, 256, 512 tuned, the others, 80
+ * included, generic); every other argument as for the fp16 call, which
+ * shares the workspace sizing (pda_workspace_bytes). The split and merge
+ * passes exist as for fp16; merge with the _q8 entry after a _q8 split. */
 int pda_paged_decode_attention_q8(const void* queries, const void* keys,
                                   const void* values, const void* key_scales,
                                   const void* value_scales,
@@ -207,7 +222,7 @@ int pda_paged_decode_attention_q8(const void* queries, const void* keys,
                                   int32_t page_size, int32_t table_stride,
                                   int64_t arena_rows, int32_t layout,
                                   int32_t longest, float scale, int32_t window,
-                                  float softcap, int32_t split_pages,
+                                  float softcap, int32_t split_pages, int32_t flags,
                                   void* workspace, size_t workspace_bytes,
                                   void* stream);
 int pda_decode_split_q8(const void* queries, const void* keys, const void* values,
@@ -217,7 +232,7 @@ int pda_decode_split_q8(const void* queries, const void* keys, const void* value
                         int32_t head_dim, int32_t page_size, int32_t table_stride,
                         int64_t arena_rows, int32_t layout, int32_t longest,
                         float scale, int32_t window, float softcap,
-                        int32_t split_pages, void* workspace,
+                        int32_t split_pages, int32_t flags, void* workspace,
                         size_t workspace_bytes, void* stream);
 int pda_decode_merge_q8(const void* queries, const void* keys, const void* values,
                         const void* key_scales, const void* value_scales,
@@ -226,7 +241,7 @@ int pda_decode_merge_q8(const void* queries, const void* keys, const void* value
                         int32_t head_dim, int32_t page_size, int32_t table_stride,
                         int64_t arena_rows, int32_t layout, int32_t longest,
                         float scale, int32_t window, float softcap,
-                        int32_t split_pages, void* workspace,
+                        int32_t split_pages, int32_t flags, void* workspace,
                         size_t workspace_bytes, void* stream);
 
 /* K/V append with rotary position embedding, one launch for n tokens.

@@ -59,6 +59,7 @@
 #include <utility>
 
 #include "pda.h"
+#include "pda_decode.h"
 #include "pda_internal.h"
 
 namespace pda_internal {
@@ -86,1048 +87,44 @@ const char* last_error() { return g_error; }
 
 namespace {
 
-typedef _Float16 f16;
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16;
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef int i32x4 __attribute__((ext_vector_type(4)));
-
-constexpr float kLog2e = 1.44269504088896340736f;
-// Lazy rescale threshold (log2 units): probabilities stay below 2^8.
-constexpr float kSlack = 8.0f;
-constexpr int kSplitWaves = 8;                 // waves per split workgroup
-constexpr int kSplitThreads = kSplitWaves * 64;
-constexpr int kPairs = kSplitWaves / 2;        // wave pairs per workgroup
-constexpr int kNbuf = 2;                       // K/V steps in flight per wave
-constexpr int kTablePages = 64;                // page-table entries held per VGPR refill
-constexpr int kMaxGroups = 512;                // resident split workgroups (256 CUs x 2)
-constexpr int kMaxWaves = kMaxGroups * kSplitWaves;
-constexpr int kMaxPairs = kMaxWaves / 2;
-constexpr int kSlots = 2 * kMaxWaves;          // partial slots: first and last unit of a wave
-constexpr int kMinPagesPerWave = 1;            // default: spread no thinner than this
-constexpr int kMaxBatch = 8184;                // per-sequence tables in LDS: (2B + 1) ints
-constexpr int kMergeMaxWaves = 16;             // waves per merge workgroup, at most
-
-struct Params {
-  const f16* q;
-  const f16* k;
-  const f16* v;
-  const int32_t* tables;
-  const int32_t* lengths;
-  f16* out;
-  int32_t* prefix;    // [B + 1] visible pages before each sequence (workspace)
-  int32_t* meet;      // [pairs] pages the first wave of each pair took (workspace)
-  float2* part_ml;    // [kSlots][G] (running max, sum) of cut units
-  float* part_o;      // [kSlots][G][D] unnormalised outputs of cut units
-  const f16* kscale;  // 8-bit K/V: fp16 scale per (row, kv head) of keys,
-  const f16* vscale;  //   of values (null for fp16 K/V)
-  int64_t scale_page; // scale elements between pages,
-  int32_t scale_head; //   between kv heads of one page,
-  int32_t scale_row;  //   between rows of one page and kv head
-  int64_t arena_pages;
-  int64_t page_bytes; // K/V arena: bytes between pages,
-  int32_t head_bytes; //   between kv heads of one page,
-  int32_t row_bytes;  //   between rows (keys) of one page and kv head
-  int32_t batch;
-  int32_t table_stride;
-  int32_t page_size;
-  int32_t hq;
-  int32_t hkv;
-  int32_t gtot;       // query heads per kv head
-  int32_t nhg;        // head groups per kv head (gtot / G)
-  int32_t window;
-  int32_t grid_pairs; // wave pairs of the split kernel's grid
-  int32_t min_pages;  // fewest pages per wave before the stream uses fewer pairs
-  float scale_log2;   // scale * log2(e)
-  float softcap;      // 0 = off
-  float cap_in;       // 2 * log2(e) * scale / softcap
-  float cap_out;      // softcap * log2(e)
-};
-
-constexpr int next_pow2(int x) {
-  int p = 1;
-  while (p < x) p <<= 1;
-  return p;
-}
-
-// Lane geometry of a head_dim. R lanes share one key; each active lane holds
-// EPL elements of it as NV chunks of 8 (one 16-byte load each). Chunk c of
-// lane r covers elements [c * DC + r * 8, c * DC + r * 8 + 8), DC = D / NV, so
-// one load instruction of the wave reads whole 128-byte lines of KPS rows.
-//
-// 8-bit K/V (Q8): a lane holds 16 consecutive int8 elements [r * 16, r * 16 +
-// 16) of its key, one 16-byte load; R = D / 16, and p.v always runs on key
-// pairs, the values of one pair loaded as two 8-byte pieces.
-template <int D, bool Q8 = false>
-struct Geom {
-  static constexpr int EPL = Q8 ? 16 : ((D >= 80 && D % 16 == 0) ? 16 : 8);  // per lane
-  static constexpr int NV = Q8 ? 1 : EPL / 8;                     // 16-byte K loads
-  static constexpr int DC = D / NV;                               // chunk stride
-  static constexpr int SLICES = D / EPL;
-  static constexpr int R = next_pow2(SLICES);                     // lanes per key
-  static constexpr int KPS = 64 / R;                              // keys per step
-  // p.v on v_dot2 over key pairs (head dims with 2R lanes x 8 elements):
-  // lane (kp, r2), kp = lane / 2R, r2 = lane % 2R, holds elements
-  // [r2 * 8, r2 * 8 + 8) of the step's keys 2 kp and 2 kp + 1.
-  static constexpr bool PV2 = EPL == 16 && D == 2 * R * 8;
-  static constexpr int OPL = PV2 ? 8 : EPL;                       // outputs per lane
-  static constexpr int NPAIR = KPS / 2;                           // key pairs per step
-  // Vector memory loads per step: K and V (fp16); K, the two V pieces and the
-  // key scale and the pair's two value scales (8-bit).
-  static constexpr int LOADS = Q8 ? 6 : 2 * NV;
-  static_assert(D % EPL == 0 && DC % 8 == 0, "head_dim must be a multiple of 8");
-  static_assert(!Q8 || PV2, "8-bit K/V needs the key-pair p.v layout");
-  static_assert(R <= 32, "head_dim too large");
-};
-
-template <int CTRL>
-__device__ __forceinline__ float dpp(float x) {
-  return __builtin_bit_cast(
-      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL,
-                                         0xF, 0xF, false));
-}
-
-// Sum over the R consecutive lanes that share a key (xor butterfly: every
-// lane of the group ends with the bitwise-identical total).
-template <int R>
-__device__ __forceinline__ float group_sum(float x) {
-  if constexpr (R >= 2) x += dpp<0xB1>(x);   // quad_perm [1,0,3,2]
-  if constexpr (R >= 4) x += dpp<0x4E>(x);   // quad_perm [2,3,0,1]
-  if constexpr (R >= 8) x += dpp<0x141>(x);  // row_half_mirror
-  if constexpr (R >= 16) x += dpp<0x140>(x); // row_mirror
-  if constexpr (R >= 32) x += __shfl_xor(x, 16);
-  return x;
-}
-
-// Sum over the 64 / R key subsets (lanes r, r + R, r + 2R, ...).
-template <int R>
-__device__ __forceinline__ float subset_sum(float x) {
-  if constexpr (R <= 4) x += __shfl_xor(x, 4);
-  if constexpr (R <= 8) x += dpp<0x128>(x);  // row_ror:8 == lane ^ 8
-  if constexpr (R <= 16) x += __shfl_xor(x, 16);
-  if constexpr (R <= 32) x += __shfl_xor(x, 32);
-  return x;
-}
-
-// Sum over the key pairs of the p.v layout (lanes r2, r2 + 2R, ...).
-template <int R>
-__device__ __forceinline__ float pair_sum(float x) {
-  if constexpr (2 * R <= 8) x += dpp<0x128>(x);  // row_ror:8 == lane ^ 8
-  if constexpr (2 * R <= 16) x += __shfl_xor(x, 16);
-  if constexpr (2 * R <= 32) x += __shfl_xor(x, 32);
-  return x;
-}
-
-// The value of lane ^ R (the other key of this lane's pair).
-template <int R>
-__device__ __forceinline__ float pair_swap(float x) {
-  if constexpr (R == 8)  // row_ror:8 == lane ^ 8, every lane valid: no old value
-    return __builtin_bit_cast(
-        float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x128, 0xF, 0xF, true));
-  else
-    return __shfl_xor(x, R);
-}
-
-// a.x * b.x + a.y * b.y in fp32: the 3-operand v_dot2 with an inline zero
-// (the compiler would otherwise zero a register to use the accumulating form).
-__device__ __forceinline__ float dot2_first(f16x2 a, f16x2 b) {
-  float d;
-  asm("v_dot2_f32_f16 %0, %1, %2, 0" : "=v"(d) : "v"(a), "v"(b));
-  return d;
-}
-
-// bf16 counterpart of dot2_first.
-__device__ __forceinline__ float dot2_first_bf16(bf16x2 a, bf16x2 b) {
-  float d;
-  asm("v_dot2_f32_bf16 %0, %1, %2, 0" : "=v"(d) : "v"(a), "v"(b));
-  return d;
-}
-
-__device__ __forceinline__ float wave_max(float x) {
-  x = fmaxf(x, dpp<0xB1>(x));
-  x = fmaxf(x, dpp<0x4E>(x));
-  x = fmaxf(x, dpp<0x141>(x));
-  x = fmaxf(x, dpp<0x140>(x));
-  x = fmaxf(x, __shfl_xor(x, 16));
-  x = fmaxf(x, __shfl_xor(x, 32));
-  return __builtin_bit_cast(
-      float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, x)));
-}
-
-__device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
-
-// Log-sum-exp combination of pieces (metal_kernels.py:103-124): a running
-// maximum, pieces whose max is -inf (no visible key) weigh 0.
-template <int NC>
-__device__ __forceinline__ void lse_add(float& top, float& sum, float (&acc)[NC], float2 ml,
-                                        const float (&part)[NC]) {
-  if (ml.x == -INFINITY) return;
-  const float mn = fmaxf(top, ml.x);
-  const float fo = __builtin_amdgcn_exp2f(top - mn);  // 0 while top = -inf
-  const float fn = __builtin_amdgcn_exp2f(ml.x - mn);
-  top = mn;
-  sum = sum * fo + ml.y * fn;
-#pragma unroll
-  for (int c = 0; c < NC; ++c) acc[c] = acc[c] * fo + part[c] * fn;
-}
-
-// s_waitcnt on the vector memory counter alone: at most N loads outstanding
-// (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]).
-template <int N>
-__device__ __forceinline__ void wait_vmem() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
-
-__device__ __forceinline__ f16x8 zero_unless(f16x8 x, bool keep) {
-  i32x4 bits = __builtin_bit_cast(i32x4, x);
-  bits.x = keep ? bits.x : 0;
-  bits.y = keep ? bits.y : 0;
-  bits.z = keep ? bits.z : 0;
-  bits.w = keep ? bits.w : 0;
-  return __builtin_bit_cast(f16x8, bits);
-}
-
-// Int8 bytes to fp16 pairs, exactly (pda_internal.h).
-using pda_internal::bytes_to_f16x2;
-
-struct SeqGeometry {
-  int len, first, first_page, npages;
-};
-
-// Visible range [first, len) of sequence b (metal_kernels.py:32-36, length
-// clamped to the table) and the pages it touches.
-__device__ __forceinline__ SeqGeometry sequence_geometry(const Params& p, int b) {
-  SeqGeometry g;
-  const int P = p.page_size;
-  g.len = min(max(p.lengths[b], 0), p.table_stride * P);
-  g.first = p.window > 0 ? max(0, g.len - p.window) : 0;
-  g.first_page = g.first / P;
-  g.npages = g.len > g.first ? (g.len - 1) / P - g.first_page + 1 : 0;
-  return g;
-}
-
-// Wave pairs the stream of `total` pages is spread over (both kernels agree).
-__device__ __forceinline__ int stream_pairs(int64_t total, const Params& p) {
-  if (total <= 0) return 0;
-  const int64_t want = (total + 2 * p.min_pages - 1) / (2 * p.min_pages);
-  return (int)min<int64_t>(want, p.grid_pairs);
-}
-
-// First page of pair q's range, and the pair whose range holds page x.
-__device__ __forceinline__ int64_t range_start(int q, int64_t total, int pairs) {
-  return (int64_t)q * total / pairs;
-}
-__device__ __forceinline__ int pair_of(int64_t x, int64_t total, int pairs) {
-  return (int)(((x + 1) * pairs - 1) / total);
-}
-
-// Exclusive prefix of visible pages over the batch, into LDS (all threads of
-// the workgroup), plus each sequence's clamped length.
-template <int kThreads>
-__device__ void build_prefix(const Params& p, int* s_prefix, int* s_len) {
-  constexpr int kWaves = kThreads / 64;
-  __shared__ int s_wsum[kWaves];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int B = p.batch;
-  int carry = 0;
-  for (int base = 0; base < B; base += kThreads) {
-    const int b = base + tid;
-    int x = 0;
-    if (b < B) {
-      const SeqGeometry g = sequence_geometry(p, b);
-      x = g.npages;
-      s_len[b] = g.len;
-    }
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int y = __shfl_up(x, off);
-      if (lane >= off) x += y;
-    }
-    if (lane == 63) s_wsum[w] = x;
-    __syncthreads();
-    int before = carry, block = 0;
-#pragma unroll
-    for (int i = 0; i < kWaves; ++i) {
-      before += i < w ? s_wsum[i] : 0;
-      block += s_wsum[i];
-    }
-    if (b < B) s_prefix[b + 1] = before + x;
-    carry += block;
-    __syncthreads();
-  }
-  if (tid == 0) s_prefix[0] = 0;
-  __syncthreads();
-}
-
-// Split kernel: a persistent grid of wave pairs (see the file comment).
-// At least two waves per SIMD (<= 256 registers): with G = 7 or 8 heads the
-// few values that do not fit live outside the main loop.
-// BF: queries, K/V and output in bf16 (the model dtype of the reference's
-// bf16 models; their arenas hold the model dtype, paged_kv.py:156-292). The
-// 16-bit buffers are addressed as fp16 storage and reinterpreted: q.k and
-// p.v run on bf16 v_dot2, the probabilities are rounded to bf16 for p.v.
-template <int D, int G, bool Q8, bool BF>
-__global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(2)))
-void paged_decode_kernel(const Params p) {
-  static_assert(!(Q8 && BF), "8-bit K/V is dequantized to fp16");
-  using Gm = Geom<D, Q8>;
-  constexpr int EPL = Gm::EPL, NV = Gm::NV, DC = Gm::DC, R = Gm::R, KPS = Gm::KPS;
-  constexpr bool PV2 = Gm::PV2;
-  constexpr int OPL = Gm::OPL;
-  extern __shared__ int s_dyn[];
-  __shared__ int s_ticket[kPairs];
-  const int B = p.batch;
-  int* const s_prefix = s_dyn;         // [B + 1]
-  int* const s_len = s_dyn + B + 1;    // [B]
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int w = uniform(tid >> 6);
-  const int kk = lane / R;  // key of the step this lane works on
-  const int r = lane % R;   // slice of the head this lane holds
-  const bool active = r < Gm::SLICES;
-  const int d0 = active ? r * 8 : 0;  // first element of chunk 0
-  const int r2 = lane % (2 * R);      // p.v layout: element group and key pair
-  const int kp = lane / (2 * R);
-  const bool hi = kk & 1;             // this lane's key is the second of its pair
-  // v_perm selectors that pair V elements as (this lane's key, the other),
-  // the order of the probability pair below: bytes 0-3 of the source pair
-  // are the second key's dword, 4-7 the first key's.
-  const uint32_t sel_lo = hi ? 0x05040100u : 0x01000504u;
-  const uint32_t sel_hi = hi ? 0x07060302u : 0x03020706u;
-  // 8-bit: bytes (this lane's key, the other) of two elements, from the
-  // first key's dword (source bytes 4-7) and the second's (0-3).
-  const uint32_t sel8_lo = hi ? 0x05010400u : 0x01050004u;
-  const uint32_t sel8_hi = hi ? 0x07030602u : 0x03070206u;
-  const int P = p.page_size;
-  const int spp = P / KPS;  // steps per page
-  const int nkvg = p.hkv * p.nhg;
-
-  if (tid < kPairs) s_ticket[tid] = 0;
-  build_prefix<kSplitThreads>(p, s_prefix, s_len);  // ends with a barrier
-  if (blockIdx.x == 0)
-    for (int i = tid; i <= B; i += kSplitThreads) p.prefix[i] = s_prefix[i];
-  // Sequences with no visible key get zeros (metal_kernels.py:88-90 with a
-  // zero sum); workgroup j takes sequences j, j + grid, ...
-  for (int bz = blockIdx.x; bz < B; bz += gridDim.x) {
-    if (s_prefix[bz + 1] != s_prefix[bz]) continue;
-    f16* const dz = p.out + (int64_t)bz * p.hq * D;
-    for (int i = tid * 8; i < p.hq * D; i += kSplitThreads * 8)
-      *reinterpret_cast<f16x8*>(dz + i) = f16x8{};
-  }
-  const int64_t total = (int64_t)s_prefix[B] * nkvg;
-  const int npairs = stream_pairs(total, p);
-  const int pl = w % kPairs;
-  const bool back = w >= kPairs;  // takes its pair's range from the end
-  const int pair = blockIdx.x * kPairs + pl;
-  if (pair >= npairs) return;
-  const int64_t x0 = range_start(pair, total, npairs);
-  const int n_range = (int)(range_start(pair + 1, total, npairs) - x0);
-  const int dir = back ? -1 : 1;
-  const int64_t vw = 2 * (int64_t)pair + (back ? 1 : 0);  // slots 2 vw, 2 vw + 1
-
-  // One ticket per page; a ticket below n_range is a page of the range. All
-  // lanes take part without a branch, lane 0 adding 1 and the others 0, so
-  // lane 0 always reads the count before its own add. The result stays in a
-  // VGPR until it is needed, one page later.
-  auto take_ticket = [&]() -> int {
-    return __hip_atomic_fetch_add(&s_ticket[pl], lane == 0 ? 1 : 0, __ATOMIC_RELAXED,
-                                  __HIP_MEMORY_SCOPE_WORKGROUP);
-  };
-  auto granted = [&](int t) -> bool { return uniform(t) < n_range; };
-
-  // Unit holding the first page this wave would take: the last b with
-  // nkvg * prefix[b] <= x (never an empty sequence, since x < total).
-  const int64_t xs = back ? x0 + n_range - 1 : x0;
-  int b = 0;
-  {
-    int lo = 0, hi = B - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if ((int64_t)s_prefix[mid] * nkvg <= xs) lo = mid; else hi = mid - 1;
-    }
-    b = lo;
-  }
-  int npg = s_prefix[b + 1] - s_prefix[b];
-  if (npg <= 0) return;  // cannot happen for xs < total; guards the division
-  int kvg, pa;
-  {
-    const int64_t rel = xs - (int64_t)s_prefix[b] * nkvg;
-    kvg = (int)(rel / npg);
-    pa = (int)(rel - (int64_t)kvg * npg);
-  }
-
-  const char* const kbase = reinterpret_cast<const char*>(p.k);
-  const char* const vbase = reinterpret_cast<const char*>(p.v);
-
-  bool first_unit = true;
-  int taken = 0;               // pages this wave processed
-  bool pending = granted(take_ticket());  // the next page along the wave's way is ours
-
-  while (pending) {
-    // Unit (b, kvg): pages pa, pa + dir, ... while tickets last.
-    const int len = s_len[b];
-    const int first = p.window > 0 ? max(0, len - p.window) : 0;
-    const int first_page = first / P;
-    const int kvh = kvg / p.nhg;
-    const int h0 = kvh * p.gtot + (kvg - kvh * p.nhg) * G;
-    const int32_t* const table = p.tables + (int64_t)b * p.table_stride + first_page;
-
-    // Queries of the G heads, this lane's slice, as fp16 pairs for v_dot2
-    // (bf16: the same bits, read as bf16 pairs where used).
-    f16x2 q[G][EPL / 2];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      if constexpr (Q8) {
-        // Elements [r * 16, r * 16 + 16), the slice of the int8 key row.
-        const f16* qp = p.q + ((int64_t)b * p.hq + h0 + g) * D + r * 16;
-#pragma unroll
-        for (int v = 0; v < 2; ++v) {
-          const f16x8 xq = *reinterpret_cast<const f16x8*>(qp + 8 * v);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) q[g][4 * v + i] = f16x2{xq[2 * i], xq[2 * i + 1]};
-        }
-      } else {
-        const f16* qp = p.q + ((int64_t)b * p.hq + h0 + g) * D + d0;
-#pragma unroll
-        for (int v = 0; v < NV; ++v) {
-          f16x8 xq = zero_unless(*reinterpret_cast<const f16x8*>(qp + DC * v), active);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) q[g][4 * v + i] = f16x2{xq[2 * i], xq[2 * i + 1]};
-        }
-      }
-    }
-
-    float o[G][OPL];
-    float l[G];
-    float m[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      l[g] = 0.0f;
-      m[g] = -INFINITY;
-#pragma unroll
-      for (int i = 0; i < OPL; ++i) o[g][i] = 0.0f;
-    }
-
-    // Addressing: a wave-uniform byte offset per step (page and first key of
-    // the step) plus 32-bit per-lane offsets: K by (key, kv head, chunk), V
-    // by (key pair, kv head, element group) on the p.v path, else as K.
-    const uint32_t lane_off =
-        Q8 ? (uint32_t)(kk * p.row_bytes + kvh * p.head_bytes + r * 16)
-           : (uint32_t)(kk * p.row_bytes + kvh * p.head_bytes + d0 * 2);
-    const uint32_t v_off =
-        Q8    ? (uint32_t)(2 * kp * p.row_bytes + kvh * p.head_bytes + r2 * 8)
-        : PV2 ? (uint32_t)(2 * kp * p.row_bytes + kvh * p.head_bytes + r2 * 16)
-              : lane_off;
-    // 8-bit scales, in elements from the step's first key: this lane's key,
-    // and its pair's keys with this lane's own key first.
-    const uint32_t ks_off = (uint32_t)(kvh * p.scale_head + kk * p.scale_row);
-    const uint32_t vs_own = (uint32_t)(kvh * p.scale_head + (2 * kp + (hi ? 1 : 0)) * p.scale_row);
-    const uint32_t vs_other = (uint32_t)(kvh * p.scale_head + (2 * kp + (hi ? 0 : 1)) * p.scale_row);
-
-    // Page-table window: lane i holds the physical id of unit page
-    // win + dir * i (lanes past the unit's ends hold an end entry and are
-    // never read). One load for all lanes, no branch.
-    int win = pa;
-    int tbl = 0;
-    auto load_window = [&]() {
-      const int e = win + dir * lane;
-      tbl = table[min(max(e, 0), npg - 1)];
-    };
-    load_window();
-
-    // Loader state: the page being loaded (lpa, its id) and the next step in
-    // it; `loading` turns false when the unit or the tickets run out.
-    int lpa = pa;
-    int lsub = 0;
-    int lpid = 0;
-    bool loading = true;
-    int next_ticket = 0;
-    bool start_page = true;
-    int cnt = 0;  // pages of this unit taken by this wave
-    // Per ring slot: is it a real step, its first key position, page usable.
-    bool s_real[kNbuf];
-    int s_t0[kNbuf];
-    bool s_ok[kNbuf];
-    int64_t last_off = 0;
-    int64_t last_soff = 0;  // 8-bit: scale element of the step's first key
-
-    f16x8 kb[kNbuf][NV], vb[kNbuf][NV];
-    // 8-bit: this lane's key scale and the value scales of its pair's keys
-    // (own, other), kept apart until the step is computed so that no
-    // instruction waits on them at load time.
-    f16 ksb[kNbuf], vs_own_b[kNbuf], vs_other_b[kNbuf];
-
-    auto load_step = [&](int u) {
-      if (loading && start_page) {
-        // Start page lpa: its ticket was granted (`pending`); take the ticket
-        // of the page after it now, while this one loads.
-        if (!pending) {
-          loading = false;
-        } else {
-          pending = false;
-          ++cnt;
-          ++taken;
-          const int idx = dir * (lpa - win);
-          if (idx < 0 || idx >= kTablePages) {
-            // Rare: the next 64 entries. Read here, so the common path never
-            // waits on this load.
-            win = lpa;
-            load_window();
-            lpid = __builtin_amdgcn_readlane(tbl, 0);
-          } else {
-            lpid = __builtin_amdgcn_readlane(tbl, idx);
-          }
-          start_page = false;
-          next_ticket = take_ticket();
-        }
-      }
-      if (loading) {
-        const bool ok = lpid >= 0 && lpid < p.arena_pages;
-        const int pid = ok ? lpid : 0;
-        last_off = (int64_t)pid * p.page_bytes + lsub * KPS * p.row_bytes;
-        if constexpr (Q8) last_soff = (int64_t)pid * p.scale_page + lsub * KPS * p.scale_row;
-        s_real[u] = true;
-        s_t0[u] = (first_page + lpa) * P + lsub * KPS;
-        s_ok[u] = ok;
-        if (++lsub == spp) {
-          lsub = 0;
-          start_page = true;
-          lpa += dir;
-          // The ticket taken for the next page decides whether it is ours;
-          // past the unit's end it is the next unit's first page.
-          pending = granted(next_ticket);
-          if (lpa < 0 || lpa >= npg) loading = false;
-        }
-      } else {
-        s_real[u] = false;
-      }
-      // Once the unit is done the ring keeps reloading the last step (cache
-      // hits, never used), so every slot always has one load in flight.
-      const char* kq = kbase + last_off + lane_off;
-      const char* vq = vbase + last_off + v_off;
-      if constexpr (Q8) {
-        kb[u][0] = *reinterpret_cast<const f16x8*>(kq);
-        const uint2 va = *reinterpret_cast<const uint2*>(vq);
-        const uint2 vc = *reinterpret_cast<const uint2*>(vq + p.row_bytes);
-        vb[u][0] = __builtin_bit_cast(f16x8, i32x4{(int)va.x, (int)va.y, (int)vc.x, (int)vc.y});
-        const f16* ks = p.kscale + last_soff;
-        const f16* vs = p.vscale + last_soff;
-        ksb[u] = ks[ks_off];
-        vs_own_b[u] = vs[vs_own];
-        vs_other_b[u] = vs[vs_other];
-      } else {
-#pragma unroll
-        for (int v = 0; v < NV; ++v) {
-          kb[u][v] = *reinterpret_cast<const f16x8*>(kq + 2 * DC * v);
-          vb[u][v] = *reinterpret_cast<const f16x8*>(vq + (PV2 ? v * p.row_bytes : 2 * DC * v));
-        }
-      }
-    };
-
-    auto compute_step = [&](int u) {
-      if (!s_ok[u]) return;  // released or out-of-range page: masked
-      const int t0 = s_t0[u];
-      f16x8(&kd)[NV] = kb[u];
-      f16x8(&vd)[NV] = vb[u];
-      // q.k for every head of the group: v_dot2 over this lane's slice,
-      // then the butterfly over the R lanes of the key.
-      // This lane's key elements as fp16 pairs (8-bit: converted exactly).
-      f16x2 kp2[EPL / 2];
-      if constexpr (Q8) {
-        const i32x4 raw = __builtin_bit_cast(i32x4, kd[0]);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint32_t flipped = (uint32_t)raw[j] ^ 0x80808080u;
-          kp2[2 * j] = bytes_to_f16x2(flipped, 0x04010400u);
-          kp2[2 * j + 1] = bytes_to_f16x2(flipped, 0x04030402u);
-        }
-      } else {
-#pragma unroll
-        for (int v = 0; v < NV; ++v)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) kp2[4 * v + i] = f16x2{kd[v][2 * i], kd[v][2 * i + 1]};
-      }
-      float s[G];
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        float acc;
-        if constexpr (BF) {
-          acc = dot2_first_bf16(__builtin_bit_cast(bf16x2, q[g][0]),
-                                __builtin_bit_cast(bf16x2, kp2[0]));
-#pragma unroll
-          for (int i = 1; i < EPL / 2; ++i)
-            acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, q[g][i]),
-                                                  __builtin_bit_cast(bf16x2, kp2[i]), acc, false);
-        } else {
-          acc = dot2_first(q[g][0], kp2[0]);
-#pragma unroll
-          for (int i = 1; i < EPL / 2; ++i) acc = __builtin_amdgcn_fdot2(q[g][i], kp2[i], acc, false);
-        }
-        s[g] = acc;
-      }
-#pragma unroll
-      for (int g = 0; g < G; ++g) s[g] = group_sum<R>(s[g]);
-      // Scores in log2 units per unit of s (8-bit: times this key's scale,
-      // metal_kernels.py:52 KEY_SCALE).
-      float sl2 = p.scale_log2;
-      if constexpr (Q8) {
-        const float ksf = (float)ksb[u];
-        sl2 *= ksf;
-        if (p.softcap > 0.0f) {
-#pragma unroll
-          for (int g = 0; g < G; ++g) s[g] *= ksf;
-        }
-      }
-      // x = score - running max, in log2 units; softcap c * tanh(x / c)
-      // (metal_kernels.py:53) as c * (1 - 2 / (e^(2x/c) + 1)).
-      float x[G];
-      if (p.softcap > 0.0f) {
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          const float e = __builtin_amdgcn_exp2f(s[g] * p.cap_in);
-          x[g] = (1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f)) * p.cap_out - m[g];
-        }
-      } else {
-#pragma unroll
-        for (int g = 0; g < G; ++g) x[g] = __builtin_fmaf(s[g], sl2, -m[g]);
-      }
-      if (!(t0 >= first && t0 + KPS <= len)) {
-        // Boundary step. A step with no visible key is skipped: before the
-        // first visible key the running max is still -inf, and -inf - -inf
-        // would poison the sums. Rows outside [first, len) may hold
-        // anything, so their scores are masked and their values zeroed.
-        const int t = t0 + kk;
-        const bool valid = t >= first && t < len;
-        if (!__any(valid)) return;
-#pragma unroll
-        for (int g = 0; g < G; ++g) x[g] = valid ? x[g] : -INFINITY;
-        if constexpr (Q8) {
-          // Zero bytes are zero values; the scales of masked keys may hold
-          // anything, so they are zeroed too.
-          const int ta = t0 + 2 * kp;
-          const bool v0 = ta >= first && ta < len, v1 = ta + 1 >= first && ta + 1 < len;
-          i32x4 bits = __builtin_bit_cast(i32x4, vd[0]);
-          bits.x = v0 ? bits.x : 0;
-          bits.y = v0 ? bits.y : 0;
-          bits.z = v1 ? bits.z : 0;
-          bits.w = v1 ? bits.w : 0;
-          vd[0] = __builtin_bit_cast(f16x8, bits);
-          const bool own_ok = hi ? v1 : v0, other_ok = hi ? v0 : v1;
-          vs_own_b[u] = own_ok ? vs_own_b[u] : (f16)0.0f;
-          vs_other_b[u] = other_ok ? vs_other_b[u] : (f16)0.0f;
-        } else if constexpr (PV2) {
-          const int ta = t0 + 2 * kp;
-#pragma unroll
-          for (int v = 0; v < NV; ++v) vd[v] = zero_unless(vd[v], ta + v >= first && ta + v < len);
-        } else {
-#pragma unroll
-          for (int v = 0; v < NV; ++v) vd[v] = zero_unless(vd[v], valid);
-        }
-      }
-      bool grow = false;
-#pragma unroll
-      for (int g = 0; g < G; ++g) grow |= x[g] > kSlack;
-      if (__any(grow)) {
-        // Rare: a score passed the running max by 2^8 (always so for the
-        // first visible key, while the max is -inf). Raise the max to the
-        // wave's largest score and rescale what was summed so far. The
-        // scores are recomputed from s: x + m would be inf - inf there.
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          float sc;
-          if (p.softcap > 0.0f) {
-            const float e = __builtin_amdgcn_exp2f(s[g] * p.cap_in);
-            sc = (1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f)) * p.cap_out;
-          } else {
-            sc = s[g] * sl2;
-          }
-          sc = x[g] == -INFINITY ? -INFINITY : sc;  // masked keys stay out
-          const float mn = fmaxf(m[g], wave_max(sc));
-          const float f = __builtin_amdgcn_exp2f(m[g] - mn);
-          x[g] = sc - mn;
-          m[g] = mn;
-          l[g] *= f;
-#pragma unroll
-          for (int i = 0; i < OPL; ++i) o[g][i] *= f;
-        }
-      }
-      if constexpr (PV2) {
-        // V element pairs (this lane's key, the other key of its pair),
-        // shared by all heads.
-        f16x2 vv[8];
-        if constexpr (Q8) {
-          // Bytes of keys 2 kp (dwords x, y) and 2 kp + 1 (z, w), elements
-          // r2 * 8 .. r2 * 8 + 7: interleave them (this lane's key first),
-          // convert exactly, then weight by the keys' value scales
-          // (metal_kernels.py:58 VALUE_SCALE).
-          const i32x4 raw = __builtin_bit_cast(i32x4, vd[0]);
-          const f16x2 vsp = f16x2{vs_own_b[u], vs_other_b[u]};
-#pragma unroll
-          for (int j = 0; j < 2; ++j) {
-            const uint32_t a = (uint32_t)raw[j] ^ 0x80808080u;
-            const uint32_t c = (uint32_t)raw[2 + j] ^ 0x80808080u;
-            const uint32_t lo = __builtin_amdgcn_perm(a, c, sel8_lo);  // elements 4j, 4j + 1
-            const uint32_t hi2 = __builtin_amdgcn_perm(a, c, sel8_hi); // elements 4j + 2, 4j + 3
-            vv[4 * j] = bytes_to_f16x2(lo, 0x04010400u) * vsp;
-            vv[4 * j + 1] = bytes_to_f16x2(lo, 0x04030402u) * vsp;
-            vv[4 * j + 2] = bytes_to_f16x2(hi2, 0x04010400u) * vsp;
-            vv[4 * j + 3] = bytes_to_f16x2(hi2, 0x04030402u) * vsp;
-          }
-        } else {
-          const i32x4 va = __builtin_bit_cast(i32x4, vd[0]);  // key 2 kp
-          const i32x4 vb = __builtin_bit_cast(i32x4, vd[1]);  // key 2 kp + 1
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            vv[2 * j] = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(va[j], vb[j], sel_lo));
-            vv[2 * j + 1] = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(va[j], vb[j], sel_hi));
-          }
-        }
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          // Probabilities of the pair's two keys as fp16: this lane holds its
-          // own key's, lane ^ R the other's. The sum uses the same rounded
-          // values, so the weights stay a normalised combination.
-          const float pr = __builtin_amdgcn_exp2f(x[g]);
-          const float other = pair_swap<R>(pr);
-          if constexpr (BF) {
-            const bf16x2 pp = bf16x2{(bf16)pr, (bf16)other};
-            l[g] = __builtin_amdgcn_fdot2_f32_bf16(pp, bf16x2{(bf16)1.0f, (bf16)1.0f}, l[g], false);
-#pragma unroll
-            for (int i = 0; i < 8; ++i)
-              o[g][i] = __builtin_amdgcn_fdot2_f32_bf16(pp, __builtin_bit_cast(bf16x2, vv[i]),
-                                                        o[g][i], false);
-          } else {
-            const f16x2 pp = f16x2{(f16)pr, (f16)other};
-            l[g] = __builtin_amdgcn_fdot2(pp, f16x2{(f16)1.0f, (f16)1.0f}, l[g], false);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) o[g][i] = __builtin_amdgcn_fdot2(pp, vv[i], o[g][i], false);
-          }
-        }
-      } else {
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          const float pr = __builtin_amdgcn_exp2f(x[g]);
-          l[g] += pr;
-#pragma unroll
-          for (int v = 0; v < NV; ++v) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i)
-              o[g][8 * v + i] = __builtin_fmaf(
-                  pr, BF ? (float)__builtin_bit_cast(bf16x8, vd[v])[i] : (float)vd[v][i],
-                  o[g][8 * v + i]);
-          }
-        }
-      }
-    };
-
-#pragma unroll
-    for (int u = 0; u < kNbuf; ++u) load_step(u);
-    // The ring: every slot is waited for (its loads are complete once only
-    // the other slots' remain), computed if it holds a real step and
-    // reloaded, in issue order on every path, with the loop test at the
-    // bottom; the compiler's wait counts then stay those of a steady ring.
-    do {
-#pragma unroll
-      for (int u = 0; u < kNbuf; ++u) {
-        wait_vmem<(kNbuf - 1) * Gm::LOADS>();
-        if (s_real[u]) compute_step(u);
-        load_step(u);
-      }
-    } while (s_real[0]);
-    // `pending` now tells whether the page after this unit is ours too.
-
-    // Fold the wave's key subsets (metal_kernels.py:63-81); every lane then
-    // holds the totals of its elements. On the p.v pair path the lanes of
-    // key pair kp write the heads g with g % NPAIR == kp, elements r2 * 8 ..;
-    // otherwise the lanes of key subset kk write the heads g with
-    // g % KPS == kk, in chunks.
-    constexpr int kWriters = PV2 ? Gm::NPAIR : KPS;
-    const int writer = PV2 ? kp : kk;
-    const bool writes = PV2 || active;
-    const int e0 = PV2 ? r2 * 8 : d0;      // first output element of this lane
-    const int estride = PV2 ? 8 : DC;     // between its chunks of 8
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      if constexpr (PV2) {
-        l[g] = pair_sum<R>(l[g]);
-#pragma unroll
-        for (int i = 0; i < OPL; ++i) o[g][i] = pair_sum<R>(o[g][i]);
-      } else {
-        l[g] = subset_sum<R>(l[g]);
-#pragma unroll
-        for (int i = 0; i < OPL; ++i) o[g][i] = subset_sum<R>(o[g][i]);
-      }
-    }
-    if (cnt == npg) {
-      // The whole unit is here: normalise and write (metal_kernels.py:87-91).
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        if (g % kWriters != writer || !writes) continue;
-        const float inv = l[g] > 0.0f ? 1.0f / l[g] : 0.0f;
-        f16* dst = p.out + ((int64_t)b * p.hq + h0 + g) * D + e0;
-#pragma unroll
-        for (int v = 0; v < OPL / 8; ++v) {
-          if constexpr (BF) {
-            bf16x8 y;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) y[i] = (bf16)(o[g][8 * v + i] * inv);
-            *reinterpret_cast<bf16x8*>(dst + estride * v) = y;
-          } else {
-            f16x8 y;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) y[i] = (f16)(o[g][8 * v + i] * inv);
-            *reinterpret_cast<f16x8*>(dst + estride * v) = y;
-          }
-        }
-      }
-    } else {
-      // Cut unit: unnormalised partial (metal_kernels.py:93-101) in slot 0 if
-      // the unit holds the first page of this wave's final range (the first
-      // wave's first unit, the second wave's last), else in slot 1.
-      const bool holds_start = back ? !pending : first_unit;
-      const int64_t slot = 2 * vw + (holds_start ? 0 : 1);
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        if (g % kWriters != writer || !writes) continue;
-        float* dst = p.part_o + (slot * G + g) * D + e0;
-#pragma unroll
-        for (int i = 0; i < OPL; i += 4)
-          *reinterpret_cast<float4*>(dst + estride * (i / 8) + i % 8) =
-              make_float4(o[g][i], o[g][i + 1], o[g][i + 2], o[g][i + 3]);
-        if ((PV2 ? r2 : r) == 0) p.part_ml[slot * G + g] = make_float2(m[g], l[g]);
-      }
-    }
-    first_unit = false;
-    if (!pending) break;
-
-    // The next unit along the wave's way (empty sequences hold no pages).
-    if (!back) {
-      if (++kvg == nkvg) {
-        kvg = 0;
-        do {
-          ++b;
-        } while (b < B && s_prefix[b + 1] == s_prefix[b]);
-      }
-      if (b >= B) break;  // cannot happen: tickets never pass the range
-      npg = s_prefix[b + 1] - s_prefix[b];
-      pa = 0;
-    } else {
-      if (--kvg < 0) {
-        kvg = nkvg - 1;
-        do {
-          --b;
-        } while (b >= 0 && s_prefix[b + 1] == s_prefix[b]);
-      }
-      if (b < 0) break;  // cannot happen: tickets never pass the range
-      npg = s_prefix[b + 1] - s_prefix[b];
-      pa = npg - 1;
-    }
-  }
-  // The first wave of the pair records the meeting point for the merge.
-  if (!back && lane == 0) p.meet[pair] = taken;
-}
-
-// Merge kernel (metal_kernels.py:103-124): one workgroup of MW waves per
-// (sequence, kv head group, head of the group). The unit's pages [s, e) of
-// the stream lie in the ranges of pairs qa..qb; pair q split its range
-// [X, Xn) at M = X + meet[q] into the first wave's [X, M) and the second
-// wave's [M, Xn). Each of these ranges that meets [s, e) holds one piece of
-// the unit, in slot 0 of that wave if the range starts inside the unit, else
-// in slot 1. A unit with one piece was written by the split kernel, one with
-// no visible page zeroed there. Candidate pieces are numbered 2 (q - qa) +
-// (second wave); wave w takes the batches of kBatch candidates w, w + MW, ...:
-// one lane per candidate reads its pair's meeting point, then the loads of
-// all pieces of the batch go out together and the batch is combined at once
-// against its own maximum with log-sum-exp weights (pieces whose max is -inf
-// hold no visible key and weigh 0; a zero total gives 0, :116,122). Batches
-// and waves are folded in a fixed order, so the result does not depend on
-// timing.
-template <int D, int G, bool BF>
-__global__ __launch_bounds__(kMergeMaxWaves * 64) void paged_decode_merge_kernel(const Params p) {
-  constexpr int kChunks = (D + 63) / 64;  // elements l, l + 64, ... of lane l
-  constexpr int kBatch = 32 / kChunks;    // candidates whose loads go out together
-  __shared__ float s_top[kMergeMaxWaves], s_sum[kMergeMaxWaves];
-  __shared__ float s_acc[kMergeMaxWaves][kChunks * 64];
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int w = uniform(tid >> 6);
-  const int mw = blockDim.x >> 6;
-  const int kvg = blockIdx.x / G;
-  const int g = blockIdx.x - kvg * G;
-  const int b = blockIdx.y;
-  const int kvh = kvg / p.nhg;
-  const int h = kvh * p.gtot + (kvg - kvh * p.nhg) * G + g;
-  f16* const dst = p.out + ((int64_t)b * p.hq + h) * D;
-  const int nkvg = p.hkv * p.nhg;
-  const int pb0 = p.prefix[b];
-  const int npg = p.prefix[b + 1] - pb0;
-  if (npg == 0) return;  // zeroed by the split kernel
-  const int64_t total = (int64_t)p.prefix[p.batch] * nkvg;
-  const int pairs = stream_pairs(total, p);
-  const int64_t s = (int64_t)pb0 * nkvg + (int64_t)kvg * npg;
-  const int64_t e = s + npg;
-  const int qa = pair_of(s, total, pairs);
-  const int qb = pair_of(e - 1, total, pairs);
-  const int cand = 2 * (qb - qa + 1);
-
-  // Slot of candidate j, or -1 when that wave's range misses the unit.
-  auto piece_slot = [&](int j) -> int {
-    const int q = qa + (j >> 1);
-    const int64_t X = range_start(q, total, pairs);
-    const int64_t Xn = range_start(q + 1, total, pairs);
-    const int64_t M = X + p.meet[q];
-    if ((j & 1) == 0)
-      return X < M && X < e && M > s ? 2 * (2 * q) + (X >= s ? 0 : 1) : -1;
-    return M < Xn && M < e && Xn > s ? 2 * (2 * q + 1) + (M >= s ? 0 : 1) : -1;
-  };
-  if (cand == 2) {
-    // Inside one pair's range: a single piece means one wave held the whole
-    // unit and wrote it.
-    const int sl = lane < 2 ? piece_slot(lane) : -1;
-    if (__popcll(__ballot(sl >= 0)) <= 1) return;
-  }
-
-  float top = -INFINITY, sum = 0.0f, acc[kChunks];
-#pragma unroll
-  for (int c = 0; c < kChunks; ++c) acc[c] = 0.0f;
-  for (int base = w * kBatch; base < cand; base += mw * kBatch) {
-    const int mine = lane < kBatch && base + lane < cand ? piece_slot(base + lane) : -1;
-    int sl[kBatch];
-    float2 ml[kBatch];
-    float part[kBatch][kChunks];
-#pragma unroll
-    for (int u = 0; u < kBatch; ++u) {
-      sl[u] = __builtin_amdgcn_readlane(mine, u);
-      const int64_t at = sl[u] < 0 ? 0 : sl[u];
-      ml[u] = p.part_ml[at * G + g];
-#pragma unroll
-      for (int c = 0; c < kChunks; ++c) {
-        const int d = c * 64 + lane;
-        part[u][c] = d < D ? p.part_o[(at * G + g) * D + d] : 0.0f;
-      }
-    }
-    float bt = -INFINITY;
-#pragma unroll
-    for (int u = 0; u < kBatch; ++u)
-      if (sl[u] >= 0) bt = fmaxf(bt, ml[u].x);
-    if (bt == -INFINITY) continue;  // no visible key in this batch
-    float bs = 0.0f, ba[kChunks];
-#pragma unroll
-    for (int c = 0; c < kChunks; ++c) ba[c] = 0.0f;
-#pragma unroll
-    for (int u = 0; u < kBatch; ++u) {
-      const float wt = sl[u] >= 0 ? __builtin_amdgcn_exp2f(ml[u].x - bt) : 0.0f;
-      bs = __builtin_fmaf(wt, ml[u].y, bs);
-#pragma unroll
-      for (int c = 0; c < kChunks; ++c) ba[c] = __builtin_fmaf(wt, part[u][c], ba[c]);
-    }
-    lse_add<kChunks>(top, sum, acc, make_float2(bt, bs), ba);
-  }
-  if (mw > 1) {
-    // Combine the waves: each publishes its maximum, rescales to the common
-    // one and leaves its sums in LDS; wave 0 adds them in a fixed order.
-    if (lane == 0) s_top[w] = top;
-    __syncthreads();
-    float all = -INFINITY;
-    for (int x = 0; x < mw; ++x) all = fmaxf(all, s_top[x]);
-    const float f = top == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(top - all);
-#pragma unroll
-    for (int c = 0; c < kChunks; ++c) s_acc[w][c * 64 + lane] = acc[c] * f;
-    if (lane == 0) s_sum[w] = sum * f;
-    __syncthreads();
-    if (w != 0) return;
-    sum = 0.0f;
-#pragma unroll
-    for (int c = 0; c < kChunks; ++c) acc[c] = 0.0f;
-    for (int x = 0; x < mw; ++x) {
-      sum += s_sum[x];
-#pragma unroll
-      for (int c = 0; c < kChunks; ++c) acc[c] += s_acc[x][c * 64 + lane];
-    }
-  }
-  const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
-#pragma unroll
-  for (int c = 0; c < kChunks; ++c)
-    if (c * 64 + lane < D) {
-      if constexpr (BF)
-        dst[c * 64 + lane] = __builtin_bit_cast(f16, (bf16)(acc[c] * inv));
-      else
-        dst[c * 64 + lane] = (f16)(acc[c] * inv);
-    }
-}
-
-// ---------------------------------------------------------------------------
-// Host side: validation, planning, dispatch.
-
+using namespace pda_decode;
 using pda_internal::fail;
 using pda_internal::ok;
 
-using KernelFn = void (*)(Params);
-
-struct KernelPair {
-  KernelFn split = nullptr;
-  KernelFn merge = nullptr;
-};
-
-template <int D, int G, bool Q8, bool BF>
-KernelPair pair() {
-  return {paged_decode_kernel<D, G, Q8, BF>, paged_decode_merge_kernel<D, G, BF>};
+// Head dims with a compiled fast path: 16-bit 64, 80, 96, 128, 256, 512;
+// 8-bit 64, 128, 256, 512 (the dims whose p.v runs on key pairs). Every
+// other even head dim up to 512 runs a generic kernel padded to a power of
+// two (any dim at 8 bits that has no fast path, 80 included).
+bool fast_dim(int d, bool q8) {
+  if (q8) return d == 64 || d == 128 || d == 256 || d == 512;
+  return d == 64 || d == 80 || d == 96 || d == 128 || d == 256 || d == 512;
 }
 
-template <int D, bool Q8, bool BF = false>
-KernelPair kernels_for_g(int g) {
-  switch (g) {
-    case 1: return pair<D, 1, Q8, BF>();
-    case 2: return pair<D, 2, Q8, BF>();
-    case 3: return pair<D, 3, Q8, BF>();
-    case 4: return pair<D, 4, Q8, BF>();
-    case 5: return pair<D, 5, Q8, BF>();
-    case 6: return pair<D, 6, Q8, BF>();
-    case 7: return pair<D, 7, Q8, BF>();
-    case 8: return pair<D, 8, Q8, BF>();
-  }
-  return {};
+// Padded head dim of a generic kernel: the next power of two, at least 8.
+int generic_dim(int d) {
+  int dp = 8;
+  while (dp < d) dp <<= 1;
+  return dp;
 }
 
-// Compiled head dims: fp16 and bf16 K/V 64, 80, 96, 128, 256, 512; 8-bit K/V
-// the dims whose p.v runs on key pairs (64, 128, 256, 512).
+// The head dim the kernels lay partials out on: d, or its generic padding.
+int kernel_dim(int d, bool q8) { return fast_dim(d, q8) ? d : generic_dim(d); }
+
+// Partial row length the workspace is sized for: the larger of the 16-bit
+// and 8-bit layouts, so pda_workspace_bytes holds for either cache.
+int workspace_dim(int d) { return std::max(kernel_dim(d, false), kernel_dim(d, true)); }
+
 KernelPair kernels_for(int d, int g, bool q8, bool bf16 = false) {
-  if (bf16) {
-    switch (d) {
-      case 64: return kernels_for_g<64, false, true>(g);
-      case 80: return kernels_for_g<80, false, true>(g);
-      case 96: return kernels_for_g<96, false, true>(g);
-      case 128: return kernels_for_g<128, false, true>(g);
-      case 256: return kernels_for_g<256, false, true>(g);
-      case 512: return kernels_for_g<512, false, true>(g);
-    }
-    return {};
-  }
-  if (q8) {
-    switch (d) {
-      case 64: return kernels_for_g<64, true>(g);
-      case 128: return kernels_for_g<128, true>(g);
-      case 256: return kernels_for_g<256, true>(g);
-      case 512: return kernels_for_g<512, true>(g);
-    }
-    return {};
-  }
-  switch (d) {
-    case 64: return kernels_for_g<64, false>(g);
-    case 80: return kernels_for_g<80, false>(g);
-    case 96: return kernels_for_g<96, false>(g);
-    case 128: return kernels_for_g<128, false>(g);
-    case 256: return kernels_for_g<256, false>(g);
-    case 512: return kernels_for_g<512, false>(g);
-  }
-  return {};
+  if (d <= 0 || d > 512 || d % 2) return {};
+  if (fast_dim(d, q8)) return bf16 ? kernels_bf16(d, g) : q8 ? kernels_q8(d, g) : kernels_f16(d, g);
+  const int dp = generic_dim(d);
+  return bf16 ? kernels_gen_bf16(dp, g) : q8 ? kernels_gen_q8(dp, g) : kernels_gen_f16(dp, g);
 }
 
+// Keys one wave step covers for a head dim (generic kernels: 8 elements per
+// lane, so 64 / (dp / 8) keys).
 int keys_per_step(int d, bool q8) {
+  if (!fast_dim(d, q8)) return 64 / (generic_dim(d) / 8);
   if (q8) {
     switch (d) {
       case 64: return Geom<64, true>::KPS;
@@ -1168,7 +165,7 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 int make_plan(int32_t batch, int32_t q_heads, int32_t kv_heads, int32_t head_dim,
               int32_t page_size, int32_t table_stride, int32_t longest,
-              int32_t window, int32_t split_pages, Plan* out, bool q8 = false) {
+              int32_t window, int32_t split_pages, Plan* out) {
   if (batch < 0 || q_heads <= 0 || kv_heads <= 0 || head_dim <= 0 ||
       page_size <= 0 || table_stride <= 0 || window < 0 || split_pages < 0)
     return fail(PDA_ERR_INVALID_ARGUMENT,
@@ -1178,14 +175,8 @@ int make_plan(int32_t batch, int32_t q_heads, int32_t kv_heads, int32_t head_dim
                 window, split_pages);
   if (q_heads % kv_heads)
     return fail(PDA_ERR_HEAD_RATIO, "query heads must be a multiple of kv heads");
-  if (!kernels_for(head_dim, 1, q8).split)
-    return fail(PDA_ERR_HEAD_DIM, "head_dim %d has no %s kernel (supported: %s)", head_dim,
-                q8 ? "8-bit" : "fp16", q8 ? "64, 128, 256, 512" : "64, 80, 96, 128, 256, 512");
-  const int kps = keys_per_step(head_dim, q8);
-  if (page_size % kps)
-    return fail(PDA_ERR_PAGE_SIZE,
-                "page_size %d must be a multiple of %d for head_dim %d",
-                page_size, kps, head_dim);
+  if (head_dim > 512 || head_dim % 2)
+    return fail(PDA_ERR_HEAD_DIM, "head_dim %d is not an even number up to 512", head_dim);
   if ((int64_t)table_stride * page_size > INT32_MAX)
     return fail(PDA_ERR_TOO_LONG, "table_stride * page_size exceeds 2^31");
   if (batch > kMaxBatch)
@@ -1214,7 +205,7 @@ int make_plan(int32_t batch, int32_t q_heads, int32_t kv_heads, int32_t head_dim
   pl.off_meet = align256((size_t)(batch + 1) * sizeof(int32_t));
   pl.off_ml = pl.off_meet + align256((size_t)kMaxPairs * sizeof(int32_t));
   pl.off_o = pl.off_ml + align256((size_t)kSlots * pl.G * sizeof(float2));
-  pl.total = pl.off_o + align256((size_t)kSlots * pl.G * head_dim * sizeof(float));
+  pl.total = pl.off_o + align256((size_t)kSlots * pl.G * workspace_dim(head_dim) * sizeof(float));
   *out = pl;
   return PDA_OK;
 }
@@ -1256,7 +247,7 @@ int merge_waves(const Plan& pl, int head_dim, int grid_pairs) {
 
 extern "C" {
 
-int pda_version(void) { return (0 << 16) | 5; }
+int pda_version(void) { return (0 << 16) | 6; }
 
 const char* pda_last_error(void) { return pda_internal::last_error(); }
 
@@ -1306,12 +297,12 @@ int decode(int passes, const void* queries, const void* keys, const void* values
            const int32_t* tables, const int32_t* lengths, void* out, int32_t batch,
            int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t page_size,
            int32_t table_stride, int64_t arena_rows, int32_t layout, int32_t longest,
-           float scale, int32_t window, float softcap, int32_t split_pages, void* workspace,
-           size_t workspace_bytes, void* stream) {
+           float scale, int32_t window, float softcap, int32_t split_pages, int32_t flags,
+           void* workspace, size_t workspace_bytes, void* stream) {
   const bool q8 = key_scales || value_scales;
   Plan pl;
   int rc = make_plan(batch, q_heads, kv_heads, head_dim, page_size, table_stride,
-                     longest, window, split_pages, &pl, q8);
+                     longest, window, split_pages, &pl);
   if (rc) return rc;
   if (batch == 0) return ok();
   if (!queries || !keys || !values || !tables || !lengths || !out ||
@@ -1322,6 +313,8 @@ int decode(int passes, const void* queries, const void* keys, const void* values
                 (long long)arena_rows);
   if (layout != PDA_LAYOUT_ROWS && layout != PDA_LAYOUT_PAGES)
     return fail(PDA_ERR_INVALID_ARGUMENT, "unknown K/V layout %d", layout);
+  if (flags & ~PDA_DECODE_FIXED_SPLIT)
+    return fail(PDA_ERR_INVALID_ARGUMENT, "unknown decode flags 0x%x", flags);
   const int elem = q8 ? 1 : 2;  // bytes per K/V element
   const int64_t page_bytes = (int64_t)page_size * kv_heads * head_dim * elem;
   if (page_bytes > INT32_MAX)
@@ -1343,6 +336,7 @@ int decode(int passes, const void* queries, const void* keys, const void* values
     return fail(PDA_ERR_ALIGNMENT, "workspace must be 256-byte aligned");
 
   const KernelPair kp = kernels_for(head_dim, pl.G, q8, bf16);
+  if (!kp.split) return fail(PDA_ERR_HEAD_DIM, "head_dim %d has no kernel", head_dim);
   const size_t lds = (size_t)(2 * batch + 1) * sizeof(int32_t);
   const int groups = resident_groups(kp.split, lds);
   if (groups < 0) return fail(PDA_ERR_HIP, "device query failed");
@@ -1380,11 +374,14 @@ int decode(int passes, const void* queries, const void* keys, const void* values
   prm.page_size = page_size;
   prm.hq = q_heads;
   prm.hkv = kv_heads;
+  prm.head_dim = head_dim;
   prm.gtot = q_heads / kv_heads;
   prm.nhg = pl.nhg;
   prm.window = window;
   prm.grid_pairs = groups * kPairs;
   prm.min_pages = pl.min_pages;
+  prm.fixed = (flags & PDA_DECODE_FIXED_SPLIT) ? 1 : 0;
+  prm.ragged = page_size % keys_per_step(head_dim, q8) ? 1 : 0;
   prm.scale_log2 = scale * kLog2e;
   prm.softcap = softcap;
   prm.cap_in = softcap > 0.0f ? 2.0f * kLog2e * scale / softcap : 0.0f;
@@ -1416,12 +413,12 @@ extern "C" {
       int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t page_size,  \
       int32_t table_stride, int64_t arena_rows, int32_t layout,                \
       int32_t longest, float scale, int32_t window, float softcap,             \
-      int32_t split_pages, void *workspace, size_t workspace_bytes,            \
-      void *stream
+      int32_t split_pages, int32_t flags, void *workspace,                     \
+      size_t workspace_bytes, void *stream
 #define PDA_DECODE_ARGS(BF16)                                                  \
   queries, keys, values, nullptr, nullptr, BF16, tables, lengths, out, batch,  \
       q_heads, kv_heads, head_dim, page_size, table_stride, arena_rows,        \
-      layout, longest, scale, window, softcap, split_pages, workspace,         \
+      layout, longest, scale, window, softcap, split_pages, flags, workspace,  \
       workspace_bytes, stream
 #define PDA_DECODE_PARAMS_Q8                                                   \
   const void *queries, const void *keys, const void *values,                   \
@@ -1430,12 +427,12 @@ extern "C" {
       int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t page_size,  \
       int32_t table_stride, int64_t arena_rows, int32_t layout,                \
       int32_t longest, float scale, int32_t window, float softcap,             \
-      int32_t split_pages, void *workspace, size_t workspace_bytes,            \
-      void *stream
+      int32_t split_pages, int32_t flags, void *workspace,                     \
+      size_t workspace_bytes, void *stream
 #define PDA_DECODE_ARGS_Q8                                                     \
   queries, keys, values, key_scales, value_scales, false, tables, lengths, out,\
       batch, q_heads, kv_heads, head_dim, page_size, table_stride, arena_rows, \
-      layout, longest, scale, window, softcap, split_pages, workspace,         \
+      layout, longest, scale, window, softcap, split_pages, flags, workspace,  \
       workspace_bytes, stream
 
 int pda_paged_decode_attention(PDA_DECODE_PARAMS) {

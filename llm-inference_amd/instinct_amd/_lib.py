@@ -26,6 +26,9 @@ PDA_ERR_ALIGNMENT = -6
 PDA_ERR_TOO_LONG = -7
 PDA_ERR_HIP = -8
 
+# Decode flags (pda.h).
+PDA_DECODE_FIXED_SPLIT = 1  # fixed split points: bitwise reproducible output
+
 # K/V arena layouts (pda.h).
 PDA_LAYOUT_ROWS = 0   # [rows, kv_heads, head_dim], the reference's arena
 PDA_LAYOUT_PAGES = 1  # [pages, kv_heads, page_size, head_dim] tiles
@@ -44,8 +47,8 @@ SIGNATURES = {
     ),
 }
 _DECODE_ARGS = ([c_void_p] * 6 + [c_int32] * 6
-                + [c_int64, c_int32, c_int32, c_float, c_int32, c_float, c_int32, c_void_p,
-                   c_size_t, c_void_p])
+                + [c_int64, c_int32, c_int32, c_float, c_int32, c_float, c_int32, c_int32,
+                   c_void_p, c_size_t, c_void_p])
 for _name in ("pda_paged_decode_attention", "pda_decode_split", "pda_decode_merge"):
     SIGNATURES[_name] = (ctypes.c_int, _DECODE_ARGS)
     SIGNATURES[_name + "_bf16"] = (ctypes.c_int, _DECODE_ARGS)

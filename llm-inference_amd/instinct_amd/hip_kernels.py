@@ -73,6 +73,27 @@ def _given_workspace(ws: torch.Tensor, device: torch.device, nbytes: int) -> tor
     return ws
 
 
+_FAST_DIMS = {16: (64, 80, 96, 128, 256, 512), 8: (64, 128, 256, 512)}
+
+
+def decode_kernel_names(q_heads: int, kv_heads: int, head_dim: int, *, bits: int = 16,
+                        bf16: bool = False) -> dict[str, Any]:
+    """The kernels a decode call of this shape launches, as the library's
+    dispatch picks them (csrc/pda_kernels.hip ``kernels_for`` and
+    ``heads_per_group``): template arguments ``<D, G, Q8, BF, GEN>`` of the
+    split and merge kernels, the query heads one unit serves (G) and the
+    head groups per kv head (each re-reads the kv head's K/V)."""
+    group = q_heads // kv_heads
+    heads = next(g for g in range(min(group, 8), 0, -1) if group % g == 0)
+    generic = head_dim not in _FAST_DIMS[bits]
+    dim = max(8, 1 << (head_dim - 1).bit_length()) if generic else head_dim
+    b = lambda x: str(bool(x)).lower()  # noqa: E731
+    targs = f"{dim},{heads},{b(bits == 8)},{b(bf16)},{b(generic)}"
+    return {"split": f"paged_decode_kernel<{targs}>",
+            "merge": f"paged_decode_merge_kernel<{dim},{heads},{b(bf16)},{b(generic)}>",
+            "heads_per_unit": heads, "head_groups_per_kv_head": group // heads}
+
+
 def decode_workspace_bytes(queries_shape: tuple[int, int, int], keys: torch.Tensor, *,
                            page_size: int, table_width: int, longest: int, window: int = 0,
                            split_pages: int = 0) -> int:
@@ -100,6 +121,7 @@ def paged_decode_attention(
     out: torch.Tensor | None = None,
     passes: str = "both",
     workspace: torch.Tensor | None = None,
+    deterministic: bool = False,
 ) -> torch.Tensor:
     """Attention for one new token per sequence over its paged keys
     (metal_kernels.py:164-186). ``split_pages`` is the fewest pages a wave
@@ -108,6 +130,13 @@ def paged_decode_attention(
     one of the two kernels only (the output is complete after the merge).
     ``workspace``: a uint8 device tensor the caller owns (at least
     :func:`decode_workspace_bytes`), else the stream's cached one.
+    ``deterministic``: fixed split points (``PDA_DECODE_FIXED_SPLIT``), so
+    repeated calls on the same inputs give bitwise-identical outputs, as the
+    reference's fixed split ranges do (metal_kernels.py:32-36); without it
+    the split points follow the waves' progress and the last bits of a
+    sequence's output can differ from call to call (within the parity bar).
+    Any even ``head_dim`` up to 512 and any ``page_size`` are accepted, as by
+    the reference op (metal_kernels.py:28-30,204).
 
     ``scales`` = (key_scales, value_scales) selects 8-bit K/V
     (metal_kernels.py:134-141): ``keys``/``values`` are int8 arenas and the
@@ -177,7 +206,8 @@ def paged_decode_attention(
         queries.data_ptr(), keys.data_ptr(), values.data_ptr(), *extra, tables.data_ptr(),
         lengths.data_ptr(), out.data_ptr(), batch, q_heads, kv_heads, head_dim,
         int(page_size), stride, arena_rows, layout, int(longest), float(scale),
-        int(window), float(softcap), int(split_pages), ws.data_ptr(),
+        int(window), float(softcap), int(split_pages),
+        _lib.PDA_DECODE_FIXED_SPLIT if deterministic else 0, ws.data_ptr(),
         ws.numel(), ctypes.c_void_p(stream))
     _lib.check(rc)
     return out

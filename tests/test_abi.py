@@ -35,8 +35,8 @@ def decode(**overrides):
                 batch=4, q_heads=28, kv_heads=4, head_dim=128, page_size=16,
                 table_stride=64, arena_rows=4096, layout=_lib.PDA_LAYOUT_ROWS,
                 longest=1000, scale=0.088, window=0,
-                softcap=0.0, split_pages=0, workspace=FAKE * 16, workspace_bytes=1 << 30,
-                stream=None)
+                softcap=0.0, split_pages=0, flags=0, workspace=FAKE * 16,
+                workspace_bytes=1 << 30, stream=None)
     args.update(overrides)
     lib = _lib.library()
     return lib.pda_paged_decode_attention(*args.values())
@@ -44,11 +44,10 @@ def decode(**overrides):
 
 @pytest.mark.parametrize("overrides, code", [
     (dict(q_heads=30), _lib.PDA_ERR_HEAD_RATIO),
-    (dict(head_dim=72), _lib.PDA_ERR_HEAD_DIM),
-    (dict(head_dim=4, q_heads=2, kv_heads=1), _lib.PDA_ERR_HEAD_DIM),
-    (dict(page_size=12), _lib.PDA_ERR_PAGE_SIZE),
-    (dict(page_size=4), _lib.PDA_ERR_PAGE_SIZE),
-    (dict(head_dim=256, page_size=2), _lib.PDA_ERR_PAGE_SIZE),
+    (dict(head_dim=7), _lib.PDA_ERR_HEAD_DIM),
+    (dict(head_dim=514), _lib.PDA_ERR_HEAD_DIM),
+    (dict(head_dim=0), _lib.PDA_ERR_INVALID_ARGUMENT),
+    (dict(flags=2), _lib.PDA_ERR_INVALID_ARGUMENT),
     (dict(kv_heads=0), _lib.PDA_ERR_INVALID_ARGUMENT),
     (dict(batch=-1), _lib.PDA_ERR_INVALID_ARGUMENT),
     (dict(window=-1), _lib.PDA_ERR_INVALID_ARGUMENT),

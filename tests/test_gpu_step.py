@@ -136,6 +136,9 @@ def test_graph_keeps_its_workspace_when_the_stream_cache_grows(gpu):
     replay after that writes nothing into those tensors and still matches
     the eager step."""
     layers, batch = 2, 6
+    # Start from an empty stream cache (earlier tests may have grown it).
+    hip_kernels._workspaces.clear()
+    torch.cuda.empty_cache()
     cache_g, start, slot_lists, seq_tables, width, hq = setup(gpu, "pages", 16, layers, batch)
     cache_e, *_ = setup(gpu, "pages", 16, layers, batch)
     arenas = [(cache_g.keys[l], cache_g.values[l]) for l in range(layers)]
@@ -183,9 +186,10 @@ def test_graph_keeps_its_workspace_when_the_stream_cache_grows(gpu):
     before = hip_kernels.stream_workspace(gpu, 0)
     old_bytes, old_ptr = before.numel(), before.data_ptr()
     del before
-    # A 512-token prefill chunk over a 32256-token prefix: its key ranges
-    # need a workspace larger than the decode call's, so the stream's cached
-    # buffer is replaced (and the old one returned to the allocator).
+    # A 512-token prefill chunk over a 32256-token prefix in 8 key ranges:
+    # its partials (8 x 512 x 28 x 128 floats) need a workspace larger than
+    # the decode call's, so the stream's cached buffer is replaced (and the
+    # old one returned to the allocator).
     P, hkv, d, pos0, count = 16, 4, 128, 32256, 512
     pages = (pos0 + count) // P
     pk = torch.randn((pages, hkv, P, d), device=gpu, dtype=torch.float16)
@@ -194,7 +198,7 @@ def test_graph_keeps_its_workspace_when_the_stream_cache_grows(gpu):
                             device=gpu)
     pq = torch.randn((count, hq, d), device=gpu, dtype=torch.float16)
     hip_kernels.paged_prefill_attention(pq, pk, pv, table, start=pos0, page_size=P,
-                                        scale=d ** -0.5)
+                                        scale=d ** -0.5, splits=8)
     torch.cuda.synchronize()
     grown = hip_kernels.stream_workspace(gpu, 0)
     assert grown.numel() > old_bytes and grown.data_ptr() != old_ptr
