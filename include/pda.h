@@ -140,6 +140,32 @@ int pda_paged_decode_attention(const void* queries, const void* keys,
                                int32_t split_pages, int32_t flags, void* workspace,
                                size_t workspace_bytes, void* stream);
 
+/* pda_paged_decode_attention without a workspace argument: a call that
+ * allocates nothing. No counterpart in the reference (its op allocates its
+ * partials per call, metal_kernels.py:228-239); it is for callers that
+ * cannot allocate or hand over device memory on the call path: code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.
+ * The workspace is a static device array of 32 MiB per GPU inside the
+ * library (held until the process ends), laid out for this device's grid;
+ * a shape that needs more (about 2 x CUs x 8 waves x G x head_dim x 4
+ * bytes: head_dim 128 with G = 8, head_dim 256 with G = 4, head_dim 512
+ * with G = 2 fit on MI355X) returns PDA_ERR_WORKSPACE. Nothing in the
+ * scratch outlives a call, so it needs no clearing, but every call on one
+ * GPU shares it: calls that overlap on one GPU (several streams, several
+ * host threads) race and must be serialised by the caller. fp16 only;
+ * every other argument as for pda_paged_decode_attention. */
+int pda_paged_decode_attention_noalloc(const void* queries, const void* keys,
+                                       const void* values, const int32_t* tables,
+                                       const int32_t* lengths, void* out,
+                                       int32_t batch, int32_t q_heads,
+                                       int32_t kv_heads, int32_t head_dim,
+                                       int32_t page_size, int32_t table_stride,
+                                       int64_t arena_rows, int32_t layout,
+                                       int32_t longest, float scale,
+                                       int32_t window, float softcap,
+                                       int32_t split_pages, int32_t flags,
+                                       void* stream);
+
 /* The two passes of pda_paged_decode_attention, for callers that schedule or
  * time them separately; the reference's host wrapper launches the same two
  * kernels (metal_kernels.py:228-239 split, :240-247 merge). Call

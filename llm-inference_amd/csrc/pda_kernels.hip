@@ -284,10 +284,58 @@ int pda_plan(int32_t batch, int32_t q_heads, int32_t kv_heads,
 
 }  // extern "C"
 
+// Scratch of the no-allocation decode entry point
+// (pda_paged_decode_attention_noalloc): the workspace lives in this
+// file-scope device array, 32 MiB on every GPU the library runs on, held
+// until the process ends. Host code never passes `scratch` itself to a
+// kernel (on the host the name is a stand-in, not a device address); it
+// passes the address hipGetSymbolAddress returns for the current device.
+static __device__ __align__(256) unsigned char scratch[size_t(32) << 20];
+
 namespace {
 
+constexpr size_t kScratchBytes = sizeof(scratch);
 constexpr int kPassSplit = 1;
 constexpr int kPassMerge = 2;
+
+// Device address of `scratch` on the current device, looked up once per
+// device (with that device current) and kept.
+int scratch_address(void** ptr) {
+  static std::mutex mu;
+  static std::map<int, void*> addresses;
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess)
+    return fail(PDA_ERR_HIP, "hipGetDevice failed: %s", hipGetErrorString(err));
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = addresses.find(dev);
+  if (it == addresses.end()) {
+    void* address = nullptr;
+    err = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !address)
+      return fail(PDA_ERR_HIP, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                  hipGetErrorString(err));
+    it = addresses.emplace(dev, address).first;
+  }
+  *ptr = it->second;
+  return PDA_OK;
+}
+
+// Workspace offsets of a call: the page prefix at 0, then the meeting
+// points of `pairs` wave pairs, the (max, sum) pairs and the partial outputs
+// of `slots` slots of G heads x `dim` floats.
+struct WorkspaceLayout {
+  size_t off_meet = 0, off_ml = 0, off_o = 0, total = 0;
+};
+
+WorkspaceLayout workspace_layout(int batch, int G, int dim, int64_t pairs, int64_t slots) {
+  WorkspaceLayout w;
+  w.off_meet = align256((size_t)(batch + 1) * sizeof(int32_t));
+  w.off_ml = w.off_meet + align256((size_t)pairs * sizeof(int32_t));
+  w.off_o = w.off_ml + align256((size_t)slots * G * sizeof(float2));
+  w.total = w.off_o + align256((size_t)slots * G * dim * sizeof(float));
+  return w;
+}
 
 // Validates, plans and launches the split pass, the merge pass or both.
 // key_scales / value_scales non-null: 8-bit K/V (int8 arenas); bf16: q, K/V
@@ -298,7 +346,7 @@ int decode(int passes, const void* queries, const void* keys, const void* values
            int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t page_size,
            int32_t table_stride, int64_t arena_rows, int32_t layout, int32_t longest,
            float scale, int32_t window, float softcap, int32_t split_pages, int32_t flags,
-           void* workspace, size_t workspace_bytes, void* stream) {
+           void* workspace, size_t workspace_bytes, void* stream, bool use_scratch = false) {
   const bool q8 = key_scales || value_scales;
   Plan pl;
   int rc = make_plan(batch, q_heads, kv_heads, head_dim, page_size, table_stride,
@@ -329,17 +377,39 @@ int decode(int passes, const void* queries, const void* keys, const void* values
     return fail(PDA_ERR_ALIGNMENT, "fp16 scale buffers must be 2-byte aligned");
   if ((uintptr_t)tables & 3 || (uintptr_t)lengths & 3)
     return fail(PDA_ERR_ALIGNMENT, "int32 buffers must be 4-byte aligned");
-  if (!workspace || workspace_bytes < pl.total)
-    return fail(PDA_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given",
-                pl.total, workspace ? workspace_bytes : (size_t)0);
-  if ((uintptr_t)workspace & 255)
-    return fail(PDA_ERR_ALIGNMENT, "workspace must be 256-byte aligned");
+  if (!use_scratch) {
+    if (!workspace || workspace_bytes < pl.total)
+      return fail(PDA_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given",
+                  pl.total, workspace ? workspace_bytes : (size_t)0);
+    if ((uintptr_t)workspace & 255)
+      return fail(PDA_ERR_ALIGNMENT, "workspace must be 256-byte aligned");
+  }
 
   const KernelPair kp = kernels_for(head_dim, pl.G, q8, bf16);
   if (!kp.split) return fail(PDA_ERR_HEAD_DIM, "head_dim %d has no kernel", head_dim);
   const size_t lds = (size_t)(2 * batch + 1) * sizeof(int32_t);
   const int groups = resident_groups(kp.split, lds);
   if (groups < 0) return fail(PDA_ERR_HIP, "device query failed");
+
+  // Caller's workspace: the layout pda_workspace_bytes sizes (any grid).
+  // Scratch: the same layout packed for this device's grid and this call's
+  // head dim, within the scratch's fixed size.
+  WorkspaceLayout wl;
+  wl.off_meet = pl.off_meet;
+  wl.off_ml = pl.off_ml;
+  wl.off_o = pl.off_o;
+  wl.total = pl.total;
+  if (use_scratch) {
+    wl = workspace_layout(batch, pl.G, kernel_dim(head_dim, q8), (int64_t)groups * kPairs,
+                          (int64_t)groups * 2 * kSplitWaves);
+    if (wl.total > kScratchBytes)
+      return fail(PDA_ERR_WORKSPACE,
+                  "the no-allocation call needs %zu bytes of scratch for this shape, above "
+                  "its %zu-byte maximum; call pda_paged_decode_attention with a workspace",
+                  wl.total, kScratchBytes);
+    rc = scratch_address(&workspace);
+    if (rc) return rc;
+  }
 
   Params prm;
   prm.q = static_cast<const f16*>(queries);
@@ -350,9 +420,9 @@ int decode(int passes, const void* queries, const void* keys, const void* values
   prm.out = static_cast<f16*>(out);
   char* ws = static_cast<char*>(workspace);
   prm.prefix = reinterpret_cast<int32_t*>(ws);
-  prm.meet = reinterpret_cast<int32_t*>(ws + pl.off_meet);
-  prm.part_ml = reinterpret_cast<float2*>(ws + pl.off_ml);
-  prm.part_o = reinterpret_cast<float*>(ws + pl.off_o);
+  prm.meet = reinterpret_cast<int32_t*>(ws + wl.off_meet);
+  prm.part_ml = reinterpret_cast<float2*>(ws + wl.off_ml);
+  prm.part_o = reinterpret_cast<float*>(ws + wl.off_o);
   prm.arena_pages = arena_rows / page_size;
   prm.page_bytes = page_bytes;
   prm.kscale = static_cast<const f16*>(key_scales);
@@ -440,6 +510,18 @@ int pda_paged_decode_attention(PDA_DECODE_PARAMS) {
 }
 
 int pda_decode_split(PDA_DECODE_PARAMS) { return decode(kPassSplit, PDA_DECODE_ARGS(false)); }
+
+int pda_paged_decode_attention_noalloc(
+    const void* queries, const void* keys, const void* values, const int32_t* tables,
+    const int32_t* lengths, void* out, int32_t batch, int32_t q_heads, int32_t kv_heads,
+    int32_t head_dim, int32_t page_size, int32_t table_stride, int64_t arena_rows,
+    int32_t layout, int32_t longest, float scale, int32_t window, float softcap,
+    int32_t split_pages, int32_t flags, void* stream) {
+  return decode(kPassSplit | kPassMerge, queries, keys, values, nullptr, nullptr, false, tables,
+                lengths, out, batch, q_heads, kv_heads, head_dim, page_size, table_stride,
+                arena_rows, layout, longest, scale, window, softcap, split_pages, flags,
+                nullptr, 0, stream, true);
+}
 
 int pda_decode_merge(PDA_DECODE_PARAMS) { return decode(kPassMerge, PDA_DECODE_ARGS(false)); }
 

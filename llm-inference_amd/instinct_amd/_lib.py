@@ -52,6 +52,10 @@ _DECODE_ARGS = ([c_void_p] * 6 + [c_int32] * 6
 for _name in ("pda_paged_decode_attention", "pda_decode_split", "pda_decode_merge"):
     SIGNATURES[_name] = (ctypes.c_int, _DECODE_ARGS)
     SIGNATURES[_name + "_bf16"] = (ctypes.c_int, _DECODE_ARGS)
+# No workspace: the library's static device scratch (the same arguments
+# without the workspace pointer and size).
+SIGNATURES["pda_paged_decode_attention_noalloc"] = (
+    ctypes.c_int, _DECODE_ARGS[:-3] + [c_void_p])
 # 8-bit K/V: key and value scale arenas after the values.
 _DECODE_ARGS_Q8 = _DECODE_ARGS[:3] + [c_void_p, c_void_p] + _DECODE_ARGS[3:]
 for _name in ("pda_paged_decode_attention_q8", "pda_decode_split_q8", "pda_decode_merge_q8"):
