@@ -54,6 +54,10 @@ def parse():
                     help="config 3: sequences (1, 2 or 4; default 1)")
     ap.add_argument("--context", type=int, default=0,
                     help="config 3: tokens per sequence (32768 or 131072; default 32768)")
+    ap.add_argument("--group", type=int, default=0,
+                    help="query heads per kv head (0 = the config's): the config's lengths, "
+                         "tables and K/V with a larger or smaller GQA group, for the "
+                         "matrix-core vs VALU study at G >= 8")
     ap.add_argument("--split-pages", type=int, default=0)
     ap.add_argument("--deterministic", action="store_true",
                     help="fixed split points (PDA_DECODE_FIXED_SPLIT): bitwise reproducible")
@@ -441,6 +445,12 @@ def main():
         print("bench.py: --batch/--context choose among config 3's points", file=sys.stderr)
         sys.exit(2)
     w = workloads.CONFIGS[args.config](device=device, **cfg_kw).to_layout(args.layout)
+    if args.group:
+        # Same lengths, tables and K/V; G query heads per kv head.
+        gen = torch.Generator(device=device).manual_seed(100 + args.group)
+        w.q = torch.randn((w.batch, args.group * w.kv_heads, w.head_dim), generator=gen,
+                          device=device).to(w.q.dtype)
+        w.name += f"-g{args.group}"
     if bf16:
         # The same seeded values rounded to bf16: a bf16 model's cache.
         w.q, w.keys, w.values = w.q.bfloat16(), w.keys.bfloat16(), w.values.bfloat16()
@@ -525,6 +535,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": ("bf16" if bf16 else "f16") if args.kv_bits == 16 else "i8 K/V, f16 math",
+        "matrix_cores": names["matrix_cores"],
         "data": "synthetic (seeded N(0,1) K/V/Q, random page permutation)",
         "config": {
             "workload": w.name,

@@ -29,6 +29,10 @@ typedef __bf16 bf16;
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 constexpr float kLog2e = 1.44269504088896340736f;
 // Lazy rescale threshold (log2 units): probabilities stay below 2^8.
@@ -73,7 +77,8 @@ struct Params {
   int32_t hkv;
   int32_t head_dim;   // elements per row (the template's D except for generic kernels)
   int32_t gtot;       // query heads per kv head
-  int32_t nhg;        // head groups per kv head (gtot / G)
+  int32_t nhg;        // head groups per kv head (gtot / unit_heads)
+  int32_t unit_heads; // query heads of one unit (G, or fewer for matrix-core kernels)
   int32_t window;
   int32_t grid_pairs; // wave pairs of the split kernel's grid
   int32_t min_pages;  // fewest pages per wave before the stream uses fewer pairs
@@ -106,25 +111,31 @@ constexpr int next_pow2(int x) {
 // 2-byte loads at 8 bits, since rows of an odd number of pairs are not
 // 16-byte aligned); pairs at or past the real head dim are not loaded and
 // read as zero. p.v runs on FMAs.
-template <int D, bool Q8 = false, bool GEN = false>
+//
+// Matrix-core kernels (MF, a GQA group of 8 or more query heads): a step is
+// 16 keys; lane l loads key l % 16, elements [32 c + 8 (l / 16), + 8) of
+// each 32-element chunk c (NV = D / 32 chunks, one 16-byte load each for K
+// and for V), the A operand of v_mfma_f32_16x16x32 as it lands.
+template <int D, bool Q8 = false, bool GEN = false, bool MF = false>
 struct Geom {
   static constexpr int EPL =
-      GEN ? 8 : Q8 ? 16 : ((D >= 80 && D % 16 == 0) ? 16 : 8);  // per lane
-  static constexpr int NV = (Q8 || GEN) ? 1 : EPL / 8;            // 16-byte K loads
+      MF ? D / 4 : GEN ? 8 : Q8 ? 16 : ((D >= 80 && D % 16 == 0) ? 16 : 8);  // per lane
+  static constexpr int NV = MF ? D / 32 : (Q8 || GEN) ? 1 : EPL / 8;      // 16-byte K loads
   static constexpr int DC = D / NV;                               // chunk stride
   static constexpr int SLICES = D / EPL;
-  static constexpr int R = next_pow2(SLICES);                     // lanes per key
+  static constexpr int R = MF ? 4 : next_pow2(SLICES);            // lanes per key
   static constexpr int KPS = 64 / R;                              // keys per step
   // p.v on v_dot2 over key pairs (head dims with 2R lanes x 8 elements):
   // lane (kp, r2), kp = lane / 2R, r2 = lane % 2R, holds elements
   // [r2 * 8, r2 * 8 + 8) of the step's keys 2 kp and 2 kp + 1.
-  static constexpr bool PV2 = !GEN && EPL == 16 && D == 2 * R * 8;
+  static constexpr bool PV2 = !GEN && !MF && EPL == 16 && D == 2 * R * 8;
   static constexpr int OPL = PV2 ? 8 : EPL;                       // outputs per lane
   static constexpr int NPAIR = KPS / 2;                           // key pairs per step
   // Vector memory loads per step: K and V (fp16); K, the two V pieces and the
   // key scale and the pair's two value scales (8-bit); generic: four pieces
   // of K and of V, plus the key's two scales at 8 bits.
-  static constexpr int LOADS = GEN ? (Q8 ? 10 : 8) : Q8 ? 6 : 2 * NV;
+  static constexpr int LOADS = MF ? 2 * NV : GEN ? (Q8 ? 10 : 8) : Q8 ? 6 : 2 * NV;
+  static_assert(!MF || (D % 32 == 0 && !Q8 && !GEN), "matrix-core kernels: 16-bit, D % 32 == 0");
   static_assert(D % EPL == 0 && DC % 8 == 0, "head_dim must be a multiple of 8");
   static_assert(GEN || !Q8 || PV2, "8-bit K/V needs the key-pair p.v layout");
   static_assert(!GEN || (D >= 8 && D <= 512 && (D & (D - 1)) == 0),
@@ -246,6 +257,38 @@ __device__ __forceinline__ f16x8 zero_unless(f16x8 x, bool keep) {
 // Int8 bytes to fp16 pairs, exactly (pda_internal.h).
 using pda_internal::bytes_to_f16x2;
 
+// Matrix-core helpers. LDS row of a V tile (16-bit elements): the head dim
+// plus padding that puts the four rows one transposed read touches on
+// different banks.
+constexpr int mf_vrow(int d) { return d % 64 == 32 ? d + 64 : d + 32; }
+
+// S^T += K Q^T over 32 elements: A = 16 keys x 32, B = 32 x 16 heads.
+template <bool BF>
+__device__ __forceinline__ f32x4 mfma_k32(const f16x8& a, const f16x8& b, const f32x4& c) {
+  if constexpr (BF)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// O^T += V^T P^T over 16 keys: A = 16 elements x 16 keys, B = 16 keys x 16 heads.
+template <bool BF>
+__device__ __forceinline__ f32x4 mfma_k16(const f16x4& a, const f16x4& b, const f32x4& c) {
+  if constexpr (BF)
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, a),
+                                                     __builtin_bit_cast(i16x4, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+
+// gfx950 transposing LDS read: in each group of 16 lanes, lane s names four
+// 16-bit elements (row s / 4, columns 4 (s % 4) ..) of a 4 x 16 block and
+// receives column s of it, rows 0..3.
+__device__ __forceinline__ f16x4 read_tr(const f16* at) {
+  return __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)at));
+}
+
 struct SeqGeometry {
   int len, first, first_page, npages;
 };
@@ -323,16 +366,26 @@ __device__ void build_prefix(const Params& p, int* s_prefix, int* s_len) {
 // 16-bit buffers are addressed as fp16 storage and reinterpreted: q.k and
 // p.v run on bf16 v_dot2, the probabilities are rounded to bf16 for p.v.
 // GEN: generic kernel for a head dim p.head_dim below the padded D (Geom).
-template <int D, int G, bool Q8, bool BF, bool GEN>
+// MF: matrix-core kernel for a GQA group of 8 to 16 query heads per unit
+// (G = 16 slots, p.unit_heads real heads; see mf_step).
+template <int D, int G, bool Q8, bool BF, bool GEN, bool MF>
 __global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void paged_decode_kernel(const Params p) {
   static_assert(!(Q8 && BF), "8-bit K/V is dequantized to fp16");
-  using Gm = Geom<D, Q8, GEN>;
+  static_assert(!MF || G == 16, "matrix-core kernels lay 16 head slots out");
+  using Gm = Geom<D, Q8, GEN, MF>;
   constexpr int EPL = Gm::EPL, NV = Gm::NV, DC = Gm::DC, R = Gm::R, KPS = Gm::KPS;
   constexpr bool PV2 = Gm::PV2;
   constexpr int OPL = Gm::OPL;
+  // Steps in flight per wave: two, or one where a step alone is 16 KiB of
+  // K and V per wave (matrix-core kernels at D = 256), which also keeps
+  // those kernels within 256 registers.
+  constexpr int NBUF = (MF && D >= 256) ? 1 : kNbuf;
   extern __shared__ int s_dyn[];
   __shared__ int s_ticket[kPairs];
+  // Matrix-core kernels: each wave's V tile of one step, [16 keys][kVRow].
+  constexpr int kVRow = mf_vrow(D);
+  __shared__ __align__(16) f16 s_vt[MF ? kSplitWaves * 16 * kVRow : 1];
   const int B = p.batch;
   int* const s_prefix = s_dyn;         // [B + 1]
   int* const s_len = s_dyn + B + 1;    // [B]
@@ -347,6 +400,10 @@ void paged_decode_kernel(const Params p) {
   const int r2 = lane % (2 * R);      // p.v layout: element group and key pair
   const int kp = lane / (2 * R);
   const bool hi = kk & 1;             // this lane's key is the second of its pair
+  // Key this lane loads within a step (matrix-core kernels: key lane % 16;
+  // its 16-lane group lane / 16 picks the elements) and the head it scores.
+  const int lk = MF ? (lane & 15) : kk;
+  const int mg = lane >> 4;
   // v_perm selectors that pair V elements as (this lane's key, the other),
   // the order of the probability pair below: bytes 0-3 of the source pair
   // are the second key's dword, 4-7 the first key's.
@@ -444,14 +501,26 @@ void paged_decode_kernel(const Params p) {
     const int first = p.window > 0 ? max(0, len - p.window) : 0;
     const int first_page = first / P;
     const int kvh = kvg / p.nhg;
-    const int h0 = kvh * p.gtot + (kvg - kvh * p.nhg) * G;
+    const int hpu = MF ? p.unit_heads : G;  // query heads of the unit
+    const int h0 = kvh * p.gtot + (kvg - kvh * p.nhg) * hpu;
     const int32_t* const table = p.tables + (int64_t)b * p.table_stride + first_page;
 
     // Queries of the G heads, this lane's slice, as fp16 pairs for v_dot2
     // (bf16: the same bits, read as bf16 pairs where used).
-    f16x2 q[G][EPL / 2];
+    f16x2 q[MF ? 1 : G][MF ? 1 : EPL / 2];
+    // Matrix-core kernels: Q^T as the B operand of S^T = K Q^T, head
+    // lane % 16 (zero past the unit's heads), the elements this lane's K
+    // loads hold.
+    f16x8 qb[MF ? NV : 1];
+    if constexpr (MF) {
+      const bool real = (lane & 15) < hpu;
+      const f16* qp = p.q + ((int64_t)b * p.hq + h0 + (real ? (lane & 15) : 0)) * D + 8 * mg;
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
+      for (int c = 0; c < NV; ++c)
+        qb[c] = zero_unless(*reinterpret_cast<const f16x8*>(qp + 32 * c), real);
+    }
+#pragma unroll
+    for (int g = 0; g < (MF ? 0 : G); ++g) {
       if constexpr (GEN) {
         // Element pairs d0 + 2i below the real head dim; the rest stay zero,
         // so whatever the K loads of those pairs hold adds nothing.
@@ -481,24 +550,31 @@ void paged_decode_kernel(const Params p) {
       }
     }
 
-    float o[G][OPL];
-    float l[G];
-    float m[G];
+    // Matrix-core kernels keep one (max, sum) per lane, for head lane % 16,
+    // and O^T in accumulators ob (see mf_step); the others per head.
+    constexpr int kHeads = MF ? 1 : G;
+    float o[kHeads][MF ? 1 : OPL];
+    float l[kHeads];
+    float m[kHeads];
+    f32x4 ob[MF ? D / 16 : 1];
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
+    for (int g = 0; g < kHeads; ++g) {
       l[g] = 0.0f;
       m[g] = -INFINITY;
 #pragma unroll
-      for (int i = 0; i < OPL; ++i) o[g][i] = 0.0f;
+      for (int i = 0; i < (MF ? 1 : OPL); ++i) o[g][i] = 0.0f;
     }
+#pragma unroll
+    for (int i = 0; i < (MF ? D / 16 : 1); ++i) ob[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
     // Addressing: a wave-uniform byte offset per step (page and first key of
     // the step) plus 32-bit per-lane offsets: K by (key, kv head, chunk), V
     // by (key pair, kv head, element group) on the p.v path, else as K.
     const uint32_t lane_off =
-        GEN  ? (uint32_t)(kk * p.row_bytes + kvh * p.head_bytes)
-        : Q8 ? (uint32_t)(kk * p.row_bytes + kvh * p.head_bytes + r * 16)
-             : (uint32_t)(kk * p.row_bytes + kvh * p.head_bytes + d0 * 2);
+        MF    ? (uint32_t)(lk * p.row_bytes + kvh * p.head_bytes + 16 * mg)
+        : GEN ? (uint32_t)(kk * p.row_bytes + kvh * p.head_bytes)
+        : Q8  ? (uint32_t)(kk * p.row_bytes + kvh * p.head_bytes + r * 16)
+              : (uint32_t)(kk * p.row_bytes + kvh * p.head_bytes + d0 * 2);
     const uint32_t v_off =
         GEN   ? lane_off
         : Q8  ? (uint32_t)(2 * kp * p.row_bytes + kvh * p.head_bytes + r2 * 8)
@@ -541,10 +617,10 @@ void paged_decode_kernel(const Params p) {
     int cnt = 0;  // pages of this unit taken by this wave
     // Per ring slot: is it a real step, its first key position, page usable,
     // keys of the page from its first key on (KPS unless the page is ragged).
-    bool s_real[kNbuf];
-    int s_t0[kNbuf];
-    bool s_ok[kNbuf];
-    int s_kin[kNbuf];
+    bool s_real[NBUF];
+    int s_t0[NBUF];
+    bool s_ok[NBUF];
+    int s_kin[NBUF];
     int64_t last_off = 0;
     int64_t last_soff = 0;  // 8-bit: scale element of the step's first key
     // Ragged pages: rows this lane's loads move back so that the last,
@@ -552,11 +628,11 @@ void paged_decode_kernel(const Params p) {
     // its value pair); the keys they duplicate are masked.
     int last_dk = 0, last_dv0 = 0, last_dv1 = 0;
 
-    f16x8 kb[kNbuf][NV], vb[kNbuf][NV];
+    f16x8 kb[NBUF][NV], vb[NBUF][NV];
     // 8-bit: this lane's key scale and the value scales of its pair's keys
     // (own, other), kept apart until the step is computed so that no
     // instruction waits on them at load time.
-    f16 ksb[kNbuf], vs_own_b[kNbuf], vs_other_b[kNbuf];
+    f16 ksb[NBUF], vs_own_b[NBUF], vs_other_b[NBUF];
 
     auto load_step = [&](int u) {
       if (loading && start_page) {
@@ -594,7 +670,7 @@ void paged_decode_kernel(const Params p) {
         if (p.ragged) {
           const int kin = min(KPS, P - lsub * KPS);
           s_kin[u] = kin;
-          last_dk = min(kk, kin - 1) - kk;
+          last_dk = min(lk, kin - 1) - lk;
           last_dv0 = min(2 * kp, kin - 1) - 2 * kp;
           last_dv1 = min(2 * kp + 1, kin - 1) - (2 * kp + 1);
         }
@@ -667,6 +743,85 @@ void paged_decode_kernel(const Params p) {
       const int t0 = s_t0[u];
       f16x8(&kd)[NV] = kb[u];
       f16x8(&vd)[NV] = vb[u];
+      if constexpr (MF) {
+        // S^T = K Q^T over the step's 16 keys on the matrix cores: this
+        // lane holds keys 4 mg .. 4 mg + 3 of head lane % 16.
+        f32x4 sacc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int c = 0; c < NV; ++c) sacc = mfma_k32<BF>(kd[c], qb[c], sacc);
+        const int lim = min(len, t0 + s_kin[u]);
+        float sr[4], x[4];  // scores in log2 units, and minus the running max
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (p.softcap > 0.0f) {
+            const float ex = __builtin_amdgcn_exp2f(sacc[e] * p.cap_in);
+            sr[e] = (1.0f - 2.0f * __builtin_amdgcn_rcpf(ex + 1.0f)) * p.cap_out;
+          } else {
+            sr[e] = sacc[e] * p.scale_log2;
+          }
+          x[e] = sr[e] - m[0];
+        }
+        if (!(t0 >= first && t0 + 16 <= lim)) {
+          // Boundary step: scores of keys outside [first, lim) are masked,
+          // and the V row this lane loaded is zeroed if its key is.
+          bool any = false;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int t = t0 + 4 * mg + e;
+            const bool ok = t >= first && t < lim;
+            sr[e] = ok ? sr[e] : -INFINITY;
+            x[e] = ok ? x[e] : -INFINITY;
+            any |= ok;
+          }
+          if (!__any(any)) return;
+          const bool vok = t0 + lk >= first && t0 + lk < lim;
+#pragma unroll
+          for (int c = 0; c < NV; ++c) vd[c] = zero_unless(vd[c], vok);
+        }
+        if (__any(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])) > kSlack)) {
+          // Rare: raise each head's running max to its largest score of
+          // the step (every head sees the step's visible keys, so the max
+          // is finite) and rescale its sum and outputs.
+          float hm = fmaxf(fmaxf(sr[0], sr[1]), fmaxf(sr[2], sr[3]));
+          hm = fmaxf(hm, __shfl_xor(hm, 16));
+          hm = fmaxf(hm, __shfl_xor(hm, 32));
+          const float mn = fmaxf(m[0], hm);
+          const float f = __builtin_amdgcn_exp2f(m[0] - mn);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) x[e] = sr[e] - mn;
+          m[0] = mn;
+          l[0] *= f;
+#pragma unroll
+          for (int i = 0; i < D / 16; ++i) ob[i] *= f;
+        }
+        // P^T, the B operand of O^T += V^T P^T as the accumulator holds it;
+        // the sum uses the same rounded probabilities.
+        f16x4 pb;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float pr = __builtin_amdgcn_exp2f(x[e]);
+          if constexpr (BF) {
+            const bf16 r16 = (bf16)pr;
+            pb[e] = __builtin_bit_cast(f16, r16);
+            l[0] += (float)r16;
+          } else {
+            pb[e] = (f16)pr;
+            l[0] += (float)pb[e];
+          }
+        }
+        // V^T through this wave's LDS tile: the row pieces as loaded, then
+        // a transposed read gives lane l element 16 i + l % 16 of keys
+        // 4 mg .. 4 mg + 3 (in-order LDS: the next step's stores follow
+        // these reads).
+        f16* const vt = s_vt + w * 16 * kVRow;
+#pragma unroll
+        for (int c = 0; c < NV; ++c)
+          *reinterpret_cast<f16x8*>(vt + lk * kVRow + 32 * c + 8 * mg) = vd[c];
+        const f16* const vr = vt + (4 * mg + ((lane & 15) >> 2)) * kVRow + 4 * (lane & 3);
+#pragma unroll
+        for (int i = 0; i < D / 16; ++i) ob[i] = mfma_k16<BF>(read_tr(vr + 16 * i), pb, ob[i]);
+        return;
+      } else {
       // q.k for every head of the group: v_dot2 over this lane's slice,
       // then the butterfly over the R lanes of the key.
       // This lane's key elements as fp16 pairs (8-bit: converted exactly).
@@ -879,24 +1034,62 @@ void paged_decode_kernel(const Params p) {
           }
         }
       }
+      }  // not MF
     };
 
 #pragma unroll
-    for (int u = 0; u < kNbuf; ++u) load_step(u);
+    for (int u = 0; u < NBUF; ++u) load_step(u);
     // The ring: every slot is waited for (its loads are complete once only
     // the other slots' remain), computed if it holds a real step and
     // reloaded, in issue order on every path, with the loop test at the
     // bottom; the compiler's wait counts then stay those of a steady ring.
     do {
 #pragma unroll
-      for (int u = 0; u < kNbuf; ++u) {
-        wait_vmem<(kNbuf - 1) * Gm::LOADS>();
+      for (int u = 0; u < NBUF; ++u) {
+        wait_vmem<(NBUF - 1) * Gm::LOADS>();
         if (s_real[u]) compute_step(u);
         load_step(u);
       }
     } while (s_real[0]);
     // `pending` now tells whether the page after this unit is ours too.
 
+    if constexpr (MF) {
+      // Matrix-core kernels: O^T is complete in the accumulators (lane l
+      // holds elements 16 i + 4 mg .. + 3 of head l % 16); the sum of each
+      // head is spread over its four lanes l % 16 + 16 j.
+      float lt = l[0];
+      lt += __shfl_xor(lt, 16);
+      lt += __shfl_xor(lt, 32);
+      const int head = lane & 15;
+      if (cnt == npg) {
+        if (head < hpu) {  // the whole unit: normalise and write
+          const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+          f16* const dst = p.out + ((int64_t)b * p.hq + h0 + head) * D + 4 * mg;
+#pragma unroll
+          for (int i = 0; i < D / 16; ++i) {
+            f16x4 y;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              if constexpr (BF)
+                y[e] = __builtin_bit_cast(f16, (bf16)(ob[i][e] * inv));
+              else
+                y[e] = (f16)(ob[i][e] * inv);
+            }
+            *reinterpret_cast<f16x4*>(dst + 16 * i) = y;
+          }
+        }
+      } else if (head < hpu) {
+        // Cut unit: the unnormalised partial, slot chosen as below.
+        const bool holds_start = back ? !pending : first_unit;
+        const int64_t slot = 2 * vw + (holds_start ? 0 : 1);
+        float* const dst = p.part_o + (slot * G + head) * D + 4 * mg;
+#pragma unroll
+        for (int i = 0; i < D / 16; ++i)
+          *reinterpret_cast<float4*>(dst + 16 * i) =
+              make_float4(ob[i][0], ob[i][1], ob[i][2], ob[i][3]);
+        if (mg == 0) p.part_ml[slot * G + head] = make_float2(m[0], lt);
+      }
+    } else {
     // Fold the wave's key subsets (metal_kernels.py:63-81); every lane then
     // holds the totals of its elements. On the p.v pair path the lanes of
     // key pair kp write the heads g with g % NPAIR == kp, elements r2 * 8 ..;
@@ -972,6 +1165,7 @@ void paged_decode_kernel(const Params p) {
         if ((PV2 ? r2 : r) == 0) p.part_ml[slot * G + g] = make_float2(m[g], l[g]);
       }
     }
+    }  // not MF
     first_unit = false;
     if (!pending) break;
 
@@ -1027,11 +1221,12 @@ __global__ __launch_bounds__(kMergeMaxWaves * 64) void paged_decode_merge_kernel
   const int lane = tid & 63;
   const int w = uniform(tid >> 6);
   const int mw = blockDim.x >> 6;
-  const int kvg = blockIdx.x / G;
-  const int g = blockIdx.x - kvg * G;
+  const int uh = p.unit_heads;  // query heads of a unit (G slots, fewer used by MF)
+  const int kvg = blockIdx.x / uh;
+  const int g = blockIdx.x - kvg * uh;
   const int b = blockIdx.y;
   const int kvh = kvg / p.nhg;
-  const int h = kvh * p.gtot + (kvg - kvh * p.nhg) * G + g;
+  const int h = kvh * p.gtot + (kvg - kvh * p.nhg) * uh + g;
   const int hd = GEN ? p.head_dim : D;  // output row length (partials are D apart)
   f16* const dst = p.out + ((int64_t)b * p.hq + h) * hd;
   const int nkvg = p.hkv * p.nhg;
@@ -1142,9 +1337,9 @@ struct KernelPair {
   KernelFn merge = nullptr;
 };
 
-template <int D, int G, bool Q8, bool BF, bool GEN = false>
+template <int D, int G, bool Q8, bool BF, bool GEN = false, bool MF = false>
 KernelPair make_pair() {
-  return {paged_decode_kernel<D, G, Q8, BF, GEN>, paged_decode_merge_kernel<D, G, BF, GEN>};
+  return {paged_decode_kernel<D, G, Q8, BF, GEN, MF>, paged_decode_merge_kernel<D, G, BF, GEN>};
 }
 
 template <int D, bool Q8, bool BF, bool GEN = false>
@@ -1172,6 +1367,9 @@ KernelPair kernels_q8(int d, int g);
 KernelPair kernels_gen_f16(int dp, int g);
 KernelPair kernels_gen_bf16(int dp, int g);
 KernelPair kernels_gen_q8(int dp, int g);
+// Matrix-core kernels (8 to 16 query heads per unit): head dims 64, 96,
+// 128, 256 in fp16 and bf16.
+KernelPair kernels_mf(int d, bool bf16);
 
 }  // namespace pda_decode
 

@@ -53,6 +53,7 @@
 #include <map>
 #include <mutex>
 #include <stdarg.h>
+#include <stdlib.h>
 #include <stddef.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -145,16 +146,44 @@ int keys_per_step(int d, bool q8) {
   return 0;
 }
 
-// Heads per workgroup: the whole GQA group when it has at most 8 heads,
-// otherwise the largest divisor of it that does.
+// Heads per unit on the VALU kernels: the whole GQA group when it has at
+// most 8 heads, otherwise the largest divisor of it that does.
 int heads_per_group(int gtot) {
   for (int g = gtot < 8 ? gtot : 8; g >= 1; --g)
     if (gtot % g == 0) return g;
   return 1;
 }
 
+// Matrix-core kernels: 16-bit K/V, head dims whose rows split into 32-element
+// chunks, and GQA groups of at least mf_min_group() heads (8; the
+// PDA_MFMA_MIN_GROUP environment variable moves it, for measurements).
+bool mf_dim(int d) { return d == 64 || d == 96 || d == 128 || d == 256; }
+
+int mf_min_group() {
+  static const int value = [] {
+    const char* env = getenv("PDA_MFMA_MIN_GROUP");
+    const int v = env ? atoi(env) : 0;
+    return v > 0 ? v : 8;
+  }();
+  return value;
+}
+
+bool use_mf(int gtot, int d, bool q8) { return !q8 && mf_dim(d) && gtot >= mf_min_group(); }
+
+// Heads per unit on the matrix cores: the whole group when it has at most 16
+// heads (one K/V read serves them all), else the largest divisor that does.
+int mf_unit_heads(int gtot) {
+  for (int g = gtot < 16 ? gtot : 16; g >= 1; --g)
+    if (gtot % g == 0) return g;
+  return 1;
+}
+
 struct Plan {
-  int G = 0, nhg = 0, min_pages = 0;
+  int G = 0;           // partial slots per unit (the kernels' head slots)
+  int unit_heads = 0;  // query heads of a unit
+  int nhg = 0;         // units per kv head
+  bool mf = false;     // matrix-core kernels
+  int min_pages = 0;
   int64_t pages_est = 0;       // visible pages of the batch if every length = longest
   int64_t unit_pages_max = 0;  // visible pages of one unit, at most
   size_t off_meet = 0, off_ml = 0, off_o = 0, total = 0;
@@ -165,7 +194,7 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 int make_plan(int32_t batch, int32_t q_heads, int32_t kv_heads, int32_t head_dim,
               int32_t page_size, int32_t table_stride, int32_t longest,
-              int32_t window, int32_t split_pages, Plan* out) {
+              int32_t window, int32_t split_pages, Plan* out, bool q8 = false) {
   if (batch < 0 || q_heads <= 0 || kv_heads <= 0 || head_dim <= 0 ||
       page_size <= 0 || table_stride <= 0 || window < 0 || split_pages < 0)
     return fail(PDA_ERR_INVALID_ARGUMENT,
@@ -183,8 +212,13 @@ int make_plan(int32_t batch, int32_t q_heads, int32_t kv_heads, int32_t head_dim
     return fail(PDA_ERR_INVALID_ARGUMENT, "batch %d above %d", batch, kMaxBatch);
   Plan pl;
   const int gtot = q_heads / kv_heads;
-  pl.G = heads_per_group(gtot);
-  pl.nhg = gtot / pl.G;
+  pl.mf = use_mf(gtot, head_dim, q8);
+  pl.unit_heads = pl.mf ? mf_unit_heads(gtot) : heads_per_group(gtot);
+  pl.G = pl.mf ? 16 : pl.unit_heads;
+  pl.nhg = gtot / pl.unit_heads;
+  // The workspace holds the widest slot layout either cache type could use
+  // for this shape (pda_workspace_bytes does not know the element type).
+  const int g_ws = use_mf(gtot, head_dim, false) ? 16 : heads_per_group(gtot);
   if ((int64_t)kv_heads * pl.nhg > 65535)
     return fail(PDA_ERR_INVALID_ARGUMENT, "kv heads x head groups above 65535");
   // Visible pages of one sequence are bounded by the table width and, with a
@@ -204,8 +238,8 @@ int make_plan(int32_t batch, int32_t q_heads, int32_t kv_heads, int32_t head_dim
   // of any shape share one workspace without initialisation.
   pl.off_meet = align256((size_t)(batch + 1) * sizeof(int32_t));
   pl.off_ml = pl.off_meet + align256((size_t)kMaxPairs * sizeof(int32_t));
-  pl.off_o = pl.off_ml + align256((size_t)kSlots * pl.G * sizeof(float2));
-  pl.total = pl.off_o + align256((size_t)kSlots * pl.G * workspace_dim(head_dim) * sizeof(float));
+  pl.off_o = pl.off_ml + align256((size_t)kSlots * g_ws * sizeof(float2));
+  pl.total = pl.off_o + align256((size_t)kSlots * g_ws * workspace_dim(head_dim) * sizeof(float));
   *out = pl;
   return PDA_OK;
 }
@@ -350,7 +384,7 @@ int decode(int passes, const void* queries, const void* keys, const void* values
   const bool q8 = key_scales || value_scales;
   Plan pl;
   int rc = make_plan(batch, q_heads, kv_heads, head_dim, page_size, table_stride,
-                     longest, window, split_pages, &pl);
+                     longest, window, split_pages, &pl, q8);
   if (rc) return rc;
   if (batch == 0) return ok();
   if (!queries || !keys || !values || !tables || !lengths || !out ||
@@ -385,7 +419,7 @@ int decode(int passes, const void* queries, const void* keys, const void* values
       return fail(PDA_ERR_ALIGNMENT, "workspace must be 256-byte aligned");
   }
 
-  const KernelPair kp = kernels_for(head_dim, pl.G, q8, bf16);
+  const KernelPair kp = pl.mf ? kernels_mf(head_dim, bf16) : kernels_for(head_dim, pl.G, q8, bf16);
   if (!kp.split) return fail(PDA_ERR_HEAD_DIM, "head_dim %d has no kernel", head_dim);
   const size_t lds = (size_t)(2 * batch + 1) * sizeof(int32_t);
   const int groups = resident_groups(kp.split, lds);
@@ -447,11 +481,12 @@ int decode(int passes, const void* queries, const void* keys, const void* values
   prm.head_dim = head_dim;
   prm.gtot = q_heads / kv_heads;
   prm.nhg = pl.nhg;
+  prm.unit_heads = pl.unit_heads;
   prm.window = window;
   prm.grid_pairs = groups * kPairs;
   prm.min_pages = pl.min_pages;
   prm.fixed = (flags & PDA_DECODE_FIXED_SPLIT) ? 1 : 0;
-  prm.ragged = page_size % keys_per_step(head_dim, q8) ? 1 : 0;
+  prm.ragged = page_size % (pl.mf ? 16 : keys_per_step(head_dim, q8)) ? 1 : 0;
   prm.scale_log2 = scale * kLog2e;
   prm.softcap = softcap;
   prm.cap_in = softcap > 0.0f ? 2.0f * kLog2e * scale / softcap : 0.0f;
@@ -466,7 +501,8 @@ int decode(int passes, const void* queries, const void* keys, const void* values
   if (err == hipSuccess && (passes & kPassMerge)) {
     const int mw = merge_waves(pl, head_dim, prm.grid_pairs);
     err = hipLaunchKernel(reinterpret_cast<const void*>(kp.merge),
-                          dim3(kv_heads * pl.nhg * pl.G, batch), dim3(64 * mw), args, 0, st);
+                          dim3(kv_heads * pl.nhg * pl.unit_heads, batch), dim3(64 * mw), args, 0,
+                          st);
   }
   if (err != hipSuccess)
     return fail(PDA_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(err));

@@ -27,6 +27,7 @@ the split workspace, and passes device pointers and the current stream.
 from __future__ import annotations
 
 import ctypes
+import os
 from typing import Any
 
 import numpy as np
@@ -74,24 +75,31 @@ def _given_workspace(ws: torch.Tensor, device: torch.device, nbytes: int) -> tor
 
 
 _FAST_DIMS = {16: (64, 80, 96, 128, 256, 512), 8: (64, 128, 256, 512)}
+_MF_DIMS = (64, 96, 128, 256)  # matrix-core kernels (16-bit K/V, 8+ heads per kv head)
 
 
 def decode_kernel_names(q_heads: int, kv_heads: int, head_dim: int, *, bits: int = 16,
                         bf16: bool = False) -> dict[str, Any]:
     """The kernels a decode call of this shape launches, as the library's
-    dispatch picks them (csrc/pda_kernels.hip ``kernels_for`` and
-    ``heads_per_group``): template arguments ``<D, G, Q8, BF, GEN>`` of the
-    split and merge kernels, the query heads one unit serves (G) and the
-    head groups per kv head (each re-reads the kv head's K/V)."""
+    dispatch picks them (csrc/pda_kernels.hip ``make_plan``, ``kernels_for``,
+    ``heads_per_group``, ``use_mf``): template arguments ``<D, G, Q8, BF,
+    GEN, MF>`` of the split and merge kernels, whether the matrix cores run
+    it, the query heads one unit serves and the units per kv head (each
+    reads the kv head's K/V once)."""
     group = q_heads // kv_heads
-    heads = next(g for g in range(min(group, 8), 0, -1) if group % g == 0)
+    min_mf = int(os.environ.get("PDA_MFMA_MIN_GROUP", "0") or 0) or 8
+    mf = bits == 16 and head_dim in _MF_DIMS and group >= min_mf
+    cap = 16 if mf else 8
+    heads = next(g for g in range(min(group, cap), 0, -1) if group % g == 0)
     generic = head_dim not in _FAST_DIMS[bits]
     dim = max(8, 1 << (head_dim - 1).bit_length()) if generic else head_dim
+    slots = 16 if mf else heads
     b = lambda x: str(bool(x)).lower()  # noqa: E731
-    targs = f"{dim},{heads},{b(bits == 8)},{b(bf16)},{b(generic)}"
+    targs = f"{dim},{slots},{b(bits == 8)},{b(bf16)},{b(generic)},{b(mf)}"
     return {"split": f"paged_decode_kernel<{targs}>",
-            "merge": f"paged_decode_merge_kernel<{dim},{heads},{b(bf16)},{b(generic)}>",
-            "heads_per_unit": heads, "head_groups_per_kv_head": group // heads}
+            "merge": f"paged_decode_merge_kernel<{dim},{slots},{b(bf16)},{b(generic)}>",
+            "matrix_cores": mf, "heads_per_unit": heads,
+            "head_groups_per_kv_head": group // heads}
 
 
 def decode_workspace_bytes(queries_shape: tuple[int, int, int], keys: torch.Tensor, *,
