@@ -87,6 +87,9 @@ def parse():
     ap.add_argument("--wide-heads", default="16/2",
                     help="query/kv heads of the 512-wide legs (a representative shape)")
     ap.add_argument("--no-flush", action="store_true", help="skip the flushed pass")
+    ap.add_argument("--flushed-only", action="store_true",
+                    help="every decode launch follows a cache flush (warmups included, no warm "
+                         "pass): for kernel traces whose averages match the flushed timings")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="approximate CPU time budget of the CPU-baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip every CPU-baseline timing")
@@ -487,9 +490,6 @@ def main():
     def merge():
         call("merge")
 
-    for _ in range(args.warmup):
-        call()
-    torch.cuda.synchronize()
     flush_buf = torch.empty(1 << 30, dtype=torch.uint8, device=device)
     read_buf = torch.ones(1 << 28, dtype=torch.float32, device=device)
 
@@ -500,13 +500,19 @@ def main():
         flush_buf.fill_(1)
         read_buf.sum()
 
+    for _ in range(args.warmup):
+        if args.flushed_only:
+            flush()
+        call()
+    torch.cuda.synchronize()
+
     # The metric and the roofline: whole calls (split + merge, one C-ABI
     # call), HIP events on the kernels' stream. A second loop issues the two
     # passes separately (an event between them) to show where the time goes.
     flushing = None if args.no_flush else flush
     (call_ms,), wall = time_calls([call], args.steps, flushing)
     (split_ms, merge_ms), _ = time_calls([split, merge], args.steps, flushing)
-    (call_w,), _ = time_calls([call], args.steps)
+    call_w = None if args.flushed_only else time_calls([call], args.steps)[0][0]
     ms = call_ms
     med = statistics.median(ms)
     value = kv_bytes / (med * 1e-3) / 1e9
@@ -550,8 +556,9 @@ def main():
         "us_per_layer_step": round(med * 1e3, 2),
         "steps_per_s": round(1e3 / med, 1),
         "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
-        "warm": {"us_median": round(statistics.median(call_w) * 1e3, 2),
-                 "GB_per_s": round(kv_bytes / (statistics.median(call_w) * 1e-3) / 1e9, 2)},
+        "warm": None if args.flushed_only else {
+            "us_median": round(statistics.median(call_w) * 1e3, 2),
+            "GB_per_s": round(kv_bytes / (statistics.median(call_w) * 1e-3) / 1e9, 2)},
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 2),

@@ -377,10 +377,15 @@ void paged_decode_kernel(const Params p) {
   constexpr int EPL = Gm::EPL, NV = Gm::NV, DC = Gm::DC, R = Gm::R, KPS = Gm::KPS;
   constexpr bool PV2 = Gm::PV2;
   constexpr int OPL = Gm::OPL;
-  // Steps in flight per wave: two, or one where a step alone is 16 KiB of
-  // K and V per wave (matrix-core kernels at D = 256), which also keeps
-  // those kernels within 256 registers.
-  constexpr int NBUF = (MF && D >= 256) ? 1 : kNbuf;
+  // Steps in flight per wave: two; one where a step alone is 16 KiB of K
+  // and V per wave (matrix-core kernels at D = 256), which also keeps those
+  // kernels within 256 registers; four at D >= 256 with at most 2 heads per
+  // unit, whose small per-step math leaves registers free (config 4's
+  // Gemma-style shape, 42.5 -> 39.7 us; depths 3 and 4 were slower on the
+  // other configurations).
+  constexpr int NBUF = (MF && D >= 256)                       ? 1
+                       : (!MF && !Q8 && !GEN && D >= 256 && G <= 2) ? 4
+                                                              : kNbuf;
   extern __shared__ int s_dyn[];
   __shared__ int s_ticket[kPairs];
   // Matrix-core kernels: each wave's V tile of one step, [16 keys][kVRow].
