@@ -186,14 +186,36 @@ def decode_step(w, scales, layers, steps):
             times.append(e0.elapsed_time(e1) * 1e3)
         return statistics.median(times)
 
+    def back_to_back(fn, n):
+        """n steps issued one after another with no spin in front: the GPU
+        time per step, or the host's launch time where that is longer."""
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) * 1e6 / n
+        return e0.elapsed_time(e1) * 1e3 / n, wall
+
     n = max(5, min(steps, 20))
     eager = timed(step.run, n)
     graph = timed(step.replay, n)
+    b2b_eager, wall_eager = back_to_back(step.run, n)
+    b2b_graph, wall_graph = back_to_back(step.replay, n)
     del step, arenas, per_layer
     torch.cuda.empty_cache()
     return {"layers": layers, "launches_per_step": 1 + 3 * layers,
             "eager_us": round(eager, 1), "graph_us": round(graph, 1),
-            "graph_us_per_layer": round(graph / layers, 2)}
+            "graph_us_per_layer": round(graph / layers, 2),
+            "back_to_back": {
+                "note": f"{n} steps issued back to back, no spin: per-step time between events "
+                        "and per-step host wall time",
+                "eager_us": round(b2b_eager, 1), "graph_us": round(b2b_graph, 1),
+                "eager_wall_us": round(wall_eager, 1), "graph_wall_us": round(wall_graph, 1)}}
 
 
 def blas_threads() -> int:
@@ -624,6 +646,13 @@ def main():
     line["layer_step_us"] = round(statistics.median(step_ms) * 1e3, 2)
     if args.step_layers > 0:
         line["decode_step"] = decode_step(w, scales, args.step_layers, args.steps)
+        if args.config != 1 and args.kv_bits == 16 and not bf16 and 1 in others:
+            # The small shape, where the host's launch work per layer is longer
+            # than the GPU's: the step graph's case.
+            w1 = workloads.config1(device=device).to_layout(args.layout)
+            line["decode_step_config1"] = decode_step(w1, None, args.step_layers, args.steps)
+            del w1
+            torch.cuda.empty_cache()
     if args.prefill and args.kv_bits == 16:
         line["prefill"] = []
         for case in args.prefill.split(","):

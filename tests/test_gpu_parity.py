@@ -33,6 +33,14 @@ def run(w, split_pages=0, longest=None):
     return out
 
 
+def run_fixed(w):
+    out = paged_decode_attention(
+        w.q, w.keys, w.values, w.tables, w.lengths, page_size=w.page_size, longest=w.longest,
+        scale=w.scale, window=w.window, softcap=w.softcap, deterministic=True)
+    torch.cuda.synchronize()
+    return out
+
+
 def oracle(w):
     q, k, v, t, n = w.numpy()
     return cpu_oracle.decode_f64(q, k, v, t, n, page_size=w.page_size, scale=w.scale,
@@ -125,10 +133,23 @@ def test_configs_full_size(gpu, config):
     check_layouts(w, f"config{config}-full")
 
 
-@pytest.mark.parametrize("batch, length", [(1, 32768), (2, 131072)])
+@pytest.mark.parametrize("batch, length", [(1, 32768), (1, 131072), (2, 32768), (2, 131072),
+                                           (4, 32768), (4, 131072)])
 def test_config3_long_context_full_size(gpu, batch, length):
+    """All six points of BASELINE config 3 (B in {1, 2, 4} x {32768, 131072},
+    ~8 planted x8 keys per sequence and kv head, pages fragmented over a 2x
+    arena); B = 4 x 131072 reads 2.15 GB of K/V per call. The long sequences
+    are cut into the most pieces, so the log-sum-exp merge of large planted
+    logits is exercised hardest here."""
     w = workloads.config3(device=gpu, batch=batch, length=length)
-    check_layouts(w, f"config3-b{batch}-{length}")
+    assert w.meta["planted"] == 8
+    expected = oracle(w)
+    got = check_layouts(w, f"config3-b{batch}-{length}", expected)
+    # The fixed split gives the same result bit for bit on a second call.
+    a = run_fixed(w)
+    assert_parity(a, expected, f"config3-b{batch}-{length} fixed")
+    assert torch.equal(run_fixed(w), a)
+    del got
 
 
 def test_config5_full_size(gpu):
@@ -156,10 +177,10 @@ def test_longest_hint_understated_stays_correct(gpu):
     assert_parity(run(w, longest=16), oracle(w), "longest=16")
 
 
-@pytest.mark.parametrize("shape", [s for s in workloads.REFERENCE_TEST_SHAPES if s[2] != 4])
+@pytest.mark.parametrize("shape", workloads.REFERENCE_TEST_SHAPES)
 def test_reference_kernel_test_shapes(gpu, shape):
-    """The five shapes of test_mlx_engine.py:422-431 (16-bit), except head_dim
-    4, which has no MI355X kernel (the C-ABI rejects it)."""
+    """The five shapes of test_mlx_engine.py:422-431 (16-bit); head_dim 4 runs
+    the generic kernel (8-bit versions in test_gpu_shapes.py)."""
     w = workloads.reference_test_case(*shape, device=gpu)
     check_layouts(w, f"reftest{shape[:3]}")
 
