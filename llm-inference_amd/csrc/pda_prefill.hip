@@ -41,6 +41,10 @@
 //    XCD serves the tile to all of them.
 //  * LDS rows are padded so that the 16 lanes of a 16-byte K read, and the
 //    four rows of a transposed V read, fall on distinct banks.
+//  * Other even head dims up to 512 (GEN) run the kernel of the next of
+//    those widths: rows are gathered as element pairs (the row length is a
+//    multiple of 4 bytes only), the pairs past the head dim are zero in Q, K
+//    and V, and only the real dims are written.
 
 #include <hip/hip_runtime.h>
 
@@ -64,6 +68,7 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 constexpr float kLog2e = 1.44269504088896340736f;
@@ -108,6 +113,7 @@ struct PrefillParams {
   int32_t page_step;   // keys per tile / page_size when that divides, else 0
   int32_t hq;
   int32_t hkv;
+  int32_t head_dim;    // row length of Q, K, V and the output (GEN: below D)
   int32_t page_size;
   int32_t window;
   float scale_log2;
@@ -153,7 +159,8 @@ constexpr int blocks_per_tile() { return D <= 128 ? 2 : 1; }
 // BF: queries, K/V and output in bf16 (bf16 models); every 16-bit value is
 // moved as raw bits and only the matrix-core steps, the probabilities and the
 // output rounding differ.
-template <int D, bool Q8, bool BF>
+// GEN: head dim p.head_dim (even) below D; D-wide tiles, zero past it.
+template <int D, bool Q8, bool BF, bool GEN>
 __global__ __launch_bounds__(64 * waves_for(D)) void paged_prefill_kernel(const PrefillParams p) {
   static_assert(!(Q8 && BF), "8-bit K/V dequantizes to fp16");
   constexpr int KB = blocks_per_tile<D>();  // 32-key blocks per tile
@@ -228,7 +235,22 @@ __global__ __launch_bounds__(64 * waves_for(D)) void paged_prefill_kernel(const 
   // Query fragments (B operand of S^T = K Q^T): dims 16 c + 8 hh .. + 7 of
   // the wave's slice.
   f16x8 qf[kDW / 16];
-  {
+  if constexpr (GEN) {
+    // Element pairs, clamped into the row; zero past the head dim.
+    const int hd = p.head_dim;
+    const f16* qp = p.q + ((int64_t)(q_live ? qi : 0) * p.hq + h) * hd;
+#pragma unroll
+    for (int c = 0; c < kDW / 16; ++c) {
+      i32x4 x;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int d = sl * kDW + 16 * c + 8 * hh + 2 * j;
+        const int y = *reinterpret_cast<const int*>(qp + min(d, hd - 2));
+        x[j] = q_live && d < hd ? y : 0;
+      }
+      qf[c] = __builtin_bit_cast(f16x8, x);
+    }
+  } else {
     const f16* qp = p.q + ((int64_t)(q_live ? qi : 0) * p.hq + h) * D + sl * kDW + 8 * hh;
 #pragma unroll
     for (int c = 0; c < kDW / 16; ++c) {
@@ -295,7 +317,7 @@ __global__ __launch_bounds__(64 * waves_for(D)) void paged_prefill_kernel(const 
   auto lookup = [&](int& page, bool& in, int& row_off, int& scale_off) {
     in = kp <= last && pi < p.table_len;
     page = p.table[min(pi, p.table_len - 1)];
-    row_off = r * p.row_elems + kvh * p.head_elems + gp * 8;
+    row_off = r * p.row_elems + kvh * p.head_elems + (GEN ? 0 : gp * 8);
     scale_off = r * p.scale_row + kvh * p.scale_head;
     kp += kKeys;
     if (p.page_step > 0) {
@@ -305,11 +327,45 @@ __global__ __launch_bounds__(64 * waves_for(D)) void paged_prefill_kernel(const 
       r = kp - pi * p.page_size;
     }
   };
+  // GEN: dim of element pair j of piece i, clamped into the row (pairs past
+  // the head dim reload the last pair; trim zeroes them).
+  auto pair_dim = [&](int i, int j) { return min(8 * (gp + kTpk * i) + 2 * j, p.head_dim - 2); };
   auto fetch = [&](int page, bool in, int row_off, int scale_off) {
     gok = in && page >= 0 && page < p.arena_pages;
     const uint32_t pg = (uint32_t)(gok ? page : 0);
     const uint64_t at = (uint64_t)pg * (uint64_t)p.page_elems + row_off;
-    if constexpr (Q8) {
+    if constexpr (GEN && Q8) {
+      const uint8_t* kb = static_cast<const uint8_t*>(p.k) + at;
+      const uint8_t* vb = static_cast<const uint8_t*>(p.v) + at;
+#pragma unroll
+      for (int i = 0; i < kPieces; ++i) {
+        uint32_t kw[4], vw[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          kw[j] = *reinterpret_cast<const uint16_t*>(kb + pair_dim(i, j));
+          vw[j] = *reinterpret_cast<const uint16_t*>(vb + pair_dim(i, j));
+        }
+        kr[i] = uint2{kw[0] | kw[1] << 16, kw[2] | kw[3] << 16};
+        vr[i] = uint2{vw[0] | vw[1] << 16, vw[2] | vw[3] << 16};
+      }
+      const uint64_t sat = (uint64_t)pg * (uint64_t)p.scale_page + scale_off;
+      ksc = p.kscale[sat];
+      vsc = p.vscale[sat];
+    } else if constexpr (GEN) {
+      const f16* kb = static_cast<const f16*>(p.k) + at;
+      const f16* vb = static_cast<const f16*>(p.v) + at;
+#pragma unroll
+      for (int i = 0; i < kPieces; ++i) {
+        i32x4 kw, vw;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          kw[j] = *reinterpret_cast<const int*>(kb + pair_dim(i, j));
+          vw[j] = *reinterpret_cast<const int*>(vb + pair_dim(i, j));
+        }
+        kr[i] = __builtin_bit_cast(f16x8, kw);
+        vr[i] = __builtin_bit_cast(f16x8, vw);
+      }
+    } else if constexpr (Q8) {
       const uint8_t* kb = static_cast<const uint8_t*>(p.k) + at;
       const uint8_t* vb = static_cast<const uint8_t*>(p.v) + at;
 #pragma unroll
@@ -332,7 +388,8 @@ __global__ __launch_bounds__(64 * waves_for(D)) void paged_prefill_kernel(const 
   };
   // A staged piece as 8 fp16 values (8-bit: fp16(int8 x scale), one
   // rounding of the exact product).
-  auto as_f16 = [&](const piece_t& x, f16 scale) -> f16x8 {
+  auto as_f16 = [&](const piece_t& x, f16 scale, int i) -> f16x8 {
+    f16x8 y;
     if constexpr (Q8) {
       const f16x2 s2 = {scale, scale};
       const uint32_t lo = x.x ^ 0x80808080u, hi = x.y ^ 0x80808080u;
@@ -340,22 +397,29 @@ __global__ __launch_bounds__(64 * waves_for(D)) void paged_prefill_kernel(const 
       const f16x2 e1 = pda_internal::bytes_to_f16x2(lo, 0x04030402u) * s2;
       const f16x2 e2 = pda_internal::bytes_to_f16x2(hi, 0x04010400u) * s2;
       const f16x2 e3 = pda_internal::bytes_to_f16x2(hi, 0x04030402u) * s2;
-      return f16x8{e0[0], e0[1], e1[0], e1[1], e2[0], e2[1], e3[0], e3[1]};
+      y = f16x8{e0[0], e0[1], e1[0], e1[1], e2[0], e2[1], e3[0], e3[1]};
     } else {
       (void)scale;
-      return x;
+      y = x;
     }
+    if constexpr (GEN) {  // zero the pairs past the head dim
+      i32x4 w4 = __builtin_bit_cast(i32x4, y);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) w4[j] = 8 * (gp + kTpk * i) + 2 * j < p.head_dim ? w4[j] : 0;
+      y = __builtin_bit_cast(f16x8, w4);
+    }
+    return y;
   };
   auto stash_v = [&](int vbuf) {
     f16* vd = s_v[vbuf] + gk * kVRow + gp * 8;
     if (__ballot(gok) == ~0ull) {
 #pragma unroll
       for (int i = 0; i < kPieces; ++i)
-        *reinterpret_cast<f16x8*>(vd + 8 * kTpk * i) = as_f16(vr[i], vsc);
+        *reinterpret_cast<f16x8*>(vd + 8 * kTpk * i) = as_f16(vr[i], vsc, i);
     } else {
 #pragma unroll
       for (int i = 0; i < kPieces; ++i)
-        *reinterpret_cast<f16x8*>(vd + 8 * kTpk * i) = gok ? as_f16(vr[i], vsc) : f16x8{};
+        *reinterpret_cast<f16x8*>(vd + 8 * kTpk * i) = gok ? as_f16(vr[i], vsc, i) : f16x8{};
     }
   };
   auto stash = [&](int buf) {
@@ -366,20 +430,20 @@ __global__ __launch_bounds__(64 * waves_for(D)) void paged_prefill_kernel(const 
     if constexpr (kOneV) {
 #pragma unroll
       for (int i = 0; i < kPieces; ++i)
-        *reinterpret_cast<f16x8*>(kd + 8 * kTpk * i) = gok ? as_f16(kr[i], ksc) : f16x8{};
+        *reinterpret_cast<f16x8*>(kd + 8 * kTpk * i) = gok ? as_f16(kr[i], ksc, i) : f16x8{};
     } else {
       f16* vd = s_v[buf] + gk * kVRow + gp * 8;
       if (bits == ~0ull) {  // wave-uniform: the usual case stores without selects
 #pragma unroll
         for (int i = 0; i < kPieces; ++i) {
-          *reinterpret_cast<f16x8*>(kd + 8 * kTpk * i) = as_f16(kr[i], ksc);
-          *reinterpret_cast<f16x8*>(vd + 8 * kTpk * i) = as_f16(vr[i], vsc);
+          *reinterpret_cast<f16x8*>(kd + 8 * kTpk * i) = as_f16(kr[i], ksc, i);
+          *reinterpret_cast<f16x8*>(vd + 8 * kTpk * i) = as_f16(vr[i], vsc, i);
         }
       } else {
 #pragma unroll
         for (int i = 0; i < kPieces; ++i) {
-          *reinterpret_cast<f16x8*>(kd + 8 * kTpk * i) = gok ? as_f16(kr[i], ksc) : f16x8{};
-          *reinterpret_cast<f16x8*>(vd + 8 * kTpk * i) = gok ? as_f16(vr[i], vsc) : f16x8{};
+          *reinterpret_cast<f16x8*>(kd + 8 * kTpk * i) = gok ? as_f16(kr[i], ksc, i) : f16x8{};
+          *reinterpret_cast<f16x8*>(vd + 8 * kTpk * i) = gok ? as_f16(vr[i], vsc, i) : f16x8{};
         }
       }
     }
@@ -602,7 +666,7 @@ __global__ __launch_bounds__(64 * waves_for(D)) void paged_prefill_kernel(const 
   if (p.splits > 1) {
     // Unnormalised partial and its (max, sum) for the merge; an empty or
     // fully masked range leaves m = -inf, l = 0 and zeros.
-    const int64_t at = ((int64_t)split * p.count + qi) * p.hq + h;
+    const int64_t at = ((int64_t)split * p.count + qi) * p.hq + h;  // partials are D wide
     float* dst = p.part_o + at * D + sl * kDW;
 #pragma unroll
     for (int b = 0; b < kDW / 32; ++b)
@@ -614,6 +678,24 @@ __global__ __launch_bounds__(64 * waves_for(D)) void paged_prefill_kernel(const 
     return;
   }
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+  if constexpr (GEN) {
+    // Rows of head_dim elements: element pairs, the real dims only.
+    const int hd = p.head_dim;
+    f16* dst = p.out + ((int64_t)qi * p.hq + h) * hd;
+#pragma unroll
+    for (int b = 0; b < kDW / 32; ++b) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = sl * kDW + 32 * b + 8 * g + 4 * hh;
+        const f16x2 y0 = {round16<BF>(o[b][4 * g] * inv), round16<BF>(o[b][4 * g + 1] * inv)};
+        const f16x2 y1 = {round16<BF>(o[b][4 * g + 2] * inv),
+                          round16<BF>(o[b][4 * g + 3] * inv)};
+        if (d < hd) *reinterpret_cast<f16x2*>(dst + d) = y0;
+        if (d + 2 < hd) *reinterpret_cast<f16x2*>(dst + d + 2) = y1;
+      }
+    }
+    return;
+  }
   f16* dst = p.out + ((int64_t)qi * p.hq + h) * D + sl * kDW;
   // O^T rows: element 32 b + 8 (v / 4) + 4 hh + v % 4 of query n (of the slice).
 #pragma unroll
@@ -633,11 +715,12 @@ __global__ __launch_bounds__(64 * waves_for(D)) void paged_prefill_kernel(const 
 // sum_s w_s o_s / sum_s w_s l_s (0 when nothing was visible). The same LSE
 // merge as the reference's decode merge (metal_kernels.py:103-124), in the
 // log2 domain. One thread per 4 dims, D / 4 threads per (query, head).
-template <int D, bool BF>
+// GEN: output rows of hd (even, below D) elements; partials stay D wide.
+template <int D, bool BF, bool GEN>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restrict__ part_o,
                                                             const float2* __restrict__ part_ml,
                                                             f16* __restrict__ out, int64_t pairs,
-                                                            int splits) {
+                                                            int splits, int hd) {
   constexpr int kT = D / 4;
   // 256 / kT pairs per block; at D = 96 the last 16 threads have none.
   if (threadIdx.x >= 256 / kT * kT) return;
@@ -664,7 +747,14 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restr
   const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
   f16x4 y = {round16<BF>(acc.x * inv), round16<BF>(acc.y * inv), round16<BF>(acc.z * inv),
              round16<BF>(acc.w * inv)};
-  *reinterpret_cast<f16x4*>(out + pair * D + d) = y;
+  if constexpr (GEN) {
+    f16* row = out + pair * hd;
+    if (d < hd) *reinterpret_cast<f16x2*>(row + d) = f16x2{y[0], y[1]};
+    if (d + 2 < hd) *reinterpret_cast<f16x2*>(row + d + 2) = f16x2{y[2], y[3]};
+  } else {
+    (void)hd;
+    *reinterpret_cast<f16x4*>(out + pair * D + d) = y;
+  }
 }
 
 constexpr int kCus = 256;       // MI355X compute units
@@ -709,22 +799,42 @@ size_t prefill_workspace(int splits, int count, int q_heads, int head_dim) {
 using pda_internal::fail;
 using pda_internal::ok;
 
+// The kernel width serving a head dim: the head dim itself when a kernel
+// has it, else the next wider one (GEN kernels); 0 for head dims the
+// library does not serve (odd, or above 512).
+int prefill_dim(int head_dim) {
+  if (head_dim < 2 || head_dim > 512 || (head_dim & 1)) return 0;
+  for (int d : {64, 96, 128, 256, 512})
+    if (head_dim <= d) return d;
+  return 0;
+}
+
+template <bool Q8, bool BF, bool GEN>
+const void* prefill_kernel_for(int kdim) {
+  return kdim == 64    ? reinterpret_cast<const void*>(paged_prefill_kernel<64, Q8, BF, GEN>)
+         : kdim == 96  ? reinterpret_cast<const void*>(paged_prefill_kernel<96, Q8, BF, GEN>)
+         : kdim == 128 ? reinterpret_cast<const void*>(paged_prefill_kernel<128, Q8, BF, GEN>)
+         : kdim == 256 ? reinterpret_cast<const void*>(paged_prefill_kernel<256, Q8, BF, GEN>)
+                       : reinterpret_cast<const void*>(paged_prefill_kernel<512, Q8, BF, GEN>);
+}
+
 template <bool Q8, bool BF>
-const void* prefill_kernel_for(int head_dim) {
-  return head_dim == 64    ? reinterpret_cast<const void*>(paged_prefill_kernel<64, Q8, BF>)
-         : head_dim == 96  ? reinterpret_cast<const void*>(paged_prefill_kernel<96, Q8, BF>)
-         : head_dim == 128 ? reinterpret_cast<const void*>(paged_prefill_kernel<128, Q8, BF>)
-         : head_dim == 256 ? reinterpret_cast<const void*>(paged_prefill_kernel<256, Q8, BF>)
-                           : reinterpret_cast<const void*>(paged_prefill_kernel<512, Q8, BF>);
+const void* prefill_kernel_for(int kdim, bool gen) {
+  return gen ? prefill_kernel_for<Q8, BF, true>(kdim) : prefill_kernel_for<Q8, BF, false>(kdim);
+}
+
+template <bool BF, bool GEN>
+const void* merge_kernel_for(int kdim) {
+  return kdim == 64    ? reinterpret_cast<const void*>(prefill_merge_kernel<64, BF, GEN>)
+         : kdim == 96  ? reinterpret_cast<const void*>(prefill_merge_kernel<96, BF, GEN>)
+         : kdim == 128 ? reinterpret_cast<const void*>(prefill_merge_kernel<128, BF, GEN>)
+         : kdim == 256 ? reinterpret_cast<const void*>(prefill_merge_kernel<256, BF, GEN>)
+                       : reinterpret_cast<const void*>(prefill_merge_kernel<512, BF, GEN>);
 }
 
 template <bool BF>
-const void* merge_kernel_for(int head_dim) {
-  return head_dim == 64    ? reinterpret_cast<const void*>(prefill_merge_kernel<64, BF>)
-         : head_dim == 96  ? reinterpret_cast<const void*>(prefill_merge_kernel<96, BF>)
-         : head_dim == 128 ? reinterpret_cast<const void*>(prefill_merge_kernel<128, BF>)
-         : head_dim == 256 ? reinterpret_cast<const void*>(prefill_merge_kernel<256, BF>)
-                           : reinterpret_cast<const void*>(prefill_merge_kernel<512, BF>);
+const void* merge_kernel_for(int kdim, bool gen) {
+  return gen ? merge_kernel_for<BF, true>(kdim) : merge_kernel_for<BF, false>(kdim);
 }
 
 int prefill(const void* queries, const void* keys, const void* values, const void* key_scales,
@@ -742,10 +852,11 @@ int prefill(const void* queries, const void* keys, const void* values, const voi
                 count, start, q_heads, kv_heads, page_size, table_len, window, splits);
   if (q_heads % kv_heads)
     return fail(PDA_ERR_HEAD_RATIO, "query heads must be a multiple of kv heads");
-  if (head_dim != 64 && head_dim != 96 && head_dim != 128 && head_dim != 256 &&
-      head_dim != 512)
-    return fail(PDA_ERR_HEAD_DIM, "head_dim %d has no prefill kernel (64, 96, 128, 256, 512)",
+  const int kdim = prefill_dim(head_dim);
+  if (kdim == 0)
+    return fail(PDA_ERR_HEAD_DIM, "head_dim %d: prefill serves even head dims 2..512",
                 head_dim);
+  const bool gen = kdim != head_dim;
   if (count == 0) return ok();
   if (table_len == 0)
     return fail(PDA_ERR_INVALID_ARGUMENT, "an empty page table holds no keys of the chunk");
@@ -773,11 +884,11 @@ int prefill(const void* queries, const void* keys, const void* values, const voi
   if (q8 && (((uintptr_t)key_scales | (uintptr_t)value_scales) & 1))
     return fail(PDA_ERR_ALIGNMENT, "fp16 scale arenas must be 2-byte aligned");
   if ((uintptr_t)table & 3) return fail(PDA_ERR_ALIGNMENT, "the table must be 4-byte aligned");
-  const int nsplit = prefill_splits(start, count, q_heads, head_dim, window, splits);
-  const int per_wg = queries_for(head_dim);
+  const int nsplit = prefill_splits(start, count, q_heads, kdim, window, splits);
+  const int per_wg = queries_for(kdim);
   if ((int64_t)((count + per_wg - 1) / per_wg) * q_heads * nsplit > INT32_MAX)
     return fail(PDA_ERR_INVALID_ARGUMENT, "query tiles x query heads x splits exceeds 2^31");
-  const size_t need = prefill_workspace(nsplit, count, q_heads, head_dim);
+  const size_t need = prefill_workspace(nsplit, count, q_heads, kdim);
   if (need > 0 && (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 255)))
     return fail(PDA_ERR_WORKSPACE,
                 "%d key ranges need a 256-byte aligned workspace of %zu bytes (got %zu)", nsplit,
@@ -802,7 +913,7 @@ int prefill(const void* queries, const void* keys, const void* values, const voi
   prm.part_o = nsplit > 1 ? static_cast<float*>(workspace) : nullptr;
   prm.part_ml = nsplit > 1 ? reinterpret_cast<float2*>(
                                  static_cast<char*>(workspace) +
-                                 (((size_t)nsplit * pairs * head_dim * 4 + 255) & ~(size_t)255))
+                                 (((size_t)nsplit * pairs * kdim * 4 + 255) & ~(size_t)255))
                            : nullptr;
   prm.arena_pages = arena_rows / page_size;
   prm.page_elems = (int64_t)page_size * kv_heads * head_dim;
@@ -818,10 +929,11 @@ int prefill(const void* queries, const void* keys, const void* values, const voi
   prm.count = count;
   prm.tiles = (count + per_wg - 1) / per_wg;
   prm.splits = nsplit;
-  const int tile_keys = head_dim <= 128 ? 64 : 32;
+  const int tile_keys = kdim <= 128 ? 64 : 32;
   prm.page_step = tile_keys % page_size == 0 ? tile_keys / page_size : 0;
   prm.hq = q_heads;
   prm.hkv = kv_heads;
+  prm.head_dim = head_dim;
   prm.page_size = page_size;
   prm.window = window;
   prm.scale_log2 = scale * kLog2e;
@@ -829,24 +941,25 @@ int prefill(const void* queries, const void* keys, const void* values, const voi
   prm.cap_in = softcap > 0.0f ? 2.0f * kLog2e * scale / softcap : 0.0f;
   prm.cap_out = softcap * kLog2e;
   void* args[] = {&prm};
-  const void* fn = q8 ? prefill_kernel_for<true, false>(head_dim)
-                  : bf16_elems ? prefill_kernel_for<false, true>(head_dim)
-                               : prefill_kernel_for<false, false>(head_dim);
+  const void* fn = q8 ? prefill_kernel_for<true, false>(kdim, gen)
+                  : bf16_elems ? prefill_kernel_for<false, true>(kdim, gen)
+                               : prefill_kernel_for<false, false>(kdim, gen);
   const hipStream_t hs = static_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)((int64_t)prm.tiles * q_heads * nsplit));
-  hipError_t err = hipLaunchKernel(fn, grid, dim3(64 * waves_for(head_dim)), args, 0, hs);
+  hipError_t err = hipLaunchKernel(fn, grid, dim3(64 * waves_for(kdim)), args, 0, hs);
   if (err != hipSuccess)
     return fail(PDA_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(err));
   if (nsplit > 1) {
     const int64_t npairs = (int64_t)pairs;
-    const int per_block = 256 / (head_dim / 4);
+    const int per_block = 256 / (kdim / 4);
     const float* po = prm.part_o;
     const float2* pml = prm.part_ml;
     f16* o16 = prm.out;
     int ns = nsplit;
-    void* margs[] = {&po, &pml, &o16, (void*)&npairs, &ns};
-    const void* mfn = bf16_elems ? merge_kernel_for<true>(head_dim)
-                                 : merge_kernel_for<false>(head_dim);
+    int hd = head_dim;
+    void* margs[] = {&po, &pml, &o16, (void*)&npairs, &ns, &hd};
+    const void* mfn = bf16_elems ? merge_kernel_for<true>(kdim, gen)
+                                 : merge_kernel_for<false>(kdim, gen);
     err = hipLaunchKernel(mfn, dim3((unsigned)((npairs + per_block - 1) / per_block)),
                           dim3(256), margs, 0, hs);
     if (err != hipSuccess)
@@ -865,13 +978,13 @@ int pda_prefill_workspace_bytes(int32_t start, int32_t count, int32_t q_heads,
   if (count < 0 || start < 0 || q_heads <= 0 || window < 0 || splits < 0 || !bytes)
     return fail(PDA_ERR_INVALID_ARGUMENT, "count=%d start=%d q_heads=%d window=%d splits=%d",
                 count, start, q_heads, window, splits);
-  if (head_dim != 64 && head_dim != 96 && head_dim != 128 && head_dim != 256 &&
-      head_dim != 512)
-    return fail(PDA_ERR_HEAD_DIM, "head_dim %d has no prefill kernel (64, 96, 128, 256, 512)",
+  const int kdim = prefill_dim(head_dim);
+  if (kdim == 0)
+    return fail(PDA_ERR_HEAD_DIM, "head_dim %d: prefill serves even head dims 2..512",
                 head_dim);
-  const int s = count == 0 ? 1 : prefill_splits(start, count, q_heads, head_dim, window, splits);
+  const int s = count == 0 ? 1 : prefill_splits(start, count, q_heads, kdim, window, splits);
   if (splits_used) *splits_used = s;
-  *bytes = prefill_workspace(s, count, q_heads, head_dim);
+  *bytes = prefill_workspace(s, count, q_heads, kdim);
   return ok();
 }
 

@@ -190,7 +190,8 @@ def prefill(**overrides):
     (dict(splits=4, workspace=FAKE, workspace_bytes=1 << 20), _lib.PDA_ERR_WORKSPACE),
     (dict(splits=4, workspace=FAKE + 16, workspace_bytes=1 << 30), _lib.PDA_ERR_WORKSPACE),
     (dict(q_heads=30), _lib.PDA_ERR_HEAD_RATIO),
-    (dict(head_dim=80), _lib.PDA_ERR_HEAD_DIM),
+    (dict(head_dim=81), _lib.PDA_ERR_HEAD_DIM),
+    (dict(head_dim=514), _lib.PDA_ERR_HEAD_DIM),
     (dict(start=(1 << 31) - 100), _lib.PDA_ERR_TOO_LONG),
     (dict(out=None), _lib.PDA_ERR_INVALID_ARGUMENT),
     (dict(table=None), _lib.PDA_ERR_INVALID_ARGUMENT),
@@ -232,8 +233,13 @@ def test_prefill_split_plan():
     assert _lib.prefill_workspace_bytes(0, 100, 8, 64, splits=3)[0] == 3
     assert _lib.prefill_workspace_bytes(0, 100, 8, 64, splits=500)[0] == 64
     assert _lib.prefill_workspace_bytes(0, 0, 8, 64, splits=3) == (1, 0)
-    with pytest.raises(_lib.PdaError):
-        _lib.prefill_workspace_bytes(0, 10, 8, 80)
+    # Head dims without a kernel of their own plan as the next wider kernel.
+    for d, width in ((80, 96), (4, 64), (200, 256), (510, 512), (66, 96), (98, 128)):
+        assert _lib.prefill_workspace_bytes(3000, 256, 8, d) == \
+            _lib.prefill_workspace_bytes(3000, 256, 8, width)
+    for d in (0, 1, 81, 514, -2):
+        with pytest.raises(_lib.PdaError):
+            _lib.prefill_workspace_bytes(0, 10, 8, d)
     # 512-wide heads: 64 queries per workgroup, one workgroup per CU. A
     # 64-token chunk at 8 heads is 8 workgroups; 32 ranges would fill the
     # 256 CUs, but a range keeps at least 8 key tiles: 6064 keys / 32 / 8 = 23.
@@ -264,5 +270,5 @@ def test_prefill_q8_validation():
     assert call(ks=None) == _lib.PDA_ERR_INVALID_ARGUMENT
     assert call(vs=None) == _lib.PDA_ERR_INVALID_ARGUMENT
     assert call(ks=FAKE + 1) == _lib.PDA_ERR_ALIGNMENT
-    assert call(head_dim=80) == _lib.PDA_ERR_HEAD_DIM
+    assert call(head_dim=79) == _lib.PDA_ERR_HEAD_DIM
     assert call(count=0, ks=None, vs=None) == _lib.PDA_OK
