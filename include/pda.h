@@ -381,8 +381,11 @@ int pda_prefill_workspace_bytes(int32_t start, int32_t count, int32_t q_heads,
  * num_images is 0) lists image-token spans [begin, end) of positions: a
  * query inside a span also sees every key of that span up to the chunk's
  * end, whatever the causal limit and the window (batches.py:107-118).
- * head_dim in {64, 96, 128, 256, 512} (512: the 512-wide heads of Gemma 4's
- * global layers, docs/roadmap.md:36). With more than one key range
+ * Any even head_dim up to 512, as for the decode call: 64, 96, 128, 256 and
+ * 512 (the 512-wide heads of Gemma 4's global layers, docs/roadmap.md:36)
+ * run kernels of their own, the others the next wider one with the dims
+ * past head_dim zero; odd or larger head dims return PDA_ERR_HEAD_DIM.
+ * With more than one key range
  * (see pda_prefill_workspace_bytes; results do not depend on `splits`
  * beyond fp32 rounding) the ranges' partials go to `workspace` (256-byte
  * aligned, at least the bytes that call reports) and a second launch merges
