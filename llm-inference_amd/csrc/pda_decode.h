@@ -1087,12 +1087,12 @@ void paged_decode_kernel(const Params p) {
         // Cut unit: the unnormalised partial, slot chosen as below.
         const bool holds_start = back ? !pending : first_unit;
         const int64_t slot = 2 * vw + (holds_start ? 0 : 1);
-        float* const dst = p.part_o + (slot * G + head) * D + 4 * mg;
+        float* const dst = p.part_o + (slot * hpu + head) * D + 4 * mg;
 #pragma unroll
         for (int i = 0; i < D / 16; ++i)
           *reinterpret_cast<float4*>(dst + 16 * i) =
               make_float4(ob[i][0], ob[i][1], ob[i][2], ob[i][3]);
-        if (mg == 0) p.part_ml[slot * G + head] = make_float2(m[0], lt);
+        if (mg == 0) p.part_ml[slot * hpu + head] = make_float2(m[0], lt);
       }
     } else {
     // Fold the wave's key subsets (metal_kernels.py:63-81); every lane then
@@ -1275,11 +1275,11 @@ __global__ __launch_bounds__(kMergeMaxWaves * 64) void paged_decode_merge_kernel
     for (int u = 0; u < kBatch; ++u) {
       sl[u] = __builtin_amdgcn_readlane(mine, u);
       const int64_t at = sl[u] < 0 ? 0 : sl[u];
-      ml[u] = p.part_ml[at * G + g];
+      ml[u] = p.part_ml[at * uh + g];
 #pragma unroll
       for (int c = 0; c < kChunks; ++c) {
         const int d = c * 64 + lane;
-        part[u][c] = d < D ? p.part_o[(at * G + g) * D + d] : 0.0f;
+        part[u][c] = d < D ? p.part_o[(at * uh + g) * D + d] : 0.0f;
       }
     }
     float bt = -INFINITY;

@@ -155,15 +155,18 @@ int heads_per_group(int gtot) {
 }
 
 // Matrix-core kernels: 16-bit K/V, head dims whose rows split into 32-element
-// chunks, and GQA groups of at least mf_min_group() heads (8; the
-// PDA_MFMA_MIN_GROUP environment variable moves it, for measurements).
+// chunks, and GQA groups of at least mf_min_group() heads (5; the
+// PDA_MFMA_MIN_GROUP environment variable moves it, for measurements). From
+// 5 heads on, the VALU's q.k and p.v issue of the 8-wave workgroup costs
+// more than the matrix cores' 16-head tiles with idle head slots (config 2's
+// lengths, D 64 to 256); at 4 heads and fewer the VALU kernels are faster.
 bool mf_dim(int d) { return d == 64 || d == 96 || d == 128 || d == 256; }
 
 int mf_min_group() {
   static const int value = [] {
     const char* env = getenv("PDA_MFMA_MIN_GROUP");
     const int v = env ? atoi(env) : 0;
-    return v > 0 ? v : 8;
+    return v > 0 ? v : 5;
   }();
   return value;
 }
@@ -218,7 +221,7 @@ int make_plan(int32_t batch, int32_t q_heads, int32_t kv_heads, int32_t head_dim
   pl.nhg = gtot / pl.unit_heads;
   // The workspace holds the widest slot layout either cache type could use
   // for this shape (pda_workspace_bytes does not know the element type).
-  const int g_ws = use_mf(gtot, head_dim, false) ? 16 : heads_per_group(gtot);
+  const int g_ws = use_mf(gtot, head_dim, false) ? mf_unit_heads(gtot) : heads_per_group(gtot);
   if ((int64_t)kv_heads * pl.nhg > 65535)
     return fail(PDA_ERR_INVALID_ARGUMENT, "kv heads x head groups above 65535");
   // Visible pages of one sequence are bounded by the table width and, with a
@@ -434,7 +437,7 @@ int decode(int passes, const void* queries, const void* keys, const void* values
   wl.off_o = pl.off_o;
   wl.total = pl.total;
   if (use_scratch) {
-    wl = workspace_layout(batch, pl.G, kernel_dim(head_dim, q8), (int64_t)groups * kPairs,
+    wl = workspace_layout(batch, pl.unit_heads, kernel_dim(head_dim, q8), (int64_t)groups * kPairs,
                           (int64_t)groups * 2 * kSplitWaves);
     if (wl.total > kScratchBytes)
       return fail(PDA_ERR_WORKSPACE,

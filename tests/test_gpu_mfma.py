@@ -1,8 +1,8 @@
-"""Decode on the matrix cores: GQA groups of 8 or more query heads per kv head.
+"""Decode on the matrix cores: GQA groups of 5 or more query heads per kv head.
 
 The reference serves a whole GQA group from one K/V read whatever its size
 (32 x G x R threads per threadgroup, metal_kernels.py:191-192,216-217). Here
-groups of 8 to 16 heads (and larger groups as units of up to 16) run
+groups of 5 to 16 heads (and larger groups as units of up to 16) run
 S^T = K Q^T and O^T += V^T P^T on v_mfma_f32_16x16x32 / 16x16x16 at head dims
 64, 96, 128 and 256, one K/V read per unit. Checked against the float64
 oracle (max-abs 2e-3, mean-abs 2e-4; bf16 at its own bar,
@@ -82,7 +82,8 @@ def check(w, what, **kw):
 
 
 @pytest.mark.parametrize("head_dim", [64, 96, 128, 256])
-@pytest.mark.parametrize("q_heads,kv_heads", [(8, 1), (16, 2), (9, 1), (11, 1), (12, 1),
+@pytest.mark.parametrize("q_heads,kv_heads", [(5, 1), (6, 1), (7, 1), (28, 4), (14, 2),
+                                              (8, 1), (16, 2), (9, 1), (11, 1), (12, 1),
                                               (13, 1), (16, 1), (24, 2), (32, 2), (40, 2)])
 def test_group_sizes_and_head_dims(gpu, q_heads, kv_heads, head_dim):
     lengths = [1, 15, 16, 17, 600, 2500, 33]
