@@ -341,7 +341,9 @@ def prefill_leg(w, tokens, steps, start=0):
     med = statistics.median(ms)
     tflops = flops / (med * 1e-3) / 1e12
     bf16 = dtype == torch.bfloat16
-    return {"kernel": f"paged_prefill_kernel<{d},false,{str(bf16).lower()}> "
+    width = next(x for x in (64, 96, 128, 256, 512) if d <= x)  # the kernel that serves d
+    return {"kernel": f"paged_prefill_kernel<{width},false,{str(bf16).lower()},"
+                      f"{str(width != d).lower()}> "
                       f"(pda_paged_prefill_attention{'_bf16' if bf16 else ''})",
             "tokens": tokens, "start": start, "key_ranges": splits, "q_heads": hq,
             "kv_heads": hkv, "head_dim": d,
