@@ -57,7 +57,7 @@ def parse():
     ap.add_argument("--group", type=int, default=0,
                     help="query heads per kv head (0 = the config's): the config's lengths, "
                          "tables and K/V with a larger or smaller GQA group, for the "
-                         "matrix-core vs VALU study at G >= 8")
+                         "matrix-core vs VALU study")
     ap.add_argument("--split-pages", type=int, default=0)
     ap.add_argument("--deterministic", action="store_true",
                     help="fixed split points (PDA_DECODE_FIXED_SPLIT): bitwise reproducible")

@@ -59,8 +59,8 @@ struct Params {
   f16* out;
   int32_t* prefix;    // [B + 1] visible pages before each sequence (workspace)
   int32_t* meet;      // [pairs] pages the first wave of each pair took (workspace)
-  float2* part_ml;    // [kSlots][G] (running max, sum) of cut units
-  float* part_o;      // [kSlots][G][D] unnormalised outputs of cut units
+  float2* part_ml;    // [slots][unit_heads] (running max, sum) of cut units
+  float* part_o;      // [slots][unit_heads][D] unnormalised outputs of cut units
   const f16* kscale;  // 8-bit K/V: fp16 scale per (row, kv head) of keys,
   const f16* vscale;  //   of values (null for fp16 K/V)
   int64_t scale_page; // scale elements between pages,
@@ -112,7 +112,7 @@ constexpr int next_pow2(int x) {
 // 16-byte aligned); pairs at or past the real head dim are not loaded and
 // read as zero. p.v runs on FMAs.
 //
-// Matrix-core kernels (MF, a GQA group of 8 or more query heads): a step is
+// Matrix-core kernels (MF, a GQA group of 5 or more query heads): a step is
 // 16 keys; lane l loads key l % 16, elements [32 c + 8 (l / 16), + 8) of
 // each 32-element chunk c (NV = D / 32 chunks, one 16-byte load each for K
 // and for V), the A operand of v_mfma_f32_16x16x32 as it lands.
@@ -366,7 +366,7 @@ __device__ void build_prefix(const Params& p, int* s_prefix, int* s_len) {
 // 16-bit buffers are addressed as fp16 storage and reinterpreted: q.k and
 // p.v run on bf16 v_dot2, the probabilities are rounded to bf16 for p.v.
 // GEN: generic kernel for a head dim p.head_dim below the padded D (Geom).
-// MF: matrix-core kernel for a GQA group of 8 to 16 query heads per unit
+// MF: matrix-core kernel for a GQA group of 5 to 16 query heads per unit
 // (G = 16 slots, p.unit_heads real heads; see mf_step).
 template <int D, int G, bool Q8, bool BF, bool GEN, bool MF>
 __global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(2)))
@@ -1372,7 +1372,7 @@ KernelPair kernels_q8(int d, int g);
 KernelPair kernels_gen_f16(int dp, int g);
 KernelPair kernels_gen_bf16(int dp, int g);
 KernelPair kernels_gen_q8(int dp, int g);
-// Matrix-core kernels (8 to 16 query heads per unit): head dims 64, 96,
+// Matrix-core kernels (5 to 16 query heads per unit): head dims 64, 96,
 // 128, 256 in fp16 and bf16.
 KernelPair kernels_mf(int d, bool bf16);
 

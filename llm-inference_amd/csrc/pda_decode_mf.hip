@@ -1,5 +1,5 @@
 // Matrix-core instantiations of the paged decode kernels (templates in
-// pda_decode.h) for GQA groups of 8 to 16 query heads per unit, in a
+// pda_decode.h) for GQA groups of 5 to 16 query heads per unit, in a
 // translation unit of their own so the build compiles them in parallel.
 #include "pda_decode.h"
 

@@ -100,10 +100,16 @@ def test_workspace_and_plan_are_consistent():
     assert need >= 65 * 4 + slots * 7 * (128 + 2) * 4
     # The workspace does not grow with the context length.
     assert _lib.workspace_bytes(64, 28, 4, 128, 16, 8192, 131072, 0) == need
-    # More than 8 heads per kv head are served by several head groups (8 each).
-    one = _lib.workspace_bytes(2, 8, 1, 128, 16, 64, 1024, 0)
-    two = _lib.workspace_bytes(2, 16, 1, 128, 16, 64, 1024, 0)
-    assert two == one
+    # The partial slots hold one unit's query heads: a 16-head group (one
+    # matrix-core unit) needs twice the partial space of an 8-head one, and
+    # 32 heads (two units of 16) no more than 16.
+    eight = _lib.workspace_bytes(2, 8, 1, 128, 16, 64, 1024, 0)
+    sixteen = _lib.workspace_bytes(2, 16, 1, 128, 16, 64, 1024, 0)
+    thirty_two = _lib.workspace_bytes(2, 32, 1, 128, 16, 64, 1024, 0)
+    one = _lib.workspace_bytes(2, 1, 1, 128, 16, 64, 1024, 0)
+    assert thirty_two == sixteen
+    assert (sixteen - eight) * 7 == (eight - one) * 8  # partial space per head
+    assert sixteen - eight >= slots * 8 * (128 + 2) * 4
 
 
 def test_batch_limit():
