@@ -235,8 +235,12 @@ int pda_decode_merge_bf16(const void* queries, const void* keys, const void* val
  *   key_scales, value_scales  fp16, [arena_rows, kv_heads] beside a row
  *                 arena, [arena_rows / page_size, kv_heads, page_size] beside
  *                 a page-tile arena
- * Any even head_dim up to 512 (64, 128, 256, 512 tuned, the others, 80
- * included, generic); every other argument as for the fp16 call, which
+ * Here K rows are converted exactly to fp16 and each score is multiplied by
+ * its key's scale; V rows are dequantized to fp16(int8 x scale), the value
+ * the reference's gather hands its portable path (paged_kv.py:285-292).
+ * Any even head_dim up to 512 (64, 128, 256 on the matrix cores at any GQA
+ * group, 512 tuned, the others, 80 included, generic); every other
+ * argument as for the fp16 call, which
  * shares the workspace sizing (pda_workspace_bytes). The split and merge
  * passes exist as for fp16; merge with the _q8 entry after a _q8 split. */
 int pda_paged_decode_attention_q8(const void* queries, const void* keys,

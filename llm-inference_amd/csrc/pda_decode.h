@@ -115,7 +115,10 @@ constexpr int next_pow2(int x) {
 // Matrix-core kernels (MF, a GQA group of 5 or more query heads): a step is
 // 16 keys; lane l loads key l % 16, elements [32 c + 8 (l / 16), + 8) of
 // each 32-element chunk c (NV = D / 32 chunks, one 16-byte load each for K
-// and for V), the A operand of v_mfma_f32_16x16x32 as it lands.
+// and for V), the A operand of v_mfma_f32_16x16x32 as it lands. At 8 bits
+// (MF and Q8, D a multiple of 64) chunk c = 2 j + h holds elements
+// [64 j + 16 (l / 16) + 8 h, + 8) instead, so that one 16-byte load brings
+// a lane's int8 elements of two chunks; the queries follow the same order.
 template <int D, bool Q8 = false, bool GEN = false, bool MF = false>
 struct Geom {
   static constexpr int EPL =
@@ -134,10 +137,13 @@ struct Geom {
   // Vector memory loads per step: K and V (fp16); K, the two V pieces and the
   // key scale and the pair's two value scales (8-bit); generic: four pieces
   // of K and of V, plus the key's two scales at 8 bits.
-  static constexpr int LOADS = MF ? 2 * NV : GEN ? (Q8 ? 10 : 8) : Q8 ? 6 : 2 * NV;
-  static_assert(!MF || (D % 32 == 0 && !Q8 && !GEN), "matrix-core kernels: 16-bit, D % 32 == 0");
+  // Matrix-core kernels at 8 bits: NV / 2 pieces of K and of V, the key's
+  // two scales.
+  static constexpr int LOADS = MF ? (Q8 ? NV + 2 : 2 * NV) : GEN ? (Q8 ? 10 : 8) : Q8 ? 6 : 2 * NV;
+  static_assert(!MF || (D % 32 == 0 && !GEN && (!Q8 || D % 64 == 0)),
+                "matrix-core kernels: D % 32 == 0 (8-bit: D % 64 == 0), no generic dims");
   static_assert(D % EPL == 0 && DC % 8 == 0, "head_dim must be a multiple of 8");
-  static_assert(GEN || !Q8 || PV2, "8-bit K/V needs the key-pair p.v layout");
+  static_assert(GEN || MF || !Q8 || PV2, "8-bit K/V needs the key-pair p.v layout");
   static_assert(!GEN || (D >= 8 && D <= 512 && (D & (D - 1)) == 0),
                 "generic kernels pad the head dim to a power of two");
   static_assert(R <= 64, "head_dim too large");
@@ -519,10 +525,13 @@ void paged_decode_kernel(const Params p) {
     f16x8 qb[MF ? NV : 1];
     if constexpr (MF) {
       const bool real = (lane & 15) < hpu;
-      const f16* qp = p.q + ((int64_t)b * p.hq + h0 + (real ? (lane & 15) : 0)) * D + 8 * mg;
+      const f16* qp = p.q + ((int64_t)b * p.hq + h0 + (real ? (lane & 15) : 0)) * D;
 #pragma unroll
-      for (int c = 0; c < NV; ++c)
-        qb[c] = zero_unless(*reinterpret_cast<const f16x8*>(qp + 32 * c), real);
+      for (int c = 0; c < NV; ++c) {
+        // The elements chunk c of the K loads holds (8-bit: two chunks per load).
+        const int e = Q8 ? 64 * (c >> 1) + 16 * mg + 8 * (c & 1) : 32 * c + 8 * mg;
+        qb[c] = zero_unless(*reinterpret_cast<const f16x8*>(qp + e), real);
+      }
     }
 #pragma unroll
     for (int g = 0; g < (MF ? 0 : G); ++g) {
@@ -581,16 +590,17 @@ void paged_decode_kernel(const Params p) {
         : Q8  ? (uint32_t)(kk * p.row_bytes + kvh * p.head_bytes + r * 16)
               : (uint32_t)(kk * p.row_bytes + kvh * p.head_bytes + d0 * 2);
     const uint32_t v_off =
-        GEN   ? lane_off
+        (GEN || MF) ? lane_off
         : Q8  ? (uint32_t)(2 * kp * p.row_bytes + kvh * p.head_bytes + r2 * 8)
         : PV2 ? (uint32_t)(2 * kp * p.row_bytes + kvh * p.head_bytes + r2 * 16)
               : lane_off;
     // 8-bit scales, in elements from the step's first key: this lane's key,
     // and its pair's keys with this lane's own key first (generic kernels:
     // this lane's key for both).
-    const uint32_t ks_off = (uint32_t)(kvh * p.scale_head + kk * p.scale_row);
+    const uint32_t ks_off = (uint32_t)(kvh * p.scale_head + lk * p.scale_row);
     const uint32_t vs_own =
-        GEN ? ks_off : (uint32_t)(kvh * p.scale_head + (2 * kp + (hi ? 1 : 0)) * p.scale_row);
+        (GEN || MF) ? ks_off
+                    : (uint32_t)(kvh * p.scale_head + (2 * kp + (hi ? 1 : 0)) * p.scale_row);
     const uint32_t vs_other = (uint32_t)(kvh * p.scale_head + (2 * kp + (hi ? 0 : 1)) * p.scale_row);
     // Generic kernels: byte offsets of this lane's four element pairs in a
     // row; pairs past the head dim read pair 0 (in bounds, multiplied by a
@@ -723,6 +733,17 @@ void paged_decode_kernel(const Params p) {
           kb[u][0] = __builtin_bit_cast(f16x8, kw);
           vb[u][0] = __builtin_bit_cast(f16x8, vw);
         }
+      } else if constexpr (MF && Q8) {
+        // 16 int8 elements (two chunks) of this lane's key per load, K and
+        // V of the same key, and that key's two scales.
+#pragma unroll
+        for (int j = 0; j < NV / 2; ++j) {
+          kb[u][j] = *reinterpret_cast<const f16x8*>(kq + 64 * j);
+          vb[u][j] = *reinterpret_cast<const f16x8*>(vq + last_dk * rb + 64 * j);
+        }
+        const int so = last_dk * p.scale_row;
+        ksb[u] = p.kscale[last_soff + ks_off + so];
+        vs_own_b[u] = p.vscale[last_soff + vs_own + so];
       } else if constexpr (Q8) {
         kb[u][0] = *reinterpret_cast<const f16x8*>(kq);
         const uint2 va = *reinterpret_cast<const uint2*>(vq + last_dv0 * rb);
@@ -749,20 +770,64 @@ void paged_decode_kernel(const Params p) {
       f16x8(&kd)[NV] = kb[u];
       f16x8(&vd)[NV] = vb[u];
       if constexpr (MF) {
+        // 8-bit: K and V chunks converted exactly to fp16 (int8 pieces of
+        // two chunks per load); V rows times their scale, rounded to fp16
+        // as the reference's gather does (paged_kv.py:285-292).
+        f16x8 kc[NV], vc[NV];
+        if constexpr (Q8) {
+          const f16x2 vsc = {vs_own_b[u], vs_own_b[u]};
+#pragma unroll
+          for (int j = 0; j < NV / 2; ++j) {
+            const i32x4 kr = __builtin_bit_cast(i32x4, kd[j]);
+            const i32x4 vr8 = __builtin_bit_cast(i32x4, vd[j]);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              f16x2 kq2[4], vq2[4];
+#pragma unroll
+              for (int w2 = 0; w2 < 2; ++w2) {
+                const uint32_t kf = (uint32_t)kr[2 * h + w2] ^ 0x80808080u;
+                const uint32_t vf = (uint32_t)vr8[2 * h + w2] ^ 0x80808080u;
+                kq2[2 * w2] = bytes_to_f16x2(kf, 0x04010400u);
+                kq2[2 * w2 + 1] = bytes_to_f16x2(kf, 0x04030402u);
+                vq2[2 * w2] = bytes_to_f16x2(vf, 0x04010400u) * vsc;
+                vq2[2 * w2 + 1] = bytes_to_f16x2(vf, 0x04030402u) * vsc;
+              }
+              kc[2 * j + h] = f16x8{kq2[0][0], kq2[0][1], kq2[1][0], kq2[1][1],
+                                    kq2[2][0], kq2[2][1], kq2[3][0], kq2[3][1]};
+              vc[2 * j + h] = f16x8{vq2[0][0], vq2[0][1], vq2[1][0], vq2[1][1],
+                                    vq2[2][0], vq2[2][1], vq2[3][0], vq2[3][1]};
+            }
+          }
+        } else {
+#pragma unroll
+          for (int c = 0; c < NV; ++c) {
+            kc[c] = kd[c];
+            vc[c] = vd[c];
+          }
+        }
         // S^T = K Q^T over the step's 16 keys on the matrix cores: this
         // lane holds keys 4 mg .. 4 mg + 3 of head lane % 16.
         f32x4 sacc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int c = 0; c < NV; ++c) sacc = mfma_k32<BF>(kd[c], qb[c], sacc);
+        for (int c = 0; c < NV; ++c) sacc = mfma_k32<BF>(kc[c], qb[c], sacc);
+        // 8-bit: each score times its key's scale (metal_kernels.py:52
+        // KEY_SCALE); lane k % 16 loaded the scale of key k.
+        float ksc[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+        if constexpr (Q8) {
+          const float own = (float)ksb[u];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) ksc[e] = __shfl(own, 4 * mg + e);
+        }
         const int lim = min(len, t0 + s_kin[u]);
         float sr[4], x[4];  // scores in log2 units, and minus the running max
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
+          const float raw = Q8 ? sacc[e] * ksc[e] : sacc[e];
           if (p.softcap > 0.0f) {
-            const float ex = __builtin_amdgcn_exp2f(sacc[e] * p.cap_in);
+            const float ex = __builtin_amdgcn_exp2f(raw * p.cap_in);
             sr[e] = (1.0f - 2.0f * __builtin_amdgcn_rcpf(ex + 1.0f)) * p.cap_out;
           } else {
-            sr[e] = sacc[e] * p.scale_log2;
+            sr[e] = raw * p.scale_log2;
           }
           x[e] = sr[e] - m[0];
         }
@@ -781,7 +846,7 @@ void paged_decode_kernel(const Params p) {
           if (!__any(any)) return;
           const bool vok = t0 + lk >= first && t0 + lk < lim;
 #pragma unroll
-          for (int c = 0; c < NV; ++c) vd[c] = zero_unless(vd[c], vok);
+          for (int c = 0; c < NV; ++c) vc[c] = zero_unless(vc[c], vok);
         }
         if (__any(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])) > kSlack)) {
           // Rare: raise each head's running max to its largest score of
@@ -820,8 +885,10 @@ void paged_decode_kernel(const Params p) {
         // these reads).
         f16* const vt = s_vt + w * 16 * kVRow;
 #pragma unroll
-        for (int c = 0; c < NV; ++c)
-          *reinterpret_cast<f16x8*>(vt + lk * kVRow + 32 * c + 8 * mg) = vd[c];
+        for (int c = 0; c < NV; ++c) {
+          const int e = Q8 ? 64 * (c >> 1) + 16 * mg + 8 * (c & 1) : 32 * c + 8 * mg;
+          *reinterpret_cast<f16x8*>(vt + lk * kVRow + e) = vc[c];
+        }
         const f16* const vr = vt + (4 * mg + ((lane & 15) >> 2)) * kVRow + 4 * (lane & 3);
 #pragma unroll
         for (int i = 0; i < D / 16; ++i) ob[i] = mfma_k16<BF>(read_tr(vr + 16 * i), pb, ob[i]);
@@ -1373,8 +1440,9 @@ KernelPair kernels_gen_f16(int dp, int g);
 KernelPair kernels_gen_bf16(int dp, int g);
 KernelPair kernels_gen_q8(int dp, int g);
 // Matrix-core kernels (5 to 16 query heads per unit): head dims 64, 96,
-// 128, 256 in fp16 and bf16.
+// 128, 256 in fp16 and bf16; 64, 128, 256 over 8-bit K/V.
 KernelPair kernels_mf(int d, bool bf16);
+KernelPair kernels_mf_q8(int d);
 
 }  // namespace pda_decode
 

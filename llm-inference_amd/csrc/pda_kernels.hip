@@ -154,24 +154,30 @@ int heads_per_group(int gtot) {
   return 1;
 }
 
-// Matrix-core kernels: 16-bit K/V, head dims whose rows split into 32-element
-// chunks, and GQA groups of at least mf_min_group() heads (5; the
-// PDA_MFMA_MIN_GROUP environment variable moves it, for measurements). From
-// 5 heads on, the VALU's q.k and p.v issue of the 8-wave workgroup costs
-// more than the matrix cores' 16-head tiles with idle head slots (config 2's
-// lengths, D 64 to 256); at 4 heads and fewer the VALU kernels are faster.
-bool mf_dim(int d) { return d == 64 || d == 96 || d == 128 || d == 256; }
-
-int mf_min_group() {
-  static const int value = [] {
-    const char* env = getenv("PDA_MFMA_MIN_GROUP");
-    const int v = env ? atoi(env) : 0;
-    return v > 0 ? v : 5;
-  }();
-  return value;
+// Matrix-core kernels: head dims whose rows split into 32-element chunks
+// (64-element ones at 8 bits), and GQA groups of at least mf_min_group(q8)
+// heads (the PDA_MFMA_MIN_GROUP environment variable moves both thresholds,
+// for measurements). 16-bit K/V: from 5 heads on, the VALU's q.k and p.v
+// issue of the 8-wave workgroup costs more than the matrix cores' 16-head
+// tiles with idle head slots (config 2's lengths, D 64 to 256); at 4 heads
+// and fewer the VALU kernels are faster. 8-bit K/V: the VALU kernels spend
+// most of their issue on the int8 conversions, which the matrix-core kernel
+// does once per element for all heads; it is level or faster at every group
+// size measured (1 to 7 heads, configs 1-5: config 2 114.7 -> 74.1 us).
+bool mf_dim(int d, bool q8) {
+  return q8 ? (d == 64 || d == 128 || d == 256) : (d == 64 || d == 96 || d == 128 || d == 256);
 }
 
-bool use_mf(int gtot, int d, bool q8) { return !q8 && mf_dim(d) && gtot >= mf_min_group(); }
+int mf_min_group(bool q8) {
+  static const int env = [] {
+    const char* e = getenv("PDA_MFMA_MIN_GROUP");
+    return e ? atoi(e) : 0;
+  }();
+  if (env > 0) return env;
+  return q8 ? 1 : 5;
+}
+
+bool use_mf(int gtot, int d, bool q8) { return mf_dim(d, q8) && gtot >= mf_min_group(q8); }
 
 // Heads per unit on the matrix cores: the whole group when it has at most 16
 // heads (one K/V read serves them all), else the largest divisor that does.
@@ -221,7 +227,9 @@ int make_plan(int32_t batch, int32_t q_heads, int32_t kv_heads, int32_t head_dim
   pl.nhg = gtot / pl.unit_heads;
   // The workspace holds the widest slot layout either cache type could use
   // for this shape (pda_workspace_bytes does not know the element type).
-  const int g_ws = use_mf(gtot, head_dim, false) ? mf_unit_heads(gtot) : heads_per_group(gtot);
+  const int g_ws = std::max(
+      use_mf(gtot, head_dim, false) ? mf_unit_heads(gtot) : heads_per_group(gtot),
+      use_mf(gtot, head_dim, true) ? mf_unit_heads(gtot) : heads_per_group(gtot));
   if ((int64_t)kv_heads * pl.nhg > 65535)
     return fail(PDA_ERR_INVALID_ARGUMENT, "kv heads x head groups above 65535");
   // Visible pages of one sequence are bounded by the table width and, with a
@@ -422,7 +430,8 @@ int decode(int passes, const void* queries, const void* keys, const void* values
       return fail(PDA_ERR_ALIGNMENT, "workspace must be 256-byte aligned");
   }
 
-  const KernelPair kp = pl.mf ? kernels_mf(head_dim, bf16) : kernels_for(head_dim, pl.G, q8, bf16);
+  const KernelPair kp = pl.mf ? (q8 ? kernels_mf_q8(head_dim) : kernels_mf(head_dim, bf16))
+                              : kernels_for(head_dim, pl.G, q8, bf16);
   if (!kp.split) return fail(PDA_ERR_HEAD_DIM, "head_dim %d has no kernel", head_dim);
   const size_t lds = (size_t)(2 * batch + 1) * sizeof(int32_t);
   const int groups = resident_groups(kp.split, lds);

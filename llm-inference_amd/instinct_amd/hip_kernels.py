@@ -75,7 +75,9 @@ def _given_workspace(ws: torch.Tensor, device: torch.device, nbytes: int) -> tor
 
 
 _FAST_DIMS = {16: (64, 80, 96, 128, 256, 512), 8: (64, 128, 256, 512)}
-_MF_DIMS = (64, 96, 128, 256)  # matrix-core kernels (16-bit K/V, 5+ heads per kv head)
+# Matrix-core kernels by K/V bits: head dims, and the fewest heads per kv head.
+_MF_DIMS = {16: (64, 96, 128, 256), 8: (64, 128, 256)}
+_MF_MIN_GROUP = {16: 5, 8: 1}
 
 
 def decode_kernel_names(q_heads: int, kv_heads: int, head_dim: int, *, bits: int = 16,
@@ -87,8 +89,8 @@ def decode_kernel_names(q_heads: int, kv_heads: int, head_dim: int, *, bits: int
     it, the query heads one unit serves and the units per kv head (each
     reads the kv head's K/V once)."""
     group = q_heads // kv_heads
-    min_mf = int(os.environ.get("PDA_MFMA_MIN_GROUP", "0") or 0) or 5
-    mf = bits == 16 and head_dim in _MF_DIMS and group >= min_mf
+    min_mf = int(os.environ.get("PDA_MFMA_MIN_GROUP", "0") or 0) or _MF_MIN_GROUP[bits]
+    mf = head_dim in _MF_DIMS[bits] and group >= min_mf
     cap = 16 if mf else 8
     heads = next(g for g in range(min(group, cap), 0, -1) if group % g == 0)
     generic = head_dim not in _FAST_DIMS[bits]

@@ -93,8 +93,9 @@ def test_config2_shape_reduced(gpu, layout):
 def test_reference_kernel_shapes(gpu, layout, q_heads, kv_heads, head_dim, lengths, window,
                                  softcap):
     """The reference's bits=8 kernel-test shapes (test_mlx_engine.py:422-431;
-    head_dim 80 and 4 have no 8-bit kernel) plus config 1's and config 2's
-    head shapes, with a softcap."""
+    head_dim 80 and 4 run the generic kernels, tests/test_gpu_shapes.py) plus
+    config 1's and config 2's head shapes (the matrix-core kernels), with a
+    softcap."""
     w = workloads.reference_test_case(q_heads, kv_heads, head_dim, lengths, window, softcap,
                                       device=gpu)
     check(Quantized(w, layout), f"q8 {q_heads}/{kv_heads} D{head_dim} {layout}")
@@ -127,6 +128,78 @@ def test_split_and_merge_passes_and_call_to_call(gpu):
     d = (out.float() - whole.float()).abs()
     assert d.max().item() <= MAX_ABS and d.mean().item() <= MEAN_ABS
     check(qw, "q8 split pages=4", split_pages=4)
+
+
+# ---------------------------------------------------------------------------
+# 8-bit K/V on the matrix cores: GQA groups of 5 or more heads at head dims
+# 64, 128, 256 (int8 rows converted in registers, scores times the key
+# scale, V rows dequantized to fp16 into the LDS tile).
+
+from instinct_amd.hip_kernels import decode_kernel_names  # noqa: E402
+
+
+def mf_case(gpu, q_heads, kv_heads, head_dim, lengths, page=16, window=0, softcap=0.0, seed=0):
+    rng = np.random.default_rng(seed)
+    need = [max(0, -(-n // page)) for n in lengths]
+    arena = sum(need) + 3
+    order = rng.permutation(arena)
+    tables = np.zeros((len(lengths), max(1, max(need))), dtype=np.int32)
+    c = 0
+    for b, k in enumerate(need):
+        tables[b, :k] = order[c:c + k]
+        c += k
+    return workloads.build(f"mfq8-{q_heads}/{kv_heads}/{head_dim}", lengths=lengths,
+                           tables=tables, arena_pages=arena, q_heads=q_heads,
+                           kv_heads=kv_heads, head_dim=head_dim, page_size=page,
+                           scale=head_dim ** -0.5, window=window, softcap=softcap,
+                           device=gpu, seed=seed + 1)
+
+
+@pytest.mark.parametrize("head_dim", [64, 128, 256])
+@pytest.mark.parametrize("q_heads,kv_heads", [(5, 1), (7, 1), (8, 1), (11, 1), (16, 2),
+                                              (24, 2), (28, 4)])
+def test_matrix_cores_group_sizes(gpu, q_heads, kv_heads, head_dim):
+    names = decode_kernel_names(q_heads, kv_heads, head_dim, bits=8)
+    assert names["matrix_cores"], names
+    w = mf_case(gpu, q_heads, kv_heads, head_dim, [1, 15, 16, 17, 700, 2500, 33],
+                seed=q_heads * 10 + head_dim)
+    for layout in ("pages", "rows"):
+        qw = Quantized(w, layout)
+        check(qw, f"mf q8 {q_heads}/{kv_heads} D{head_dim} {layout}")
+        check(qw, f"mf q8 {q_heads}/{kv_heads} D{head_dim} {layout} fixed", deterministic=True)
+
+
+@pytest.mark.parametrize("page", [1, 5, 12, 24, 64])
+def test_matrix_cores_page_sizes(gpu, page):
+    """Pages that are not a multiple of the 16-key step: the last step of a
+    page moves its rows back inside the page and masks the duplicates."""
+    w = mf_case(gpu, 14, 2, 128, [1, page, page + 1, 777, 1500], page=page, seed=page)
+    for layout in ("pages", "rows"):
+        check(Quantized(w, layout), f"mf q8 page {page} {layout}")
+
+
+@pytest.mark.parametrize("layout", ["pages", "rows"])
+def test_matrix_cores_window_poison_softcap(gpu, layout):
+    """Rows before the window hold NaN key scales and inf value scales; the
+    masked keys' values are zeroed after dequantization, so nothing leaks."""
+    P, W = 16, 300
+    lengths = [1200, 301, 299, 4000, 9]
+    w = mf_case(gpu, 24, 2, 128, lengths, window=W, softcap=30.0, seed=8)
+    _, _, _, t, n = w.numpy()
+    poison = []
+    for b, length in enumerate(lengths):
+        for pos in range(0, max(0, length - W)):
+            poison.append(int(t[b, pos // P]) * P + pos % P)
+    qw = Quantized(w, layout, poison_rows=np.array(poison, dtype=np.int64))
+    check(qw, f"mf q8 window poison softcap {layout}")
+
+
+def test_matrix_cores_fixed_split_is_bitwise_reproducible(gpu):
+    w = workloads.config2(device=gpu, batch=16, low=512, high=4096)
+    qw = Quantized(w, "pages")
+    first = check(qw, "mf q8 config2 fixed", deterministic=True)
+    for _ in range(3):
+        assert np.array_equal(qw.run(deterministic=True).float().cpu().numpy(), first)
 
 
 # ---------------------------------------------------------------------------
