@@ -87,13 +87,19 @@ template <typename E>
 __device__ __forceinline__ void rotate_head(const E* src, E* dst, float pos,
                                             const float* inv_freq, int half, int d,
                                             int lane) {
+  // No fused multiply-add: the products are rounded before the sum, as in the
+  // reference's float32 expression (device code contracts x * y - z by default,
+  // into a multiply-add that may even round straight to the 16-bit result;
+  // the pragma covers the expressions written here, not those inside library
+  // helpers such as __fmul_rn).
+#pragma clang fp contract(off)
   for (int j = lane; j < half; j += 64) {
     const float x1 = (float)src[j];
     const float x2 = (float)src[j + half];
     float s, c;
-    sincosf(__fmul_rn(pos, inv_freq[j]), &s, &c);
-    dst[j] = (E)__fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, s));
-    dst[j + half] = (E)__fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, s));
+    sincosf(pos * inv_freq[j], &s, &c);
+    dst[j] = (E)(x1 * c - x2 * s);
+    dst[j + half] = (E)(x2 * c + x1 * s);
   }
   for (int e = 2 * half + lane; e < d; e += 64) dst[e] = src[e];
 }
@@ -132,14 +138,14 @@ constexpr int kMaxPerLane = kMaxHeadDim / 64;  // elements of a row per lane
 // reading the element and its rotation partner.
 __device__ __forceinline__ f16 rotated(const f16* src, int e, float pos, const float* inv_freq,
                                        int half) {
+#pragma clang fp contract(off)
   if (e >= 2 * half) return src[e];
   const int j = e < half ? e : e - half;
   const float x1 = (float)src[j];
   const float x2 = (float)src[j + half];
   float s, c;
-  sincosf(__fmul_rn(pos, inv_freq[j]), &s, &c);
-  return e < half ? (f16)__fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, s))
-                  : (f16)__fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, s));
+  sincosf(pos * inv_freq[j], &s, &c);
+  return e < half ? (f16)(x1 * c - x2 * s) : (f16)(x2 * c + x1 * s);
 }
 
 // One row of one wave, lane-owned elements e = lane + 64 i, quantized as
