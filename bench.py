@@ -86,6 +86,10 @@ def parse():
                          "prefill bottleneck (docs/benchmarks.md:102-105, roadmap.md:36)")
     ap.add_argument("--wide-heads", default="16/2",
                     help="query/kv heads of the 512-wide legs (a representative shape)")
+    ap.add_argument("--published", default="261840",
+                    help="context length of the reference's published decode workload, "
+                         "timed in the same run ('' = skip): a Gemma 4 global layer, 2 x "
+                         "512-wide bf16 KV heads, one sequence (docs/benchmarks.md:102-110)")
     ap.add_argument("--no-flush", action="store_true", help="skip the flushed pass")
     ap.add_argument("--flushed-only", action="store_true",
                     help="every decode launch follows a cache flush (warmups included, no warm "
@@ -96,6 +100,12 @@ def parse():
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (rocprof counter scale)")
     return ap.parse_args()
+
+
+def merge_shape_of(w):
+    """What the merge launch depends on besides the heads (row slicing)."""
+    return dict(batch=w.batch, longest=w.longest, page_size=w.page_size,
+                table_width=int(w.tables.shape[1]), window=w.window)
 
 
 def time_calls(passes, steps, flush=None):
@@ -377,7 +387,7 @@ def config_leg(cfg, args, flush):
     (ms,), _ = time_calls([call], args.steps, flush)
     med = statistics.median(ms)
     kv_bytes = w.kv_bytes()
-    names = decode_kernel_names(w.q_heads, w.kv_heads, w.head_dim)
+    names = decode_kernel_names(w.q_heads, w.kv_heads, w.head_dim, **merge_shape_of(w))
     leg = {"workload": w.name, "batch": w.batch, "q_heads": w.q_heads,
            "kv_heads": w.kv_heads, "head_dim": w.head_dim, "kv_bytes": kv_bytes,
            "kernel": f"{names['split']} + {names['merge']}",
@@ -386,6 +396,55 @@ def config_leg(cfg, args, flush):
            "pct_hbm_peak": round(100 * kv_bytes / (med * 1e-3) / 1e9 / HBM_PEAK_GBS, 2)}
     if not args.no_cpu:
         leg["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds / 2)
+    del w, out
+    torch.cuda.empty_cache()
+    return leg
+
+
+def published_leg(args, flush):
+    """The reference's one published decode-kernel figure, re-measured here on
+    its own workload: a Gemma 4 global layer (two 512-wide KV heads, bf16)
+    with one sequence at 261,840 tokens. The reference reports ~6.7 ms per
+    layer and "about 320 GB/s" of K/V on an Apple M3 Max (MLX 0.32.2, Metal;
+    docs/benchmarks.md:102-110); K+V of that layer is 1.07 GB, so 6.7 ms is
+    160 GB/s by this file's accounting. The time ratio is the comparable
+    figure. Caches flushed between calls (the arena is 4x the last-level
+    cache anyway)."""
+    import torch
+
+    from instinct_amd import workloads
+    from instinct_amd.hip_kernels import decode_kernel_names, paged_decode_attention
+
+    hq, _ = (int(x) for x in args.wide_heads.split("/"))
+    w = workloads.gemma4_global(device=torch.device("cuda:0"), length=int(args.published),
+                                q_heads=hq).to_layout(args.layout)
+    out = torch.empty_like(w.q)
+
+    def call():
+        paged_decode_attention(w.q, w.keys, w.values, w.tables, w.lengths,
+                               page_size=w.page_size, longest=w.longest, scale=w.scale,
+                               out=out, deterministic=args.deterministic)
+
+    for _ in range(args.warmup):
+        call()
+    (ms,), _ = time_calls([call], args.steps, flush)
+    med = statistics.median(ms)
+    kv_bytes = w.kv_bytes()
+    names = decode_kernel_names(w.q_heads, w.kv_heads, w.head_dim, bf16=True,
+                                **merge_shape_of(w))
+    rate = kv_bytes / (med * 1e-3) / 1e9
+    leg = {"workload": w.name, "dtype": "bf16", "batch": w.batch, "q_heads": w.q_heads,
+           "kv_heads": w.kv_heads, "head_dim": w.head_dim, "context": int(args.published),
+           "kv_bytes": kv_bytes, "kernel": f"{names['split']} + {names['merge']}",
+           "us_median": round(med * 1e3, 2), "us_mean": round(statistics.fmean(ms) * 1e3, 2),
+           "GB_per_s": round(rate, 2), "pct_hbm_peak": round(100 * rate / HBM_PEAK_GBS, 2)}
+    if int(args.published) == 261840:
+        leg["reference_published"] = {
+            "ms_per_layer": 6.7, "GB_per_s_as_published": 320,
+            "GB_per_s_same_accounting": round(kv_bytes / 6.7e-3 / 1e9, 1),
+            "hardware": "Apple M3 Max (128 GB), MLX 0.32.2, Metal",
+            "source": "docs/benchmarks.md:102-110"}
+        leg["time_ratio_vs_published"] = round(6.7 / med, 1)
     del w, out
     torch.cuda.empty_cache()
     return leg
@@ -546,7 +605,7 @@ def main():
     waves, _ = _lib.plan(w.batch, w.q_heads, w.kv_heads, w.head_dim, w.page_size,
                          int(w.tables.shape[1]), w.longest, w.window, args.split_pages)
     names = decode_kernel_names(w.q_heads, w.kv_heads, w.head_dim, bits=args.kv_bits,
-                                bf16=bf16)
+                                bf16=bf16, split_pages=args.split_pages, **merge_shape_of(w))
     traffic_key = (f"{w.name}/{w.layout}/{'bf16' if bf16 else 'f16'}/kv{args.kv_bits}"
                    f"{'/fixed' if args.deterministic else ''}")
     traffic = None
@@ -612,6 +671,8 @@ def main():
     if args.kv_bits == 16 and not bf16:
         line["other_configs"] = {str(c): config_leg(c, args, flushing)
                                  for c in others if c != args.config}
+    if args.published and args.kv_bits == 16:
+        line["published_workload"] = published_leg(args, flushing)
 
     # The step before the attention call: RoPE of the new queries and keys and
     # the K/V append (one launch), timed alone and followed by the call (one

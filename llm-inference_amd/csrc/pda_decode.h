@@ -49,6 +49,8 @@ constexpr int kSlots = 2 * kMaxWaves;          // partial slots: first and last 
 constexpr int kMinPagesPerWave = 1;            // default: spread no thinner than this
 constexpr int kMaxBatch = 8184;                // per-sequence tables in LDS: (2B + 1) ints
 constexpr int kMergeMaxWaves = 16;             // waves per merge workgroup, at most
+constexpr int kMergeSlicedMaxGroups = 4096;    // row-sliced merge grids, at most
+constexpr int kMergeSlicedRound = 64;          // candidates of a row-sliced merge wave's round
 
 struct Params {
   const f16* q;
@@ -1268,21 +1270,60 @@ void paged_decode_kernel(const Params p) {
   if (!back && lane == 0) p.meet[pair] = taken;
 }
 
-// Merge kernel (metal_kernels.py:103-124): one workgroup of MW waves per
-// (sequence, kv head group, head of the group). The unit's pages [s, e) of
+// The pieces of one unit for the merge kernels. The unit's pages [s, e) of
 // the stream lie in the ranges of pairs qa..qb; pair q split its range
 // [X, Xn) at M = X + meet[q] into the first wave's [X, M) and the second
 // wave's [M, Xn). Each of these ranges that meets [s, e) holds one piece of
 // the unit, in slot 0 of that wave if the range starts inside the unit, else
-// in slot 1. A unit with one piece was written by the split kernel, one with
-// no visible page zeroed there. Candidate pieces are numbered 2 (q - qa) +
-// (second wave); wave w takes the batches of kBatch candidates w, w + MW, ...:
-// one lane per candidate reads its pair's meeting point, then the loads of
-// all pieces of the batch go out together and the batch is combined at once
-// against its own maximum with log-sum-exp weights (pieces whose max is -inf
-// hold no visible key and weigh 0; a zero total gives 0, :116,122). Batches
-// and waves are folded in a fixed order, so the result does not depend on
-// timing.
+// in slot 1. Candidate pieces are numbered 2 (q - qa) + (second wave).
+struct UnitPieces {
+  int64_t s = 0, e = 0, total = 0;
+  int pairs = 0, qa = 0, cand = 0;
+
+  // Slot of candidate j, or -1 when that wave's range misses the unit.
+  __device__ __forceinline__ int slot(const Params& p, int j) const {
+    const int q = qa + (j >> 1);
+    const int64_t X = range_start(q, total, pairs);
+    const int64_t Xn = range_start(q + 1, total, pairs);
+    const int64_t M = X + p.meet[q];
+    if ((j & 1) == 0)
+      return X < M && X < e && M > s ? 2 * (2 * q) + (X >= s ? 0 : 1) : -1;
+    return M < Xn && M < e && Xn > s ? 2 * (2 * q + 1) + (M >= s ? 0 : 1) : -1;
+  }
+};
+
+// The pieces of unit kvg of sequence b; false when the split kernel already
+// wrote the output (no visible page: zeros; one piece: that wave's result).
+__device__ __forceinline__ bool unit_pieces(const Params& p, int b, int kvg, int lane,
+                                            UnitPieces& u) {
+  const int nkvg = p.hkv * p.nhg;
+  const int pb0 = p.prefix[b];
+  const int npg = p.prefix[b + 1] - pb0;
+  if (npg == 0) return false;
+  u.total = (int64_t)p.prefix[p.batch] * nkvg;
+  u.pairs = stream_pairs(u.total, p);
+  u.s = (int64_t)pb0 * nkvg + (int64_t)kvg * npg;
+  u.e = u.s + npg;
+  u.qa = pair_of(u.s, u.total, u.pairs);
+  u.cand = 2 * (pair_of(u.e - 1, u.total, u.pairs) - u.qa + 1);
+  if (u.cand == 2) {
+    // Inside one pair's range: a single piece means one wave held the whole
+    // unit and wrote it.
+    const int sl = lane < 2 ? u.slot(p, lane) : -1;
+    if (__popcll(__ballot(sl >= 0)) <= 1) return false;
+  }
+  return true;
+}
+
+// Merge kernel (metal_kernels.py:103-124): one workgroup of MW waves per
+// (sequence, kv head group, head of the group) combines the unit's pieces
+// (UnitPieces). Wave w takes the batches of kBatch candidates w, w + MW,
+// ...: one lane per candidate reads its pair's meeting point, then the
+// loads of all pieces of the batch go out together and the batch is
+// combined at once against its own maximum with log-sum-exp weights (pieces
+// whose max is -inf hold no visible key and weigh 0; a zero total gives 0,
+// :116,122). Batches and waves are folded in a fixed order, so the result
+// does not depend on timing.
 template <int D, int G, bool BF, bool GEN>
 __global__ __launch_bounds__(kMergeMaxWaves * 64) void paged_decode_merge_kernel(const Params p) {
   constexpr int kChunks = (D + 63) / 64;  // elements l, l + 64, ... of lane l
@@ -1301,40 +1342,15 @@ __global__ __launch_bounds__(kMergeMaxWaves * 64) void paged_decode_merge_kernel
   const int h = kvh * p.gtot + (kvg - kvh * p.nhg) * uh + g;
   const int hd = GEN ? p.head_dim : D;  // output row length (partials are D apart)
   f16* const dst = p.out + ((int64_t)b * p.hq + h) * hd;
-  const int nkvg = p.hkv * p.nhg;
-  const int pb0 = p.prefix[b];
-  const int npg = p.prefix[b + 1] - pb0;
-  if (npg == 0) return;  // zeroed by the split kernel
-  const int64_t total = (int64_t)p.prefix[p.batch] * nkvg;
-  const int pairs = stream_pairs(total, p);
-  const int64_t s = (int64_t)pb0 * nkvg + (int64_t)kvg * npg;
-  const int64_t e = s + npg;
-  const int qa = pair_of(s, total, pairs);
-  const int qb = pair_of(e - 1, total, pairs);
-  const int cand = 2 * (qb - qa + 1);
-
-  // Slot of candidate j, or -1 when that wave's range misses the unit.
-  auto piece_slot = [&](int j) -> int {
-    const int q = qa + (j >> 1);
-    const int64_t X = range_start(q, total, pairs);
-    const int64_t Xn = range_start(q + 1, total, pairs);
-    const int64_t M = X + p.meet[q];
-    if ((j & 1) == 0)
-      return X < M && X < e && M > s ? 2 * (2 * q) + (X >= s ? 0 : 1) : -1;
-    return M < Xn && M < e && Xn > s ? 2 * (2 * q + 1) + (M >= s ? 0 : 1) : -1;
-  };
-  if (cand == 2) {
-    // Inside one pair's range: a single piece means one wave held the whole
-    // unit and wrote it.
-    const int sl = lane < 2 ? piece_slot(lane) : -1;
-    if (__popcll(__ballot(sl >= 0)) <= 1) return;
-  }
+  UnitPieces up;
+  if (!unit_pieces(p, b, kvg, lane, up)) return;
+  const int cand = up.cand;
 
   float top = -INFINITY, sum = 0.0f, acc[kChunks];
 #pragma unroll
   for (int c = 0; c < kChunks; ++c) acc[c] = 0.0f;
   for (int base = w * kBatch; base < cand; base += mw * kBatch) {
-    const int mine = lane < kBatch && base + lane < cand ? piece_slot(base + lane) : -1;
+    const int mine = lane < kBatch && base + lane < cand ? up.slot(p, base + lane) : -1;
     int sl[kBatch];
     float2 ml[kBatch];
     float part[kBatch][kChunks];
@@ -1399,6 +1415,123 @@ __global__ __launch_bounds__(kMergeMaxWaves * 64) void paged_decode_merge_kernel
     }
 }
 
+// Row-sliced merge: the same combination, with the workgroups of one head
+// each taking one 64-element slice of its row (blockIdx.x = head x slices +
+// slice), for calls with few heads and many pieces each (a few long
+// sequences), where one workgroup per head would leave most CUs idle and
+// read whole rows on the few it has. A wave's round takes kRound
+// candidates: lane j reads candidate j's meeting point and (max, sum); the
+// pieces' slices are read with 16-byte loads, four pieces per load (lanes
+// 16 i .. 16 i + 15 read piece 4 k + i in load k). The round is weighted
+// against its own maximum; the four lane groups are summed after the last
+// round and the waves folded in a fixed order, as in the kernel above.
+template <int D, int G, bool BF, bool GEN>
+__global__ __launch_bounds__(kMergeMaxWaves * 64) void paged_decode_merge_sliced_kernel(
+    const Params p) {
+  constexpr int kSlices = (D + 63) / 64;
+  constexpr int kLoads = kMergeSlicedRound / 4;  // 16-byte loads per lane in a round
+  static_assert(kMergeSlicedRound <= 64 && D % 4 == 0, "one candidate per lane, float4 rows");
+  __shared__ float s_top[kMergeMaxWaves], s_sum[kMergeMaxWaves];
+  __shared__ float4 s_acc[kMergeMaxWaves][16];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = uniform(tid >> 6);
+  const int mw = blockDim.x >> 6;
+  const int uh = p.unit_heads;
+  const int x = blockIdx.x / kSlices;
+  const int kvg = x / uh;
+  const int g = x - kvg * uh;
+  const int b = blockIdx.y;
+  const int kvh = kvg / p.nhg;
+  const int h = kvh * p.gtot + (kvg - kvh * p.nhg) * uh + g;
+  const int hd = GEN ? p.head_dim : D;
+  const int e0 = 64 * (blockIdx.x - x * kSlices) + 4 * (lane & 15);  // this lane's 4 elements
+  const int grp = lane >> 4;
+  UnitPieces up;
+  if (!unit_pieces(p, b, kvg, lane, up)) return;
+  const int cand = up.cand;
+
+  float top = -INFINITY, sum = 0.0f;
+  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  for (int base = w * kMergeSlicedRound; base < cand; base += mw * kMergeSlicedRound) {
+    const int sl = lane < kMergeSlicedRound && base + lane < cand ? up.slot(p, base + lane) : -1;
+    const float2 ml = sl >= 0 ? p.part_ml[(int64_t)sl * uh + g] : make_float2(-INFINITY, 0.0f);
+    float4 part[kLoads];
+#pragma unroll
+    for (int k = 0; k < kLoads; ++k) {
+      const int at = __shfl(sl, 4 * k + grp);
+      part[k] = at >= 0 && e0 < D
+                    ? *reinterpret_cast<const float4*>(p.part_o + ((int64_t)at * uh + g) * D + e0)
+                    : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    const float bt = wave_max(ml.x);
+    if (bt == -INFINITY) continue;  // no visible key in this round
+    const float wt = sl >= 0 ? __builtin_amdgcn_exp2f(ml.x - bt) : 0.0f;
+    const float bs = group_sum<64>(wt * ml.y);
+    float4 ba = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int k = 0; k < kLoads; ++k) {
+      const float wk = __shfl(wt, 4 * k + grp);
+      ba.x = __builtin_fmaf(wk, part[k].x, ba.x);
+      ba.y = __builtin_fmaf(wk, part[k].y, ba.y);
+      ba.z = __builtin_fmaf(wk, part[k].z, ba.z);
+      ba.w = __builtin_fmaf(wk, part[k].w, ba.w);
+    }
+    const float mn = fmaxf(top, bt);
+    const float fo = __builtin_amdgcn_exp2f(top - mn);  // 0 while top = -inf
+    const float fn = __builtin_amdgcn_exp2f(bt - mn);
+    top = mn;
+    sum = sum * fo + bs * fn;
+    acc.x = acc.x * fo + ba.x * fn;
+    acc.y = acc.y * fo + ba.y * fn;
+    acc.z = acc.z * fo + ba.z * fn;
+    acc.w = acc.w * fo + ba.w * fn;
+  }
+  // The four lane groups hold the same elements of different pieces, all
+  // against the wave's maximum.
+  acc.x += __shfl_xor(acc.x, 16);
+  acc.y += __shfl_xor(acc.y, 16);
+  acc.z += __shfl_xor(acc.z, 16);
+  acc.w += __shfl_xor(acc.w, 16);
+  acc.x += __shfl_xor(acc.x, 32);
+  acc.y += __shfl_xor(acc.y, 32);
+  acc.z += __shfl_xor(acc.z, 32);
+  acc.w += __shfl_xor(acc.w, 32);
+  if (mw > 1) {
+    if (lane == 0) s_top[w] = top;
+    __syncthreads();
+    float all = -INFINITY;
+    for (int i = 0; i < mw; ++i) all = fmaxf(all, s_top[i]);
+    const float f = top == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(top - all);
+    if (lane < 16) s_acc[w][lane] = make_float4(acc.x * f, acc.y * f, acc.z * f, acc.w * f);
+    if (lane == 0) s_sum[w] = sum * f;
+    __syncthreads();
+    if (w != 0) return;
+    sum = 0.0f;
+    acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int i = 0; i < mw; ++i) {
+      sum += s_sum[i];
+      const float4 a = s_acc[i][lane & 15];
+      acc.x += a.x;
+      acc.y += a.y;
+      acc.z += a.z;
+      acc.w += a.w;
+    }
+  }
+  if (lane >= 16) return;
+  const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+  const float o[4] = {acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv};
+  f16* const dst = p.out + ((int64_t)b * p.hq + h) * hd;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    if (e0 + j < hd) {
+      if constexpr (BF)
+        dst[e0 + j] = __builtin_bit_cast(f16, (bf16)o[j]);
+      else
+        dst[e0 + j] = (f16)o[j];
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Instantiations, one translation unit per element type.
 
@@ -1407,11 +1540,13 @@ using KernelFn = void (*)(Params);
 struct KernelPair {
   KernelFn split = nullptr;
   KernelFn merge = nullptr;
+  KernelFn merge_sliced = nullptr;  // one 64-element slice per workgroup
 };
 
 template <int D, int G, bool Q8, bool BF, bool GEN = false, bool MF = false>
 KernelPair make_pair() {
-  return {paged_decode_kernel<D, G, Q8, BF, GEN, MF>, paged_decode_merge_kernel<D, G, BF, GEN>};
+  return {paged_decode_kernel<D, G, Q8, BF, GEN, MF>, paged_decode_merge_kernel<D, G, BF, GEN>,
+          paged_decode_merge_sliced_kernel<D, G, BF, GEN>};
 }
 
 template <int D, bool Q8, bool BF, bool GEN = false>

@@ -275,17 +275,41 @@ int resident_groups(KernelFn fn, size_t lds_bytes) {
   return groups;
 }
 
-// Waves of a merge workgroup: one batch of pieces per wave for the longest
-// unit (its pieces estimated from `longest`).
-int merge_waves(const Plan& pl, int head_dim, int grid_pairs) {
+// Merge launch. Units with many pieces (a few long sequences) take the
+// row-sliced kernel: a workgroup per 64-element slice of a head's row and
+// rounds of 64 pieces per wave, read with 16-byte loads and one (max, sum)
+// load per piece; with one workgroup per head, hundreds of pieces would be
+// read whole-row on a few CUs, 32 pieces or fewer per round, every lane
+// loading each piece's (max, sum). Waves: enough for one round per wave on
+// the longest unit (its pieces estimated from `longest`), 16 at most. `dim`
+// is the kernels' head dim (the partials' row length), `heads` the merge
+// workgroups before slicing.
+struct MergeShape {
+  bool sliced;
+  int slices;  // workgroups per head
+  int waves;   // per workgroup
+};
+
+MergeShape merge_shape(const Plan& pl, int dim, int grid_pairs, int64_t heads) {
   const int64_t pairs = std::max<int64_t>(
       1, std::min<int64_t>(grid_pairs, (pl.pages_est + 2 * pl.min_pages - 1) /
                                            (2 * pl.min_pages)));
   const int64_t per_pair = std::max<int64_t>(1, pl.pages_est / pairs);
   const int64_t pieces = 2 * (pl.unit_pages_max / per_pair + 2);
-  const int batch = 32 / ((head_dim + 63) / 64);
-  const int64_t mw = (pieces + batch - 1) / batch;
-  return (int)std::max<int64_t>(1, std::min<int64_t>(kMergeMaxWaves, mw));
+  const int chunks = (dim + 63) / 64;
+  // PDA_MERGE_SLICED=0/1 forces the choice (for measurements); results
+  // differ only in summation order.
+  static const int force = [] {
+    const char* e = getenv("PDA_MERGE_SLICED");
+    return e && *e ? atoi(e) : -1;
+  }();
+  const bool sliced = force >= 0 ? force > 0
+                                 : pieces > kMergeSlicedRound &&
+                                       heads * chunks <= kMergeSlicedMaxGroups;
+  const int per_round = sliced ? kMergeSlicedRound : 32 / chunks;
+  const int64_t mw = (pieces + per_round - 1) / per_round;
+  return {sliced, sliced ? chunks : 1,
+          (int)std::max<int64_t>(1, std::min<int64_t>(kMergeMaxWaves, mw))};
 }
 
 }  // namespace
@@ -511,10 +535,11 @@ int decode(int passes, const void* queries, const void* keys, const void* values
     err = hipLaunchKernel(reinterpret_cast<const void*>(kp.split), dim3(groups),
                           dim3(kSplitThreads), args, lds, st);
   if (err == hipSuccess && (passes & kPassMerge)) {
-    const int mw = merge_waves(pl, head_dim, prm.grid_pairs);
-    err = hipLaunchKernel(reinterpret_cast<const void*>(kp.merge),
-                          dim3(kv_heads * pl.nhg * pl.unit_heads, batch), dim3(64 * mw), args, 0,
-                          st);
+    const int heads = kv_heads * pl.nhg * pl.unit_heads;
+    const MergeShape ms = merge_shape(pl, pl.mf ? head_dim : kernel_dim(head_dim, q8),
+                                      prm.grid_pairs, (int64_t)heads * batch);
+    err = hipLaunchKernel(reinterpret_cast<const void*>(ms.sliced ? kp.merge_sliced : kp.merge),
+                          dim3(heads * ms.slices, batch), dim3(64 * ms.waves), args, 0, st);
   }
   if (err != hipSuccess)
     return fail(PDA_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(err));

@@ -78,16 +78,48 @@ _FAST_DIMS = {16: (64, 80, 96, 128, 256, 512), 8: (64, 128, 256, 512)}
 # Matrix-core kernels by K/V bits: head dims, and the fewest heads per kv head.
 _MF_DIMS = {16: (64, 96, 128, 256), 8: (64, 128, 256)}
 _MF_MIN_GROUP = {16: 5, 8: 1}
+# Merge launch (csrc/pda_kernels.hip ``merge_shape``) on MI355X: 256 CUs x
+# one split workgroup of four wave pairs; the row-sliced merge for units of
+# more than 64 pieces, in grids of 4096 workgroups at most.
+_GRID_PAIRS = 1024
+_MERGE_SLICED_ROUND = 64
+_MERGE_SLICED_MAX_GROUPS = 4096
+
+
+def _merge_sliced(dim, heads, units, *, batch, longest, page_size, table_width, window,
+                  split_pages) -> bool:
+    """Whether the merge runs row-sliced (one 64-element slice of a head per
+    workgroup): the library's rule, from the same page estimates."""
+    pages_max = table_width
+    if window > 0:
+        pages_max = min(pages_max, (window - 1) // page_size + 2)
+    est = pages_max
+    if longest > 0:
+        est = min(est, -(-longest // page_size) + 1)
+    pages_est = batch * units * est
+    min_pages = split_pages if split_pages > 0 else 1
+    pairs = max(1, min(_GRID_PAIRS, -(-pages_est // (2 * min_pages))))
+    per_pair = max(1, pages_est // pairs)
+    pieces = 2 * (est // per_pair + 2)
+    chunks = -(-dim // 64)
+    force = os.environ.get("PDA_MERGE_SLICED", "")
+    if force:
+        return int(force) > 0
+    return pieces > _MERGE_SLICED_ROUND and batch * heads * chunks <= _MERGE_SLICED_MAX_GROUPS
 
 
 def decode_kernel_names(q_heads: int, kv_heads: int, head_dim: int, *, bits: int = 16,
-                        bf16: bool = False) -> dict[str, Any]:
+                        bf16: bool = False, batch: int = 0, longest: int = 0,
+                        page_size: int = 16, table_width: int = 0, window: int = 0,
+                        split_pages: int = 0) -> dict[str, Any]:
     """The kernels a decode call of this shape launches, as the library's
     dispatch picks them (csrc/pda_kernels.hip ``make_plan``, ``kernels_for``,
-    ``heads_per_group``, ``use_mf``): template arguments ``<D, G, Q8, BF,
-    GEN, MF>`` of the split and merge kernels, whether the matrix cores run
-    it, the query heads one unit serves and the units per kv head (each
-    reads the kv head's K/V once)."""
+    ``heads_per_group``, ``use_mf``, ``merge_shape``): template arguments
+    ``<D, G, Q8, BF, GEN, MF>`` of the split kernel and ``<D, G, BF, GEN>`` of
+    the merge kernel (or its row-sliced form), whether the matrix cores run it, the query
+    heads one unit serves and the units per kv head (each reads the kv
+    head's K/V once). The merge's row slicing depends on the batch, the
+    longest length and the table width (``batch`` 0: not sliced)."""
     group = q_heads // kv_heads
     min_mf = int(os.environ.get("PDA_MFMA_MIN_GROUP", "0") or 0) or _MF_MIN_GROUP[bits]
     mf = head_dim in _MF_DIMS[bits] and group >= min_mf
@@ -96,10 +128,17 @@ def decode_kernel_names(q_heads: int, kv_heads: int, head_dim: int, *, bits: int
     generic = head_dim not in _FAST_DIMS[bits]
     dim = max(8, 1 << (head_dim - 1).bit_length()) if generic else head_dim
     slots = 16 if mf else heads
+    units = kv_heads * (group // heads)
+    sliced = batch > 0 and _merge_sliced(
+        dim, units * heads, units, batch=batch, longest=longest, page_size=page_size,
+        table_width=table_width or -(-max(longest, 1) // page_size), window=window,
+        split_pages=split_pages)
     b = lambda x: str(bool(x)).lower()  # noqa: E731
     targs = f"{dim},{slots},{b(bits == 8)},{b(bf16)},{b(generic)},{b(mf)}"
     return {"split": f"paged_decode_kernel<{targs}>",
-            "merge": f"paged_decode_merge_kernel<{dim},{slots},{b(bf16)},{b(generic)}>",
+            "merge": (f"paged_decode_merge{'_sliced' if sliced else ''}_kernel<{dim},{slots},"
+                      f"{b(bf16)},{b(generic)}>"),
+            "merge_row_sliced": sliced,
             "matrix_cores": mf, "heads_per_unit": heads,
             "head_groups_per_kv_head": group // heads}
 

@@ -291,6 +291,38 @@ def config5(device="cpu", seed=5, batch=256, low=16, high=65536, shared=64,
 CONFIGS = {1: config1, 2: config2, 3: config3, 4: config4, 5: config5}
 
 
+def gemma4_global(device="cpu", seed=6, batch=1, length=261840, q_heads=16, planted=8,
+                  dtype=torch.bfloat16) -> Workload:
+    """The workload of the reference's one published decode-kernel figure
+    (docs/benchmarks.md:102-110): a Gemma 4 global layer, two 512-wide KV
+    heads (gemma4.py:3-5, 49-66), bf16, one sequence at 261,840 tokens,
+    page 16, pages a seeded permutation of an arena that exactly fits.
+    The model attends with scale 1.0 (gemma4.py:161) on normalized
+    queries; here queries are drawn N(0,1)/sqrt(512) so that the logits
+    have unit variance. ``q_heads`` is a representative 16 (group of 8).
+    As in config 3, ``planted`` keys per (sequence, kv head) are multiplied
+    by 8: their logits dominate the softmax, so the output is O(1) rather
+    than an average of ~1/sqrt(length) over the whole context."""
+    rng = np.random.default_rng(seed)
+    P, d = 16, 512
+    lengths = [length] * batch
+    arena = int(sum(math.ceil(n / P) for n in lengths))
+    tables = _permuted_tables(rng, lengths, P, arena)
+    w = build(f"gemma4-global-b{batch}-{length}", lengths=lengths, tables=_pack(tables),
+              arena_pages=arena, q_heads=q_heads, kv_heads=2, head_dim=d, page_size=P,
+              scale=1.0, device=device, seed=seed)
+    for b in range(batch):
+        pos = rng.choice(length, size=(2, planted), replace=True)
+        rows = tables[b][pos // P].astype(np.int64) * P + pos % P
+        for kvh in range(2):
+            w.keys[torch.as_tensor(rows[kvh], device=w.keys.device), kvh] *= 8
+    w.q = (w.q.float() * d ** -0.5).to(dtype)
+    w.keys = w.keys.to(dtype)
+    w.values = w.values.to(dtype)
+    w.meta["planted"] = planted
+    return w
+
+
 # --- the reference's kernel-test shapes -----------------------------------
 
 # tests/test_mlx_engine.py:422-431: (q_heads, kv_heads, head_dim, lengths,

@@ -74,11 +74,12 @@ def attention_plain(q, k, v, *, scale: float, mask=None, softcap: float = 0.0,
     q = np.asarray(q, dtype=dtype)
     k = np.asarray(k, dtype=dtype)
     v = np.asarray(v, dtype=dtype)
-    groups = q.shape[1] // k.shape[1]
-    if groups > 1:
-        k = np.repeat(k, groups, axis=1)
-        v = np.repeat(v, groups, axis=1)
-    scores = (q * scale) @ np.swapaxes(k, -1, -2)
+    batch, heads, count, dim = q.shape
+    hkv = k.shape[1]
+    # Query head h reads kv head h // groups: the group's queries are stacked
+    # as rows of one product per kv head instead of repeating K and V.
+    grouped = (q * scale).reshape(batch, hkv, (heads // hkv) * count, dim)
+    scores = (grouped @ np.swapaxes(k, -1, -2)).reshape(batch, heads, count, -1)
     if softcap:
         scores = np.tanh(scores / softcap) * softcap
     if mask is not None:
@@ -88,7 +89,8 @@ def attention_plain(q, k, v, *, scale: float, mask=None, softcap: float = 0.0,
     weights = np.exp(scores - top)
     total = np.sum(weights, axis=-1, keepdims=True)
     probs = np.divide(weights, total, out=np.zeros_like(weights), where=total > 0)
-    return probs @ v
+    probs = probs.reshape(batch, hkv, (heads // hkv) * count, -1)
+    return (probs @ v).reshape(batch, heads, count, dim)
 
 
 def paged_decode_dense(q, keys, values, tables, lengths, *, page_size: int, scale: float,

@@ -1,0 +1,64 @@
+"""The reference's one published decode-kernel workload at its full size
+(docs/benchmarks.md:102-110): a Gemma 4 global layer, two 512-wide KV heads,
+one sequence at 261,840 tokens (K+V 1.07 GB), bf16 like the model, against
+the float64 oracle. Planted large-logit keys keep the output O(1) so that the
+absolute tolerances mean something (an average over 261,840 values would be
+~1e-2 and hide any error). The fp16 run is held to the north-star tolerance
+(max-abs 2e-3, mean-abs 2e-4)."""
+
+import numpy as np
+import pytest
+import torch
+
+from instinct_amd import workloads
+from instinct_amd.hip_kernels import paged_decode_attention
+from instinct_amd.paged_kv import pages_to_rows
+from oracle import paged_attention as pa
+
+pytestmark = pytest.mark.gpu
+
+TOLERANCE = {torch.bfloat16: (1.6e-2, 1.6e-3), torch.float16: (2e-3, 2e-4)}
+
+
+def call(w, **kw):
+    return paged_decode_attention(w.q, w.keys, w.values, w.tables, w.lengths,
+                                  page_size=w.page_size, longest=w.longest, scale=w.scale, **kw)
+
+
+def oracle(w):
+    keys, values = w.keys, w.values
+    if w.layout == "pages":
+        keys, values = pages_to_rows(keys), pages_to_rows(values)
+    f = lambda t: t.float().cpu().numpy()  # noqa: E731
+    return pa.paged_decode_dense(f(w.q), f(keys), f(values), w.tables.cpu().numpy(),
+                                 w.lengths.cpu().numpy(), page_size=w.page_size, scale=w.scale)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+def test_full_context_matches_oracle(gpu, dtype):
+    w = workloads.gemma4_global(device=gpu, dtype=dtype).to_layout("pages")
+    print(f"gemma4 global {w.name} {dtype}: {w.kv_bytes()} K/V bytes", flush=True)
+    out = call(w)
+    torch.cuda.synchronize()
+    assert out.dtype == dtype
+    got = out.float().cpu().numpy()
+    want = oracle(w)
+    assert np.isfinite(got).all()
+    assert np.abs(want).max() > 1.0  # the planted keys dominate
+    err_max, err_mean = pa.error_stats(got, want)
+    print(f"max_abs={err_max:.3e} mean_abs={err_mean:.3e}", flush=True)
+    max_abs, mean_abs = TOLERANCE[dtype]
+    assert err_max <= max_abs and err_mean <= mean_abs, (err_max, err_mean)
+
+
+def test_full_context_fixed_split_is_reproducible(gpu):
+    w = workloads.gemma4_global(device=gpu).to_layout("pages")
+    first = call(w, deterministic=True)
+    again = [call(w, deterministic=True) for _ in range(3)]
+    torch.cuda.synchronize()
+    for out in again:
+        assert torch.equal(out, first)
+    loose = call(w).float()
+    torch.cuda.synchronize()
+    # The two split plans differ only in summation order.
+    assert (loose - first.float()).abs().max().item() <= 1.6e-2

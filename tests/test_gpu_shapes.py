@@ -279,3 +279,45 @@ def test_fixed_split_8bit_and_bf16_are_reproducible(gpu):
     b = run(wb, deterministic=True)
     for _ in range(3):
         assert torch.equal(run(wb, deterministic=True), b)
+
+
+# --- row-sliced merge: few heads, many pieces each ----------------------------
+
+@pytest.mark.parametrize("q_heads,kv_heads,head_dim,lengths,window", [
+    (8, 1, 128, [40000], 0),
+    (16, 2, 512, [9000, 5], 0),
+    (12, 4, 80, [30000], 0),
+    (6, 2, 130, [20000, 700], 0),
+    (4, 1, 96, [30000], 0),
+    (8, 2, 256, [50000], 30000),
+    (28, 4, 128, [30000], 0),
+])
+def test_row_sliced_merge(gpu, q_heads, kv_heads, head_dim, lengths, window):
+    """One or two long sequences: the merge's workgroups each take one
+    64-element slice of a head's row (a generic head dim's last slices are
+    partly or wholly past it), in fp16, bf16 and with the fixed split."""
+    from instinct_amd.hip_kernels import decode_kernel_names
+
+    w = make(gpu, q_heads=q_heads, kv_heads=kv_heads, head_dim=head_dim, page=16,
+             lengths=lengths, window=window, seed=head_dim + len(lengths))
+    names = decode_kernel_names(q_heads, kv_heads, head_dim, batch=w.batch, longest=w.longest,
+                                table_width=int(w.tables.shape[1]), window=window)
+    assert names["merge_row_sliced"], names
+    check16(w, f"sliced merge {q_heads}/{kv_heads}/D{head_dim}")
+    check_bf16(w.to_layout("pages"), f"sliced merge bf16 {q_heads}/{kv_heads}/D{head_dim}")
+
+
+@pytest.mark.parametrize("q_heads,kv_heads,head_dim,lengths", [
+    (8, 2, 512, [12000]),
+    (8, 1, 80, [20000]),
+    (8, 2, 128, [20000, 9]),
+])
+def test_row_sliced_merge_8bit(gpu, q_heads, kv_heads, head_dim, lengths):
+    from instinct_amd.hip_kernels import decode_kernel_names
+
+    w = make(gpu, q_heads=q_heads, kv_heads=kv_heads, head_dim=head_dim, page=16,
+             lengths=lengths, seed=3 * head_dim)
+    names = decode_kernel_names(q_heads, kv_heads, head_dim, bits=8, batch=w.batch,
+                                longest=w.longest, table_width=int(w.tables.shape[1]))
+    assert names["merge_row_sliced"], names
+    check8(w, f"sliced merge {q_heads}/{kv_heads}/D{head_dim}")
