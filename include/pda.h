@@ -239,7 +239,8 @@ int pda_decode_merge_bf16(const void* queries, const void* keys, const void* val
  * its key's scale; V rows are dequantized to fp16(int8 x scale), the value
  * the reference's gather hands its portable path (paged_kv.py:285-292).
  * Any even head_dim up to 512 (64, 128, 256 on the matrix cores at any GQA
- * group, 512 tuned, the others, 80 included, generic); every other
+ * group, 512 on them from 4 heads per kv head and tuned VALU kernels below,
+ * the others, 80 included, generic); every other
  * argument as for the fp16 call, which
  * shares the workspace sizing (pda_workspace_bytes). The split and merge
  * passes exist as for fp16; merge with the _q8 entry after a _q8 split. */

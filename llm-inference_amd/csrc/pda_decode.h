@@ -40,6 +40,11 @@ constexpr float kSlack = 8.0f;
 constexpr int kSplitWaves = 8;                 // waves per split workgroup
 constexpr int kSplitThreads = kSplitWaves * 64;
 constexpr int kPairs = kSplitWaves / 2;        // wave pairs per workgroup
+// Waves of a split workgroup: eight (two per SIMD), except the matrix-core
+// kernels at D = 512, whose 16 x 512 output accumulators, queries and
+// 32 KiB K/V steps need a whole SIMD's registers per wave (accumulators in
+// AGPRs): four waves, one per SIMD.
+constexpr int split_waves(int d, bool mf) { return mf && d > 256 ? 4 : kSplitWaves; }
 constexpr int kNbuf = 2;                       // K/V steps in flight per wave
 constexpr int kTablePages = 64;                // page-table entries held per VGPR refill
 constexpr int kMaxGroups = 512;                // resident split workgroups (256 CUs x 2)
@@ -377,17 +382,21 @@ __device__ void build_prefix(const Params& p, int* s_prefix, int* s_len) {
 // MF: matrix-core kernel for a GQA group of 5 to 16 query heads per unit
 // (G = 16 slots, p.unit_heads real heads; see mf_step).
 template <int D, int G, bool Q8, bool BF, bool GEN, bool MF>
-__global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ __launch_bounds__(64 * split_waves(D, MF))
+__attribute__((amdgpu_waves_per_eu(split_waves(D, MF) / 4)))
 void paged_decode_kernel(const Params p) {
+  constexpr int kWaves = split_waves(D, MF);  // waves of this workgroup
+  constexpr int kThreads = 64 * kWaves;
+  constexpr int kWgPairs = kWaves / 2;
   static_assert(!(Q8 && BF), "8-bit K/V is dequantized to fp16");
   static_assert(!MF || G == 16, "matrix-core kernels lay 16 head slots out");
   using Gm = Geom<D, Q8, GEN, MF>;
   constexpr int EPL = Gm::EPL, NV = Gm::NV, DC = Gm::DC, R = Gm::R, KPS = Gm::KPS;
   constexpr bool PV2 = Gm::PV2;
   constexpr int OPL = Gm::OPL;
-  // Steps in flight per wave: two; one where a step alone is 16 KiB of K
-  // and V per wave (matrix-core kernels at D = 256), which also keeps those
-  // kernels within 256 registers; four at D >= 256 with at most 2 heads per
+  // Steps in flight per wave: two; one where a step alone is 16 KiB or more
+  // of K and V per wave (matrix-core kernels at D >= 256), which also keeps
+  // those kernels within their registers; four at D >= 256 with at most 2 heads per
   // unit, whose small per-step math leaves registers free (config 4's
   // Gemma-style shape, 42.5 -> 39.7 us; depths 3 and 4 were slower on the
   // other configurations).
@@ -395,10 +404,10 @@ void paged_decode_kernel(const Params p) {
                        : (!MF && !Q8 && !GEN && D >= 256 && G <= 2) ? 4
                                                               : kNbuf;
   extern __shared__ int s_dyn[];
-  __shared__ int s_ticket[kPairs];
+  __shared__ int s_ticket[kWgPairs];
   // Matrix-core kernels: each wave's V tile of one step, [16 keys][kVRow].
   constexpr int kVRow = mf_vrow(D);
-  __shared__ __align__(16) f16 s_vt[MF ? kSplitWaves * 16 * kVRow : 1];
+  __shared__ __align__(16) f16 s_vt[MF ? kWaves * 16 * kVRow : 1];
   const int B = p.batch;
   int* const s_prefix = s_dyn;         // [B + 1]
   int* const s_len = s_dyn + B + 1;    // [B]
@@ -433,28 +442,28 @@ void paged_decode_kernel(const Params p) {
   const int hd = GEN ? p.head_dim : D;
   constexpr int kElem = Q8 ? 1 : 2;  // bytes per K/V element
 
-  if (tid < kPairs) s_ticket[tid] = 0;
-  build_prefix<kSplitThreads>(p, s_prefix, s_len);  // ends with a barrier
+  if (tid < kWgPairs) s_ticket[tid] = 0;
+  build_prefix<kThreads>(p, s_prefix, s_len);  // ends with a barrier
   if (blockIdx.x == 0)
-    for (int i = tid; i <= B; i += kSplitThreads) p.prefix[i] = s_prefix[i];
+    for (int i = tid; i <= B; i += kThreads) p.prefix[i] = s_prefix[i];
   // Sequences with no visible key get zeros (metal_kernels.py:88-90 with a
   // zero sum); workgroup j takes sequences j, j + grid, ...
   for (int bz = blockIdx.x; bz < B; bz += gridDim.x) {
     if (s_prefix[bz + 1] != s_prefix[bz]) continue;
     f16* const dz = p.out + (int64_t)bz * p.hq * hd;
     if constexpr (GEN) {  // rows of an odd number of pairs: 4-byte stores
-      for (int i = tid * 2; i < p.hq * hd; i += kSplitThreads * 2)
+      for (int i = tid * 2; i < p.hq * hd; i += kThreads * 2)
         *reinterpret_cast<uint32_t*>(dz + i) = 0u;
     } else {
-      for (int i = tid * 8; i < p.hq * D; i += kSplitThreads * 8)
+      for (int i = tid * 8; i < p.hq * D; i += kThreads * 8)
         *reinterpret_cast<f16x8*>(dz + i) = f16x8{};
     }
   }
   const int64_t total = (int64_t)s_prefix[B] * nkvg;
   const int npairs = stream_pairs(total, p);
-  const int pl = w % kPairs;
-  const bool back = w >= kPairs;  // takes its pair's range from the end
-  const int pair = blockIdx.x * kPairs + pl;
+  const int pl = w % kWgPairs;
+  const bool back = w >= kWgPairs;  // takes its pair's range from the end
+  const int pair = blockIdx.x * kWgPairs + pl;
   if (pair >= npairs) return;
   const int64_t x0 = range_start(pair, total, npairs);
   const int n_range = (int)(range_start(pair + 1, total, npairs) - x0);
@@ -1541,12 +1550,13 @@ struct KernelPair {
   KernelFn split = nullptr;
   KernelFn merge = nullptr;
   KernelFn merge_sliced = nullptr;  // one 64-element slice per workgroup
+  int split_waves = kSplitWaves;    // waves of a split workgroup
 };
 
 template <int D, int G, bool Q8, bool BF, bool GEN = false, bool MF = false>
 KernelPair make_pair() {
   return {paged_decode_kernel<D, G, Q8, BF, GEN, MF>, paged_decode_merge_kernel<D, G, BF, GEN>,
-          paged_decode_merge_sliced_kernel<D, G, BF, GEN>};
+          paged_decode_merge_sliced_kernel<D, G, BF, GEN>, split_waves(D, MF)};
 }
 
 template <int D, bool Q8, bool BF, bool GEN = false>
@@ -1578,6 +1588,10 @@ KernelPair kernels_gen_q8(int dp, int g);
 // 128, 256 in fp16 and bf16; 64, 128, 256 over 8-bit K/V.
 KernelPair kernels_mf(int d, bool bf16);
 KernelPair kernels_mf_q8(int d);
+// Matrix-core kernels at D = 512 (fp16, bf16 and 8-bit): four-wave
+// workgroups, accumulators in AGPRs; a translation unit built without the
+// VGPR-only matrix-core form.
+KernelPair kernels_mf512(bool q8, bool bf16);
 
 }  // namespace pda_decode
 

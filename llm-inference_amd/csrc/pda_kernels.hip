@@ -155,7 +155,7 @@ int heads_per_group(int gtot) {
 }
 
 // Matrix-core kernels: head dims whose rows split into 32-element chunks
-// (64-element ones at 8 bits), and GQA groups of at least mf_min_group(q8)
+// (64-element ones at 8 bits), and GQA groups of at least mf_min_group(q8, d)
 // heads (the PDA_MFMA_MIN_GROUP environment variable moves both thresholds,
 // for measurements). 16-bit K/V: from 5 heads on, the VALU's q.k and p.v
 // issue of the 8-wave workgroup costs more than the matrix cores' 16-head
@@ -164,20 +164,26 @@ int heads_per_group(int gtot) {
 // most of their issue on the int8 conversions, which the matrix-core kernel
 // does once per element for all heads; it is level or faster at every group
 // size measured (1 to 7 heads, configs 1-5: config 2 114.7 -> 74.1 us).
+// D = 512 (four-wave workgroups, one K/V step in flight per wave): on the
+// Gemma 4 global layer (2 kv heads, 261,840 tokens) the 8-bit matrix-core
+// kernel takes 146-155 us at any group, the VALU kernel 119 us at 1-2
+// heads, 158 at 4 and 213 at 8, so 8-bit D = 512 starts at 4 heads; at 16
+// bits 197 against 204 us at 8 heads (the usual threshold of 5).
 bool mf_dim(int d, bool q8) {
-  return q8 ? (d == 64 || d == 128 || d == 256) : (d == 64 || d == 96 || d == 128 || d == 256);
+  return q8 ? (d == 64 || d == 128 || d == 256 || d == 512)
+            : (d == 64 || d == 96 || d == 128 || d == 256 || d == 512);
 }
 
-int mf_min_group(bool q8) {
+int mf_min_group(bool q8, int d) {
   static const int env = [] {
     const char* e = getenv("PDA_MFMA_MIN_GROUP");
     return e ? atoi(e) : 0;
   }();
   if (env > 0) return env;
-  return q8 ? 1 : 5;
+  return q8 ? (d == 512 ? 4 : 1) : 5;
 }
 
-bool use_mf(int gtot, int d, bool q8) { return mf_dim(d, q8) && gtot >= mf_min_group(q8); }
+bool use_mf(int gtot, int d, bool q8) { return mf_dim(d, q8) && gtot >= mf_min_group(q8, d); }
 
 // Heads per unit on the matrix cores: the whole group when it has at most 16
 // heads (one K/V read serves them all), else the largest divisor that does.
@@ -256,7 +262,7 @@ int make_plan(int32_t batch, int32_t q_heads, int32_t kv_heads, int32_t head_dim
 }
 
 // Resident workgroups of a split kernel on the current device (cached).
-int resident_groups(KernelFn fn, size_t lds_bytes) {
+int resident_groups(KernelFn fn, int threads, size_t lds_bytes) {
   static std::mutex mu;
   static std::map<std::pair<int, std::pair<const void*, size_t>>, int> cache;
   int dev = 0;
@@ -268,7 +274,7 @@ int resident_groups(KernelFn fn, size_t lds_bytes) {
   int cus = 0, per_cu = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
       hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(fn),
-                                                   kSplitThreads, lds_bytes) != hipSuccess)
+                                                   threads, lds_bytes) != hipSuccess)
     return -1;
   const int groups = std::max(1, std::min(kMaxGroups, cus * std::max(1, per_cu)));
   cache[key] = groups;
@@ -343,9 +349,11 @@ int pda_plan(int32_t batch, int32_t q_heads, int32_t kv_heads,
   const int rc = make_plan(batch, q_heads, kv_heads, head_dim, page_size,
                            table_stride, longest, window, split_pages, &pl);
   if (rc) return rc;
-  // On MI355X (256 CUs, one eight-wave workgroup each): 1024 pairs at most.
+  // On MI355X (256 CUs, one split workgroup each): 1024 pairs at most (512
+  // with the four-wave workgroups of the matrix-core kernels at D = 512).
   const int64_t want = (pl.pages_est + 2 * pl.min_pages - 1) / (2 * pl.min_pages);
-  const int64_t pairs = std::max<int64_t>(1, std::min<int64_t>(want, 256 * kPairs));
+  const int64_t pairs = std::max<int64_t>(
+      1, std::min<int64_t>(want, 256 * split_waves(pl.mf ? head_dim : 0, pl.mf) / 2));
   *waves = (int32_t)(2 * pairs);
   *pages_per_wave = (int32_t)((pl.pages_est + *waves - 1) / *waves);
   return ok();
@@ -454,11 +462,14 @@ int decode(int passes, const void* queries, const void* keys, const void* values
       return fail(PDA_ERR_ALIGNMENT, "workspace must be 256-byte aligned");
   }
 
-  const KernelPair kp = pl.mf ? (q8 ? kernels_mf_q8(head_dim) : kernels_mf(head_dim, bf16))
+  const KernelPair kp = pl.mf ? (head_dim == 512 ? kernels_mf512(q8, bf16)
+                                 : q8 ? kernels_mf_q8(head_dim)
+                                      : kernels_mf(head_dim, bf16))
                               : kernels_for(head_dim, pl.G, q8, bf16);
   if (!kp.split) return fail(PDA_ERR_HEAD_DIM, "head_dim %d has no kernel", head_dim);
   const size_t lds = (size_t)(2 * batch + 1) * sizeof(int32_t);
-  const int groups = resident_groups(kp.split, lds);
+  const int wg_pairs = kp.split_waves / 2;
+  const int groups = resident_groups(kp.split, 64 * kp.split_waves, lds);
   if (groups < 0) return fail(PDA_ERR_HIP, "device query failed");
 
   // Caller's workspace: the layout pda_workspace_bytes sizes (any grid).
@@ -470,8 +481,8 @@ int decode(int passes, const void* queries, const void* keys, const void* values
   wl.off_o = pl.off_o;
   wl.total = pl.total;
   if (use_scratch) {
-    wl = workspace_layout(batch, pl.unit_heads, kernel_dim(head_dim, q8), (int64_t)groups * kPairs,
-                          (int64_t)groups * 2 * kSplitWaves);
+    wl = workspace_layout(batch, pl.unit_heads, kernel_dim(head_dim, q8), (int64_t)groups * wg_pairs,
+                          (int64_t)groups * 4 * wg_pairs);
     if (wl.total > kScratchBytes)
       return fail(PDA_ERR_WORKSPACE,
                   "the no-allocation call needs %zu bytes of scratch for this shape, above "
@@ -519,7 +530,7 @@ int decode(int passes, const void* queries, const void* keys, const void* values
   prm.nhg = pl.nhg;
   prm.unit_heads = pl.unit_heads;
   prm.window = window;
-  prm.grid_pairs = groups * kPairs;
+  prm.grid_pairs = groups * wg_pairs;
   prm.min_pages = pl.min_pages;
   prm.fixed = (flags & PDA_DECODE_FIXED_SPLIT) ? 1 : 0;
   prm.ragged = page_size % (pl.mf ? 16 : keys_per_step(head_dim, q8)) ? 1 : 0;
@@ -533,7 +544,7 @@ int decode(int passes, const void* queries, const void* keys, const void* values
   hipError_t err = hipSuccess;
   if (passes & kPassSplit)
     err = hipLaunchKernel(reinterpret_cast<const void*>(kp.split), dim3(groups),
-                          dim3(kSplitThreads), args, lds, st);
+                          dim3(64 * kp.split_waves), args, lds, st);
   if (err == hipSuccess && (passes & kPassMerge)) {
     const int heads = kv_heads * pl.nhg * pl.unit_heads;
     const MergeShape ms = merge_shape(pl, pl.mf ? head_dim : kernel_dim(head_dim, q8),

@@ -76,18 +76,19 @@ def _given_workspace(ws: torch.Tensor, device: torch.device, nbytes: int) -> tor
 
 _FAST_DIMS = {16: (64, 80, 96, 128, 256, 512), 8: (64, 128, 256, 512)}
 # Matrix-core kernels by K/V bits: head dims, and the fewest heads per kv head.
-_MF_DIMS = {16: (64, 96, 128, 256), 8: (64, 128, 256)}
+_MF_DIMS = {16: (64, 96, 128, 256, 512), 8: (64, 128, 256, 512)}
 _MF_MIN_GROUP = {16: 5, 8: 1}
 # Merge launch (csrc/pda_kernels.hip ``merge_shape``) on MI355X: 256 CUs x
-# one split workgroup of four wave pairs; the row-sliced merge for units of
-# more than 64 pieces, in grids of 4096 workgroups at most.
+# one split workgroup of four wave pairs (two for the matrix-core kernels at
+# D = 512); the row-sliced merge for units of more than 64 pieces, in grids
+# of 4096 workgroups at most.
 _GRID_PAIRS = 1024
 _MERGE_SLICED_ROUND = 64
 _MERGE_SLICED_MAX_GROUPS = 4096
 
 
 def _merge_sliced(dim, heads, units, *, batch, longest, page_size, table_width, window,
-                  split_pages) -> bool:
+                  split_pages, grid_pairs=_GRID_PAIRS) -> bool:
     """Whether the merge runs row-sliced (one 64-element slice of a head per
     workgroup): the library's rule, from the same page estimates."""
     pages_max = table_width
@@ -98,7 +99,7 @@ def _merge_sliced(dim, heads, units, *, batch, longest, page_size, table_width, 
         est = min(est, -(-longest // page_size) + 1)
     pages_est = batch * units * est
     min_pages = split_pages if split_pages > 0 else 1
-    pairs = max(1, min(_GRID_PAIRS, -(-pages_est // (2 * min_pages))))
+    pairs = max(1, min(grid_pairs, -(-pages_est // (2 * min_pages))))
     per_pair = max(1, pages_est // pairs)
     pieces = 2 * (est // per_pair + 2)
     chunks = -(-dim // 64)
@@ -121,7 +122,8 @@ def decode_kernel_names(q_heads: int, kv_heads: int, head_dim: int, *, bits: int
     head's K/V once). The merge's row slicing depends on the batch, the
     longest length and the table width (``batch`` 0: not sliced)."""
     group = q_heads // kv_heads
-    min_mf = int(os.environ.get("PDA_MFMA_MIN_GROUP", "0") or 0) or _MF_MIN_GROUP[bits]
+    min_mf = (int(os.environ.get("PDA_MFMA_MIN_GROUP", "0") or 0)
+              or (4 if bits == 8 and head_dim == 512 else _MF_MIN_GROUP[bits]))
     mf = head_dim in _MF_DIMS[bits] and group >= min_mf
     cap = 16 if mf else 8
     heads = next(g for g in range(min(group, cap), 0, -1) if group % g == 0)
@@ -132,7 +134,7 @@ def decode_kernel_names(q_heads: int, kv_heads: int, head_dim: int, *, bits: int
     sliced = batch > 0 and _merge_sliced(
         dim, units * heads, units, batch=batch, longest=longest, page_size=page_size,
         table_width=table_width or -(-max(longest, 1) // page_size), window=window,
-        split_pages=split_pages)
+        split_pages=split_pages, grid_pairs=_GRID_PAIRS // 2 if mf and dim == 512 else _GRID_PAIRS)
     b = lambda x: str(bool(x)).lower()  # noqa: E731
     targs = f"{dim},{slots},{b(bits == 8)},{b(bf16)},{b(generic)},{b(mf)}"
     return {"split": f"paged_decode_kernel<{targs}>",

@@ -155,7 +155,7 @@ def mf_case(gpu, q_heads, kv_heads, head_dim, lengths, page=16, window=0, softca
                            device=gpu, seed=seed + 1)
 
 
-@pytest.mark.parametrize("head_dim", [64, 128, 256])
+@pytest.mark.parametrize("head_dim", [64, 128, 256, 512])
 @pytest.mark.parametrize("q_heads,kv_heads", [(5, 1), (7, 1), (8, 1), (11, 1), (16, 2),
                                               (24, 2), (28, 4)])
 def test_matrix_cores_group_sizes(gpu, q_heads, kv_heads, head_dim):
@@ -169,29 +169,31 @@ def test_matrix_cores_group_sizes(gpu, q_heads, kv_heads, head_dim):
         check(qw, f"mf q8 {q_heads}/{kv_heads} D{head_dim} {layout} fixed", deterministic=True)
 
 
+@pytest.mark.parametrize("head_dim", [128, 512])
 @pytest.mark.parametrize("page", [1, 5, 12, 24, 64])
-def test_matrix_cores_page_sizes(gpu, page):
+def test_matrix_cores_page_sizes(gpu, page, head_dim):
     """Pages that are not a multiple of the 16-key step: the last step of a
     page moves its rows back inside the page and masks the duplicates."""
-    w = mf_case(gpu, 14, 2, 128, [1, page, page + 1, 777, 1500], page=page, seed=page)
+    w = mf_case(gpu, 14, 2, head_dim, [1, page, page + 1, 777, 1500], page=page, seed=page)
     for layout in ("pages", "rows"):
-        check(Quantized(w, layout), f"mf q8 page {page} {layout}")
+        check(Quantized(w, layout), f"mf q8 page {page} D{head_dim} {layout}")
 
 
+@pytest.mark.parametrize("head_dim", [128, 512])
 @pytest.mark.parametrize("layout", ["pages", "rows"])
-def test_matrix_cores_window_poison_softcap(gpu, layout):
+def test_matrix_cores_window_poison_softcap(gpu, layout, head_dim):
     """Rows before the window hold NaN key scales and inf value scales; the
     masked keys' values are zeroed after dequantization, so nothing leaks."""
     P, W = 16, 300
     lengths = [1200, 301, 299, 4000, 9]
-    w = mf_case(gpu, 24, 2, 128, lengths, window=W, softcap=30.0, seed=8)
+    w = mf_case(gpu, 24, 2, head_dim, lengths, window=W, softcap=30.0, seed=8)
     _, _, _, t, n = w.numpy()
     poison = []
     for b, length in enumerate(lengths):
         for pos in range(0, max(0, length - W)):
             poison.append(int(t[b, pos // P]) * P + pos % P)
     qw = Quantized(w, layout, poison_rows=np.array(poison, dtype=np.int64))
-    check(qw, f"mf q8 window poison softcap {layout}")
+    check(qw, f"mf q8 window poison softcap D{head_dim} {layout}")
 
 
 def test_matrix_cores_fixed_split_is_bitwise_reproducible(gpu):

@@ -4,7 +4,8 @@ The reference serves a whole GQA group from one K/V read whatever its size
 (32 x G x R threads per threadgroup, metal_kernels.py:191-192,216-217). Here
 groups of 5 to 16 heads (and larger groups as units of up to 16) run
 S^T = K Q^T and O^T += V^T P^T on v_mfma_f32_16x16x32 / 16x16x16 at head dims
-64, 96, 128 and 256, one K/V read per unit. Checked against the float64
+64, 96, 128, 256 and 512 (four-wave workgroups, accumulators in AGPRs), one
+K/V read per unit. Checked against the float64
 oracle (max-abs 2e-3, mean-abs 2e-4; bf16 at its own bar,
 test_gpu_bf16.py), in both arena layouts, with windows, released pages and
 NaN/inf poison, softcap, ragged pages, key ranges split at many points, the
@@ -81,7 +82,7 @@ def check(w, what, **kw):
         stats(run(w, deterministic=True, **kw), want, f"{what} [{layout}, fixed]")
 
 
-@pytest.mark.parametrize("head_dim", [64, 96, 128, 256])
+@pytest.mark.parametrize("head_dim", [64, 96, 128, 256, 512])
 @pytest.mark.parametrize("q_heads,kv_heads", [(5, 1), (6, 1), (7, 1), (28, 4), (14, 2),
                                               (8, 1), (16, 2), (9, 1), (11, 1), (12, 1),
                                               (13, 1), (16, 1), (24, 2), (32, 2), (40, 2)])
@@ -92,7 +93,7 @@ def test_group_sizes_and_head_dims(gpu, q_heads, kv_heads, head_dim):
     check(w, f"mf {q_heads}/{kv_heads} D{head_dim}")
 
 
-@pytest.mark.parametrize("head_dim", [64, 128, 256])
+@pytest.mark.parametrize("head_dim", [64, 128, 256, 512])
 def test_split_into_many_pieces(gpu, head_dim):
     """split_pages 1 and 3: every unit cut into many pieces, merged."""
     w = make(gpu, q_heads=16, kv_heads=1, head_dim=head_dim, lengths=[3000, 50, 1], seed=5)
@@ -100,17 +101,19 @@ def test_split_into_many_pieces(gpu, head_dim):
     check(w, f"mf split3 D{head_dim}", split_pages=3)
 
 
+@pytest.mark.parametrize("head_dim", [128, 512])
 @pytest.mark.parametrize("page", [1, 4, 12, 24, 64])
-def test_page_sizes(gpu, page):
-    w = make(gpu, q_heads=16, kv_heads=2, head_dim=128, page=page,
+def test_page_sizes(gpu, page, head_dim):
+    w = make(gpu, q_heads=16, kv_heads=2, head_dim=head_dim, page=page,
              lengths=[1, page, page + 1, 777, 1500], seed=page)
-    check(w, f"mf P{page}")
+    check(w, f"mf P{page} D{head_dim}")
 
 
-def test_window_softcap_released_pages_and_poison(gpu):
+@pytest.mark.parametrize("head_dim", [128, 512])
+def test_window_softcap_released_pages_and_poison(gpu, head_dim):
     P, W = 16, 300
     lengths = np.array([1200, 301, 299, 4000, 9])
-    w = make(gpu, q_heads=24, kv_heads=2, head_dim=128, lengths=list(lengths), window=W,
+    w = make(gpu, q_heads=24, kv_heads=2, head_dim=head_dim, lengths=list(lengths), window=W,
              softcap=30.0, seed=8)
     t = w.tables.cpu().numpy()
     visible = np.zeros(w.keys.shape[0], dtype=bool)
@@ -123,7 +126,7 @@ def test_window_softcap_released_pages_and_poison(gpu):
     hidden = torch.as_tensor(np.flatnonzero(~visible), device=gpu)
     w.keys[hidden] = float("nan")
     w.values[hidden] = float("inf")
-    check(w, "mf window softcap poison")
+    check(w, f"mf window softcap poison D{head_dim}")
 
 
 def test_planted_large_logits(gpu):
@@ -165,7 +168,7 @@ def test_separate_passes(gpu):
 
 
 @pytest.mark.parametrize("q_heads,kv_heads,head_dim", [(16, 1, 128), (11, 1, 64), (24, 2, 256),
-                                                       (8, 1, 96)])
+                                                       (8, 1, 96), (16, 2, 512), (11, 1, 512)])
 def test_bf16(gpu, q_heads, kv_heads, head_dim):
     w = make(gpu, q_heads=q_heads, kv_heads=kv_heads, head_dim=head_dim,
              lengths=[5, 900, 2049], seed=head_dim + q_heads).to_layout("pages")

@@ -78,9 +78,22 @@ def test_noalloc_matches_the_workspace_call_on_two_calls(gpu):
         within_bar(free, want, f"{name} default vs oracle")
 
 
+def test_noalloc_at_512_wide_heads_on_four_wave_workgroups(gpu):
+    """The matrix-core kernels at D = 512 run four-wave workgroups; the
+    scratch is laid out for that grid (5 query heads per kv head: 2 x CUs x
+    4 waves x 5 x 512 floats of partials, within the 32 MiB)."""
+    w = workloads.reference_test_case(5, 1, 512, [1, 700, 2049, 6000], 0, 0.0, device=gpu)
+    w.to_layout("pages")
+    rc, fixed = noalloc(w, _lib.PDA_DECODE_FIXED_SPLIT)
+    _lib.check(rc)
+    assert torch.equal(fixed, with_workspace(w, True))
+    within_bar(fixed, oracle(w), "512-wide, 5 heads, fixed")
+
+
 def test_noalloc_rejects_a_shape_beyond_its_scratch(gpu):
-    """512-wide heads with 8 query heads per kv head: 2 x CUs x 8 waves x 8
-    x 512 floats of partials, above the 32 MiB scratch."""
+    """512-wide heads with 8 query heads per kv head: 2 x CUs x 4 waves x 8
+    x 512 floats of partials, 32 MiB, plus the pair records: above the
+    32 MiB scratch."""
     w = workloads.reference_test_case(16, 2, 512, [1, 700, 2049], 0, 0.0, device=gpu)
     rc, _ = noalloc(w, 0)
     assert rc == _lib.PDA_ERR_WORKSPACE
