@@ -18,6 +18,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "pda_internal.h"
 
 namespace pda_decode {
@@ -534,15 +536,17 @@ void paged_decode_kernel(const Params p) {
     // lane % 16 (zero past the unit's heads), the elements this lane's K
     // loads hold.
     f16x8 qb[MF ? NV : 1];
+    // Matrix-core kernels: the first of the 8 elements of a row that chunk c
+    // of this lane's K and V loads holds (8-bit: two chunks per load).
+    auto mf_elem = [&](int c) {
+      return Q8 ? 64 * (c >> 1) + 16 * mg + 8 * (c & 1) : 32 * c + 8 * mg;
+    };
     if constexpr (MF) {
       const bool real = (lane & 15) < hpu;
       const f16* qp = p.q + ((int64_t)b * p.hq + h0 + (real ? (lane & 15) : 0)) * D;
 #pragma unroll
-      for (int c = 0; c < NV; ++c) {
-        // The elements chunk c of the K loads holds (8-bit: two chunks per load).
-        const int e = Q8 ? 64 * (c >> 1) + 16 * mg + 8 * (c & 1) : 32 * c + 8 * mg;
-        qb[c] = zero_unless(*reinterpret_cast<const f16x8*>(qp + e), real);
-      }
+      for (int c = 0; c < NV; ++c)
+        qb[c] = zero_unless(*reinterpret_cast<const f16x8*>(qp + mf_elem(c)), real);
     }
 #pragma unroll
     for (int g = 0; g < (MF ? 0 : G); ++g) {
@@ -775,6 +779,152 @@ void paged_decode_kernel(const Params p) {
       }
     };
 
+    // 8-bit matrix-core step: chunk h of a 16-byte int8 K piece and of the V
+    // piece, converted exactly to fp16 (K) and to fp16(int8 x scale) (V,
+    // rounded as the reference's gather does, paged_kv.py:285-292).
+    auto q8_chunk = [&](const f16x8& kpiece, const f16x8& vpiece, int h, f16x2 vsc, f16x8& kc,
+                        f16x8& vc) {
+      const i32x4 kr = __builtin_bit_cast(i32x4, kpiece);
+      const i32x4 vr8 = __builtin_bit_cast(i32x4, vpiece);
+      f16x2 kq2[4], vq2[4];
+#pragma unroll
+      for (int w2 = 0; w2 < 2; ++w2) {
+        const uint32_t kf = (uint32_t)kr[2 * h + w2] ^ 0x80808080u;
+        const uint32_t vf = (uint32_t)vr8[2 * h + w2] ^ 0x80808080u;
+        kq2[2 * w2] = bytes_to_f16x2(kf, 0x04010400u);
+        kq2[2 * w2 + 1] = bytes_to_f16x2(kf, 0x04030402u);
+        vq2[2 * w2] = bytes_to_f16x2(vf, 0x04010400u) * vsc;
+        vq2[2 * w2 + 1] = bytes_to_f16x2(vf, 0x04030402u) * vsc;
+      }
+      kc = f16x8{kq2[0][0], kq2[0][1], kq2[1][0], kq2[1][1],
+                 kq2[2][0], kq2[2][1], kq2[3][0], kq2[3][1]};
+      vc = f16x8{vq2[0][0], vq2[0][1], vq2[1][0], vq2[1][1],
+                 vq2[2][0], vq2[2][1], vq2[3][0], vq2[3][1]};
+    };
+
+    // Matrix-core step after the S product: the scores (times their keys'
+    // scales at 8 bits; lane k % 16 loaded the scale of key k), the masks of
+    // a boundary step, the lazy running max, P^T, and O^T += V^T P^T through
+    // this wave's LDS tile. With stores_v the step's V chunks `vc` go into
+    // the tile here (masked keys' rows zeroed first); otherwise the caller
+    // has stored them.
+    auto mf_back = [&](const f32x4& sacc, int t0, int lim, float ks_own, f16x8(&vc)[NV],
+                       auto stores_v) {
+      // 8-bit: each score times its key's scale (metal_kernels.py:52
+      // KEY_SCALE); lane k % 16 loaded the scale of key k.
+      float ksc[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+      if constexpr (Q8) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ksc[e] = __shfl(ks_own, 4 * mg + e);
+      }
+      float sr[4], x[4];  // scores in log2 units, and minus the running max
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float raw = Q8 ? sacc[e] * ksc[e] : sacc[e];
+        if (p.softcap > 0.0f) {
+          const float ex = __builtin_amdgcn_exp2f(raw * p.cap_in);
+          sr[e] = (1.0f - 2.0f * __builtin_amdgcn_rcpf(ex + 1.0f)) * p.cap_out;
+        } else {
+          sr[e] = raw * p.scale_log2;
+        }
+        x[e] = sr[e] - m[0];
+      }
+      if (!(t0 >= first && t0 + 16 <= lim)) {
+        // Boundary step: scores of keys outside [first, lim) are masked,
+        // and the V row this lane loaded is zeroed if its key is.
+        bool any = false;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int t = t0 + 4 * mg + e;
+          const bool ok = t >= first && t < lim;
+          sr[e] = ok ? sr[e] : -INFINITY;
+          x[e] = ok ? x[e] : -INFINITY;
+          any |= ok;
+        }
+        if (!__any(any)) return;
+        if constexpr (decltype(stores_v)::value) {
+          const bool vok = t0 + lk >= first && t0 + lk < lim;
+#pragma unroll
+          for (int c = 0; c < NV; ++c) vc[c] = zero_unless(vc[c], vok);
+        }
+      }
+      if (__any(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])) > kSlack)) {
+        // Rare: raise each head's running max to its largest score of
+        // the step (every head sees the step's visible keys, so the max
+        // is finite) and rescale its sum and outputs.
+        float hm = fmaxf(fmaxf(sr[0], sr[1]), fmaxf(sr[2], sr[3]));
+        hm = fmaxf(hm, __shfl_xor(hm, 16));
+        hm = fmaxf(hm, __shfl_xor(hm, 32));
+        const float mn = fmaxf(m[0], hm);
+        const float f = __builtin_amdgcn_exp2f(m[0] - mn);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[e] = sr[e] - mn;
+        m[0] = mn;
+        l[0] *= f;
+#pragma unroll
+        for (int i = 0; i < D / 16; ++i) ob[i] *= f;
+      }
+      // P^T, the B operand of O^T += V^T P^T as the accumulator holds it;
+      // the sum uses the same rounded probabilities.
+      f16x4 pb;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float pr = __builtin_amdgcn_exp2f(x[e]);
+        if constexpr (BF) {
+          const bf16 r16 = (bf16)pr;
+          pb[e] = __builtin_bit_cast(f16, r16);
+          l[0] += (float)r16;
+        } else {
+          pb[e] = (f16)pr;
+          l[0] += (float)pb[e];
+        }
+      }
+      // V^T through this wave's LDS tile: the row pieces as loaded, then
+      // a transposed read gives lane l element 16 i + l % 16 of keys
+      // 4 mg .. 4 mg + 3 (in-order LDS: the next step's stores follow
+      // these reads).
+      f16* const vt = s_vt + w * 16 * kVRow;
+      if constexpr (decltype(stores_v)::value) {
+#pragma unroll
+        for (int c = 0; c < NV; ++c)
+          *reinterpret_cast<f16x8*>(vt + lk * kVRow + mf_elem(c)) = vc[c];
+      }
+      const f16* const vr = vt + (4 * mg + ((lane & 15) >> 2)) * kVRow + 4 * (lane & 3);
+#pragma unroll
+      for (int i = 0; i < D / 16; ++i) ob[i] = mfma_k16<BF>(read_tr(vr + 16 * i), pb, ob[i]);
+    };
+
+    // 8-bit matrix-core step with one step in flight (D >= 256), first part:
+    // the step's V chunks converted (8-bit) and stored into the LDS tile,
+    // masked keys' rows zeroed, and S^T = K Q^T. It consumes every register
+    // the step's loads filled, so the next step's loads can be issued before
+    // the softmax and p.v (mf_back) instead of after them.
+    auto mf_front = [&](int u, f32x4& sacc, int& t0, int& lim, float& ks_own) -> bool {
+      if (!s_ok[u]) return false;  // released or out-of-range page: masked
+      t0 = s_t0[u];
+      lim = min(len, t0 + s_kin[u]);
+      const bool vok = (t0 >= first && t0 + 16 <= lim) || (t0 + lk >= first && t0 + lk < lim);
+      f16* const vt = s_vt + w * 16 * kVRow;
+      sacc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      ks_own = 1.0f;
+      if constexpr (Q8) {
+        ks_own = (float)ksb[u];
+        const f16x2 vsc = {vs_own_b[u], vs_own_b[u]};
+#pragma unroll
+        for (int j = 0; j < NV / 2; ++j) {
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            f16x8 kc, vc;
+            q8_chunk(kb[u][j], vb[u][j], h, vsc, kc, vc);
+            *reinterpret_cast<f16x8*>(vt + lk * kVRow + mf_elem(2 * j + h)) =
+                zero_unless(vc, vok);
+            sacc = mfma_k32<BF>(kc, qb[2 * j + h], sacc);
+          }
+        }
+      }
+      return true;
+    };
+
     auto compute_step = [&](int u) {
       if (!s_ok[u]) return;  // released or out-of-range page: masked
       const int t0 = s_t0[u];
@@ -788,27 +938,9 @@ void paged_decode_kernel(const Params p) {
         if constexpr (Q8) {
           const f16x2 vsc = {vs_own_b[u], vs_own_b[u]};
 #pragma unroll
-          for (int j = 0; j < NV / 2; ++j) {
-            const i32x4 kr = __builtin_bit_cast(i32x4, kd[j]);
-            const i32x4 vr8 = __builtin_bit_cast(i32x4, vd[j]);
+          for (int j = 0; j < NV / 2; ++j)
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-              f16x2 kq2[4], vq2[4];
-#pragma unroll
-              for (int w2 = 0; w2 < 2; ++w2) {
-                const uint32_t kf = (uint32_t)kr[2 * h + w2] ^ 0x80808080u;
-                const uint32_t vf = (uint32_t)vr8[2 * h + w2] ^ 0x80808080u;
-                kq2[2 * w2] = bytes_to_f16x2(kf, 0x04010400u);
-                kq2[2 * w2 + 1] = bytes_to_f16x2(kf, 0x04030402u);
-                vq2[2 * w2] = bytes_to_f16x2(vf, 0x04010400u) * vsc;
-                vq2[2 * w2 + 1] = bytes_to_f16x2(vf, 0x04030402u) * vsc;
-              }
-              kc[2 * j + h] = f16x8{kq2[0][0], kq2[0][1], kq2[1][0], kq2[1][1],
-                                    kq2[2][0], kq2[2][1], kq2[3][0], kq2[3][1]};
-              vc[2 * j + h] = f16x8{vq2[0][0], vq2[0][1], vq2[1][0], vq2[1][1],
-                                    vq2[2][0], vq2[2][1], vq2[3][0], vq2[3][1]};
-            }
-          }
+            for (int h = 0; h < 2; ++h) q8_chunk(kd[j], vd[j], h, vsc, kc[2 * j + h], vc[2 * j + h]);
         } else {
 #pragma unroll
           for (int c = 0; c < NV; ++c) {
@@ -821,88 +953,8 @@ void paged_decode_kernel(const Params p) {
         f32x4 sacc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int c = 0; c < NV; ++c) sacc = mfma_k32<BF>(kc[c], qb[c], sacc);
-        // 8-bit: each score times its key's scale (metal_kernels.py:52
-        // KEY_SCALE); lane k % 16 loaded the scale of key k.
-        float ksc[4] = {1.0f, 1.0f, 1.0f, 1.0f};
-        if constexpr (Q8) {
-          const float own = (float)ksb[u];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) ksc[e] = __shfl(own, 4 * mg + e);
-        }
-        const int lim = min(len, t0 + s_kin[u]);
-        float sr[4], x[4];  // scores in log2 units, and minus the running max
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float raw = Q8 ? sacc[e] * ksc[e] : sacc[e];
-          if (p.softcap > 0.0f) {
-            const float ex = __builtin_amdgcn_exp2f(raw * p.cap_in);
-            sr[e] = (1.0f - 2.0f * __builtin_amdgcn_rcpf(ex + 1.0f)) * p.cap_out;
-          } else {
-            sr[e] = raw * p.scale_log2;
-          }
-          x[e] = sr[e] - m[0];
-        }
-        if (!(t0 >= first && t0 + 16 <= lim)) {
-          // Boundary step: scores of keys outside [first, lim) are masked,
-          // and the V row this lane loaded is zeroed if its key is.
-          bool any = false;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int t = t0 + 4 * mg + e;
-            const bool ok = t >= first && t < lim;
-            sr[e] = ok ? sr[e] : -INFINITY;
-            x[e] = ok ? x[e] : -INFINITY;
-            any |= ok;
-          }
-          if (!__any(any)) return;
-          const bool vok = t0 + lk >= first && t0 + lk < lim;
-#pragma unroll
-          for (int c = 0; c < NV; ++c) vc[c] = zero_unless(vc[c], vok);
-        }
-        if (__any(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])) > kSlack)) {
-          // Rare: raise each head's running max to its largest score of
-          // the step (every head sees the step's visible keys, so the max
-          // is finite) and rescale its sum and outputs.
-          float hm = fmaxf(fmaxf(sr[0], sr[1]), fmaxf(sr[2], sr[3]));
-          hm = fmaxf(hm, __shfl_xor(hm, 16));
-          hm = fmaxf(hm, __shfl_xor(hm, 32));
-          const float mn = fmaxf(m[0], hm);
-          const float f = __builtin_amdgcn_exp2f(m[0] - mn);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) x[e] = sr[e] - mn;
-          m[0] = mn;
-          l[0] *= f;
-#pragma unroll
-          for (int i = 0; i < D / 16; ++i) ob[i] *= f;
-        }
-        // P^T, the B operand of O^T += V^T P^T as the accumulator holds it;
-        // the sum uses the same rounded probabilities.
-        f16x4 pb;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float pr = __builtin_amdgcn_exp2f(x[e]);
-          if constexpr (BF) {
-            const bf16 r16 = (bf16)pr;
-            pb[e] = __builtin_bit_cast(f16, r16);
-            l[0] += (float)r16;
-          } else {
-            pb[e] = (f16)pr;
-            l[0] += (float)pb[e];
-          }
-        }
-        // V^T through this wave's LDS tile: the row pieces as loaded, then
-        // a transposed read gives lane l element 16 i + l % 16 of keys
-        // 4 mg .. 4 mg + 3 (in-order LDS: the next step's stores follow
-        // these reads).
-        f16* const vt = s_vt + w * 16 * kVRow;
-#pragma unroll
-        for (int c = 0; c < NV; ++c) {
-          const int e = Q8 ? 64 * (c >> 1) + 16 * mg + 8 * (c & 1) : 32 * c + 8 * mg;
-          *reinterpret_cast<f16x8*>(vt + lk * kVRow + e) = vc[c];
-        }
-        const f16* const vr = vt + (4 * mg + ((lane & 15) >> 2)) * kVRow + 4 * (lane & 3);
-#pragma unroll
-        for (int i = 0; i < D / 16; ++i) ob[i] = mfma_k16<BF>(read_tr(vr + 16 * i), pb, ob[i]);
+        mf_back(sacc, t0, min(len, t0 + s_kin[u]), Q8 ? (float)ksb[u] : 1.0f, vc,
+                std::true_type{});
         return;
       } else {
       // q.k for every head of the group: v_dot2 over this lane's slice,
@@ -1122,18 +1174,35 @@ void paged_decode_kernel(const Params p) {
 
 #pragma unroll
     for (int u = 0; u < NBUF; ++u) load_step(u);
-    // The ring: every slot is waited for (its loads are complete once only
-    // the other slots' remain), computed if it holds a real step and
-    // reloaded, in issue order on every path, with the loop test at the
-    // bottom; the compiler's wait counts then stay those of a steady ring.
-    do {
+    if constexpr (MF && Q8 && NBUF == 1) {
+      // One step in flight (8-bit, D >= 256): wait for it, consume its
+      // registers (mf_front), issue the next step's loads, then finish the
+      // step (mf_back) while they are in flight. On the Gemma 4 global
+      // layer at 8 bits, 152 -> 135 us; the 16-bit kernels, whose steps are
+      // twice the bytes, were 1-3% slower this way and keep the plain ring.
+      do {
+        wait_vmem<0>();
+        f32x4 sacc;
+        int t0 = 0, lim = 0;
+        float ks_own = 1.0f;
+        const bool live = s_real[0] && mf_front(0, sacc, t0, lim, ks_own);
+        load_step(0);
+        if (live) mf_back(sacc, t0, lim, ks_own, vb[0], std::false_type{});
+      } while (s_real[0]);
+    } else {
+      // The ring: every slot is waited for (its loads are complete once
+      // only the other slots' remain), computed if it holds a real step and
+      // reloaded, in issue order on every path, with the loop test at the
+      // bottom; the compiler's wait counts then stay those of a steady ring.
+      do {
 #pragma unroll
-      for (int u = 0; u < NBUF; ++u) {
-        wait_vmem<(NBUF - 1) * Gm::LOADS>();
-        if (s_real[u]) compute_step(u);
-        load_step(u);
-      }
-    } while (s_real[0]);
+        for (int u = 0; u < NBUF; ++u) {
+          wait_vmem<(NBUF - 1) * Gm::LOADS>();
+          if (s_real[u]) compute_step(u);
+          load_step(u);
+        }
+      } while (s_real[0]);
+    }
     // `pending` now tells whether the page after this unit is ours too.
 
     if constexpr (MF) {
