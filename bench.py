@@ -438,6 +438,33 @@ def published_leg(args, flush):
            "kv_bytes": kv_bytes, "kernel": f"{names['split']} + {names['merge']}",
            "us_median": round(med * 1e3, 2), "us_mean": round(statistics.fmean(ms) * 1e3, 2),
            "GB_per_s": round(rate, 2), "pct_hbm_peak": round(100 * rate / HBM_PEAK_GBS, 2)}
+    # The same layer with the 8-bit cache (KVCache(bits=8): int8 rows, an
+    # fp16 scale per row and kv head), queries in fp16.
+    def quantize(x):
+        s8 = (x.float().abs().amax(-1).clamp(min=1e-4) / 127.0).half()
+        return (x.float() / s8.float()[..., None]).round().clamp(-127, 127).to(torch.int8), s8
+
+    (keys8, kscale), (values8, vscale) = quantize(w.keys), quantize(w.values)
+    q16 = w.q.half()
+    out16 = torch.empty_like(q16)
+
+    def call8():
+        paged_decode_attention(q16, keys8, values8, w.tables, w.lengths,
+                               page_size=w.page_size, longest=w.longest, scale=w.scale,
+                               out=out16, scales=(kscale, vscale),
+                               deterministic=args.deterministic)
+
+    for _ in range(args.warmup):
+        call8()
+    (ms8,), _ = time_calls([call8], args.steps, flush)
+    med8 = statistics.median(ms8)
+    bytes8 = int(w.spans().sum()) * w.kv_heads * (w.head_dim + 2) * 2
+    names8 = decode_kernel_names(w.q_heads, w.kv_heads, w.head_dim, bits=8,
+                                 **merge_shape_of(w))
+    leg["kv8"] = {"kernel": f"{names8['split']} + {names8['merge']}",
+                  "us_median": round(med8 * 1e3, 2), "kv_bytes": bytes8,
+                  "GB_per_s": round(bytes8 / (med8 * 1e-3) / 1e9, 2)}
+    del keys8, values8, kscale, vscale
     if int(args.published) == 261840:
         leg["reference_published"] = {
             "ms_per_layer": 6.7, "GB_per_s_as_published": 320,
