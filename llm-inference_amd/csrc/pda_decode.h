@@ -121,8 +121,9 @@ constexpr int next_pow2(int x) {
 // 16-byte aligned); pairs at or past the real head dim are not loaded and
 // read as zero. p.v runs on FMAs.
 //
-// Matrix-core kernels (MF, a GQA group of 5 or more query heads): a step is
-// 16 keys; lane l loads key l % 16, elements [32 c + 8 (l / 16), + 8) of
+// Matrix-core kernels (MF; use_mf in pda_kernels.hip picks the groups each
+// head dim takes them at): a step is 16 keys; lane l loads key l % 16,
+// elements [32 c + 8 (l / 16), + 8) of
 // each 32-element chunk c (NV = D / 32 chunks, one 16-byte load each for K
 // and for V), the A operand of v_mfma_f32_16x16x32 as it lands. At 8 bits
 // (MF and Q8, D a multiple of 64) chunk c = 2 j + h holds elements

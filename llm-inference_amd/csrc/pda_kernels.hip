@@ -164,11 +164,12 @@ int heads_per_group(int gtot) {
 // most of their issue on the int8 conversions, which the matrix-core kernel
 // does once per element for all heads; it is level or faster at every group
 // size measured (1 to 7 heads, configs 1-5: config 2 114.7 -> 74.1 us).
-// D = 512 (four-wave workgroups, one K/V step in flight per wave): on the
-// Gemma 4 global layer (2 kv heads, 261,840 tokens) the 8-bit matrix-core
-// kernel takes 146-155 us at any group, the VALU kernel 119 us at 1-2
-// heads, 158 at 4 and 213 at 8, so 8-bit D = 512 starts at 4 heads; at 16
-// bits 197 against 204 us at 8 heads (the usual threshold of 5).
+// D = 512 (four-wave workgroups, one K/V step in flight per wave), on the
+// Gemma 4 global layer (2 kv heads, 261,840 tokens): at 16 bits the
+// matrix-core kernel is faster at every group (191-196 us against the VALU
+// kernel's 197-222 at 1-8 heads); at 8 bits it takes 131-135 us at any
+// group, the VALU kernel 117-131 us at 1-3 heads and 157-217 at 4-8, so
+// 8-bit D = 512 starts at 4 heads.
 bool mf_dim(int d, bool q8) {
   return q8 ? (d == 64 || d == 128 || d == 256 || d == 512)
             : (d == 64 || d == 96 || d == 128 || d == 256 || d == 512);
@@ -180,7 +181,8 @@ int mf_min_group(bool q8, int d) {
     return e ? atoi(e) : 0;
   }();
   if (env > 0) return env;
-  return q8 ? (d == 512 ? 4 : 1) : 5;
+  if (d == 512) return q8 ? 4 : 1;
+  return q8 ? 1 : 5;
 }
 
 bool use_mf(int gtot, int d, bool q8) { return mf_dim(d, q8) && gtot >= mf_min_group(q8, d); }

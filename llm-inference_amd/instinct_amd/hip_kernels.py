@@ -123,7 +123,7 @@ def decode_kernel_names(q_heads: int, kv_heads: int, head_dim: int, *, bits: int
     longest length and the table width (``batch`` 0: not sliced)."""
     group = q_heads // kv_heads
     min_mf = (int(os.environ.get("PDA_MFMA_MIN_GROUP", "0") or 0)
-              or (4 if bits == 8 and head_dim == 512 else _MF_MIN_GROUP[bits]))
+              or ((4 if bits == 8 else 1) if head_dim == 512 else _MF_MIN_GROUP[bits]))
     mf = head_dim in _MF_DIMS[bits] and group >= min_mf
     cap = 16 if mf else 8
     heads = next(g for g in range(min(group, cap), 0, -1) if group % g == 0)

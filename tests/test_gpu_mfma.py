@@ -1,4 +1,5 @@
-"""Decode on the matrix cores: GQA groups of 5 or more query heads per kv head.
+"""Decode on the matrix cores: GQA groups of 5 or more query heads per kv head
+(any group at head dim 512).
 
 The reference serves a whole GQA group from one K/V read whatever its size
 (32 x G x R threads per threadgroup, metal_kernels.py:191-192,216-217). Here
