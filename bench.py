@@ -61,10 +61,11 @@ def parse():
     ap.add_argument("--split-pages", type=int, default=0)
     ap.add_argument("--deterministic", action="store_true",
                     help="fixed split points (PDA_DECODE_FIXED_SPLIT): bitwise reproducible")
-    ap.add_argument("--latency-configs", default="1",
+    ap.add_argument("--latency-configs", default="1,3,4,5",
                     help="other configs timed in the same run, comma-separated ('' = none): "
                          "GPU call time (flushed) beside the CPU baseline on the same "
-                         "workload; BASELINE pairs config 1 with the CPU path")
+                         "workload; BASELINE pairs config 1 with the CPU path (config 3: "
+                         "its B=1 x 32768 point)")
     ap.add_argument("--layout", choices=["pages", "rows"], default="pages",
                     help="K/V arena layout: page tiles (MI355X) or the reference's rows")
     ap.add_argument("--step-layers", type=int, default=28,
@@ -394,6 +395,8 @@ def config_leg(cfg, args, flush):
            "us_median": round(med * 1e3, 2), "us_mean": round(statistics.fmean(ms) * 1e3, 2),
            "GB_per_s": round(kv_bytes / (med * 1e-3) / 1e9, 2),
            "pct_hbm_peak": round(100 * kv_bytes / (med * 1e-3) / 1e9 / HBM_PEAK_GBS, 2)}
+    if w.meta.get("sharers") is not None:
+        leg["unique_kv_bytes"] = w.unique_kv_bytes()
     if not args.no_cpu:
         leg["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds / 2)
     del w, out
@@ -477,9 +480,23 @@ def published_leg(args, flush):
     return leg
 
 
-def cpu_baseline(w, budget_s):
-    """Oracle's C++ split-K restatement on a sample of sequences of the same
-    workload, all host cores; returns the dict for the JSON line."""
+def cpu_model() -> str:
+    """The host CPU's model name (Linux), for the CPU-baseline records."""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(w, budget_s, dense=False):
+    """A CPU restatement of the reference's decode path on a sample of
+    sequences of the same workload, all host cores; returns the dict for the
+    JSON line. Default: the C++ float32 split-K restatement of the Metal
+    kernel; `dense`: the C++ restatement of the portable path (gather, then
+    dense attention; float64)."""
     import numpy as np
 
     from oracle import cpu_oracle
@@ -488,12 +505,12 @@ def cpu_baseline(w, budget_s):
     q, k, v, t, n = w.numpy()
     spans = w.spans()
     per_seq = spans * w.kv_heads * w.head_dim * 4  # K+V bytes per sequence
+    fn = cpu_oracle.decode_f64 if dense else cpu_oracle.decode_splitk
     # Calibrate on one sequence, then size the sample to the budget.
     def run(idx):
         t0 = time.perf_counter()
-        cpu_oracle.decode_splitk(q[idx], k, v, t[idx], n[idx], page_size=w.page_size,
-                                 scale=w.scale, window=w.window, softcap=w.softcap,
-                                 threads=cores)
+        fn(q[idx], k, v, t[idx], n[idx], page_size=w.page_size, scale=w.scale,
+           window=w.window, softcap=w.softcap, threads=cores)
         return time.perf_counter() - t0
 
     first = np.arange(min(4, w.batch))
@@ -508,15 +525,19 @@ def cpu_baseline(w, budget_s):
         total_t += run(idx)
         total_b += int(per_seq[idx].sum())
         reps += 1
+    what = ("C++ float64 restatement of the reference's portable path (gather, then dense "
+            "attention; portable.py:155-205, batches.py:228-246), std::thread over "
+            "(sequence, head)" if dense else
+            "C++ float32 restatement of the reference split-K kernel "
+            "(metal_kernels.py:18-124), std::thread over (sequence, kv head, split)")
     return {
         "value": round(total_b / total_t / 1e9, 3),
         "unit": "GB/s",
         "cores": cores,
         "kind": "port",
         "sample": (f"first {count} of {w.batch} sequences of {w.name} "
-                   f"({int(per_seq[idx].sum())} K/V bytes) x {reps} calls; C++ float32 "
-                   "restatement of the reference split-K kernel (metal_kernels.py:18-124), "
-                   "std::thread over (sequence, kv head, split)"),
+                   f"({int(per_seq[idx].sum())} K/V bytes) x {reps} calls; {what}"),
+        "cpu_model": cpu_model(),
         "seconds": round(total_t, 2),
     }
 
@@ -694,6 +715,7 @@ def main():
     # The CPU baselines time the fp16 oracle; a bf16 run has none.
     if not args.no_cpu and args.kv_bits == 16 and not bf16:
         line["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
+        line["cpu_baseline_dense"] = cpu_baseline(w, args.cpu_seconds / 2, dense=True)
     others = [int(c) for c in args.latency_configs.split(",") if c.strip()]
     if args.kv_bits == 16 and not bf16:
         line["other_configs"] = {str(c): config_leg(c, args, flushing)
