@@ -4,7 +4,8 @@ one sequence at 261,840 tokens (K+V 1.07 GB), bf16 like the model, against
 the float64 oracle. Planted large-logit keys keep the output O(1) so that the
 absolute tolerances mean something (an average over 261,840 values would be
 ~1e-2 and hide any error). The fp16 run is held to the north-star tolerance
-(max-abs 2e-3, mean-abs 2e-4)."""
+(max-abs 2e-3, mean-abs 2e-4), and so is the 8-bit cache (against attention
+over the dequantized rows)."""
 
 import numpy as np
 import pytest
@@ -12,7 +13,8 @@ import torch
 
 from instinct_amd import workloads
 from instinct_amd.hip_kernels import paged_decode_attention
-from instinct_amd.paged_kv import pages_to_rows
+from instinct_amd.paged_kv import pages_to_rows, rows_to_pages
+from oracle import kv8
 from oracle import paged_attention as pa
 
 pytestmark = pytest.mark.gpu
@@ -62,3 +64,27 @@ def test_full_context_fixed_split_is_reproducible(gpu):
     torch.cuda.synchronize()
     # The two split plans differ only in summation order.
     assert (loose - first.float()).abs().max().item() <= 1.6e-2
+
+
+def test_full_context_8bit_cache(gpu):
+    """The same layer with the reference's 8-bit cache (int8 rows, an fp16
+    scale per row and kv head, paged_kv.py:50-55), fp16 queries: the
+    matrix-core kernel at D = 512 against float64 attention over the
+    dequantized rows, at the north star's bar."""
+    w = workloads.gemma4_global(device=gpu, dtype=torch.float16)  # rows layout
+    q, k, v, t, n = w.numpy()
+    kq, ks = kv8.quantize(k)
+    vq, vs = kv8.quantize(v)
+    want = pa.paged_decode_dense(q, kv8.dequantize(kq, ks), kv8.dequantize(vq, vs), t, n,
+                                 page_size=w.page_size, scale=w.scale)
+    P = w.page_size
+    pages = lambda x: rows_to_pages(torch.as_tensor(x, device=gpu), P)  # noqa: E731
+    scales = lambda x: torch.as_tensor(x, device=gpu).view(-1, P, 2).permute(0, 2, 1).contiguous()  # noqa: E731
+    out = paged_decode_attention(w.q, pages(kq), pages(vq), w.tables, w.lengths, page_size=P,
+                                 longest=w.longest, scale=w.scale, scales=(scales(ks), scales(vs)))
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    err_max, err_mean = pa.error_stats(got, want)
+    print(f"8-bit: max_abs={err_max:.3e} mean_abs={err_mean:.3e}", flush=True)
+    assert err_max <= 2e-3 and err_mean <= 2e-4, (err_max, err_mean)
