@@ -147,9 +147,10 @@ int pda_paged_decode_attention(const void* queries, const void* keys,
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.
  * The workspace is a static device array of 32 MiB per GPU inside the
  * library (held until the process ends), laid out for this device's grid;
- * a shape that needs more (about 2 x CUs x 8 waves x G x head_dim x 4
- * bytes: head_dim 128 with G = 8, head_dim 256 with G = 4, head_dim 512
- * with G = 2 fit on MI355X) returns PDA_ERR_WORKSPACE. Nothing in the
+ * a shape that needs more (about 2 x CUs x W x G x head_dim x 4 bytes, W
+ * the split waves per CU: 8, or 4 for the matrix-core kernels at head_dim
+ * 512; on MI355X head_dim 128 with G = 8, 256 with G = 4 and 512 with up
+ * to 7 heads per kv head fit) returns PDA_ERR_WORKSPACE. Nothing in the
  * scratch outlives a call, so it needs no clearing, but every call on one
  * GPU shares it: calls that overlap on one GPU (several streams, several
  * host threads) race and must be serialised by the caller. fp16 only;
