@@ -103,6 +103,14 @@ def parse():
     return ap.parse_args()
 
 
+def kernel_label(names):
+    """The split kernel and the merge kernel of a call (local mode: merged in
+    the split kernel's workgroups, no merge kernel)."""
+    if names["merge"] is None:
+        return f"{names['split']} (local: one workgroup per unit, merged in LDS)"
+    return f"{names['split']} + {names['merge']}"
+
+
 def merge_shape_of(w):
     """What the merge launch depends on besides the heads (row slicing)."""
     return dict(batch=w.batch, longest=w.longest, page_size=w.page_size,
@@ -391,7 +399,7 @@ def config_leg(cfg, args, flush):
     names = decode_kernel_names(w.q_heads, w.kv_heads, w.head_dim, **merge_shape_of(w))
     leg = {"workload": w.name, "batch": w.batch, "q_heads": w.q_heads,
            "kv_heads": w.kv_heads, "head_dim": w.head_dim, "kv_bytes": kv_bytes,
-           "kernel": f"{names['split']} + {names['merge']}",
+           "kernel": kernel_label(names),
            "us_median": round(med * 1e3, 2), "us_mean": round(statistics.fmean(ms) * 1e3, 2),
            "GB_per_s": round(kv_bytes / (med * 1e-3) / 1e9, 2),
            "pct_hbm_peak": round(100 * kv_bytes / (med * 1e-3) / 1e9 / HBM_PEAK_GBS, 2)}
@@ -438,7 +446,7 @@ def published_leg(args, flush):
     rate = kv_bytes / (med * 1e-3) / 1e9
     leg = {"workload": w.name, "dtype": "bf16", "batch": w.batch, "q_heads": w.q_heads,
            "kv_heads": w.kv_heads, "head_dim": w.head_dim, "context": int(args.published),
-           "kv_bytes": kv_bytes, "kernel": f"{names['split']} + {names['merge']}",
+           "kv_bytes": kv_bytes, "kernel": kernel_label(names),
            "us_median": round(med * 1e3, 2), "us_mean": round(statistics.fmean(ms) * 1e3, 2),
            "GB_per_s": round(rate, 2), "pct_hbm_peak": round(100 * rate / HBM_PEAK_GBS, 2)}
     # The same layer with the 8-bit cache (KVCache(bits=8): int8 rows, an
@@ -464,7 +472,7 @@ def published_leg(args, flush):
     bytes8 = int(w.spans().sum()) * w.kv_heads * (w.head_dim + 2) * 2
     names8 = decode_kernel_names(w.q_heads, w.kv_heads, w.head_dim, bits=8,
                                  **merge_shape_of(w))
-    leg["kv8"] = {"kernel": f"{names8['split']} + {names8['merge']}",
+    leg["kv8"] = {"kernel": kernel_label(names8),
                   "us_median": round(med8 * 1e3, 2), "kv_bytes": bytes8,
                   "GB_per_s": round(bytes8 / (med8 * 1e-3) / 1e9, 2)}
     del keys8, values8, kscale, vscale
@@ -705,8 +713,7 @@ def main():
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
             "traffic_source": f"{TRAFFIC_FILE.relative_to(ROOT)}[{traffic_key}]",
-            "kernel": f"{names['split']} + {names['merge']} (one call: split and merge, "
-                      "events around both)",
+            "kernel": kernel_label(names) + " (one call, events around it)",
             "us_mean": round(call_mean * 1e3, 2),
             "split_us_mean": round(split_mean * 1e3, 2),
             "merge_us_mean": round(statistics.fmean(merge_ms) * 1e3, 2),

@@ -42,6 +42,13 @@ constexpr float kSlack = 8.0f;
 constexpr int kSplitWaves = 8;                 // waves per split workgroup
 constexpr int kSplitThreads = kSplitWaves * 64;
 constexpr int kPairs = kSplitWaves / 2;        // wave pairs per workgroup
+// K/V steps in flight per wave (see the split kernel): two; one for the
+// matrix-core kernels at D >= 256; four for the VALU kernels at D >= 256
+// with at most 2 heads per unit.
+constexpr int ring_depth(int d, int g, bool q8, bool gen, bool mf) {
+  return mf && d >= 256 ? 1 : !mf && !q8 && !gen && d >= 256 && g <= 2 ? 4 : 2;
+}
+
 // Waves of a split workgroup: eight (two per SIMD), except the matrix-core
 // kernels at D = 512, whose 16 x 512 output accumulators, queries and
 // 32 KiB K/V steps need a whole SIMD's registers per wave (accumulators in
@@ -93,6 +100,7 @@ struct Params {
   int32_t min_pages;  // fewest pages per wave before the stream uses fewer pairs
   int32_t fixed;      // 1: each wave of a pair takes a fixed half of the range
   int32_t ragged;     // 1: page_size is not a multiple of the keys per step
+  int32_t local;      // 1: one workgroup per unit, its pieces merged in LDS (no merge pass)
   float scale_log2;   // scale * log2(e)
   float softcap;      // 0 = off
   float cap_in;       // 2 * log2(e) * scale / softcap
@@ -321,6 +329,10 @@ __device__ __forceinline__ SeqGeometry sequence_geometry(const Params& p, int b)
   return g;
 }
 
+// Local mode: ints of dynamic LDS before the pieces (the prefix and the
+// lengths, 2 B + 1 ints), rounded to 16 bytes.
+__host__ __device__ constexpr int local_lds_offset(int batch) { return (2 * batch + 1 + 3) & ~3; }
+
 // Wave pairs the stream of `total` pages is spread over (both kernels agree).
 __device__ __forceinline__ int stream_pairs(int64_t total, const Params& p) {
   if (total <= 0) return 0;
@@ -403,10 +415,8 @@ void paged_decode_kernel(const Params p) {
   // unit, whose small per-step math leaves registers free (config 4's
   // Gemma-style shape, 42.5 -> 39.7 us; depths 3 and 4 were slower on the
   // other configurations).
-  constexpr int NBUF = (MF && D >= 256)                       ? 1
-                       : (!MF && !Q8 && !GEN && D >= 256 && G <= 2) ? 4
-                                                              : kNbuf;
-  extern __shared__ int s_dyn[];
+  constexpr int NBUF = ring_depth(D, G, Q8, GEN, MF);
+  extern __shared__ __align__(16) int s_dyn[];
   __shared__ int s_ticket[kWgPairs];
   // Matrix-core kernels: each wave's V tile of one step, [16 keys][kVRow].
   constexpr int kVRow = mf_vrow(D);
@@ -467,9 +477,29 @@ void paged_decode_kernel(const Params p) {
   const int pl = w % kWgPairs;
   const bool back = w >= kWgPairs;  // takes its pair's range from the end
   const int pair = blockIdx.x * kWgPairs + pl;
-  if (pair >= npairs) return;
-  const int64_t x0 = range_start(pair, total, npairs);
-  const int n_range = (int)(range_start(pair + 1, total, npairs) - x0);
+  // Local mode (short calls): workgroup j serves unit j alone, its pages
+  // split evenly over the workgroup's pairs; the pieces go to LDS and the
+  // workgroup merges them after its last wave is done (no merge pass).
+  // Every wave reaches that barrier: a pair with no pages starts at the
+  // unit's first page and takes none.
+  const int hpu_k = MF ? p.unit_heads : G;  // heads of a unit
+  float* const s_lo = reinterpret_cast<float*>(s_dyn + local_lds_offset(B));  // [waves][hpu][D]
+  float2* const s_lml = reinterpret_cast<float2*>(s_lo + kWaves * hpu_k * D);  // [waves][hpu]
+  int64_t x0;
+  int n_range;
+  if (p.local) {
+    const int ub = blockIdx.x / nkvg;
+    const int unpg = s_prefix[ub + 1] - s_prefix[ub];
+    if (unpg == 0) return;  // the whole workgroup: zeroed above
+    const int64_t us = (int64_t)s_prefix[ub] * nkvg + (int64_t)(blockIdx.x - ub * nkvg) * unpg;
+    x0 = us + (int64_t)unpg * pl / kWgPairs;
+    n_range = (int)(us + (int64_t)unpg * (pl + 1) / kWgPairs - x0);
+    if (lane < hpu_k) s_lml[w * hpu_k + lane] = make_float2(-INFINITY, 0.0f);
+  } else {
+    if (pair >= npairs) return;
+    x0 = range_start(pair, total, npairs);
+    n_range = (int)(range_start(pair + 1, total, npairs) - x0);
+  }
   const int dir = back ? -1 : 1;
   const int64_t vw = 2 * (int64_t)pair + (back ? 1 : 0);  // slots 2 vw, 2 vw + 1
 
@@ -494,7 +524,7 @@ void paged_decode_kernel(const Params p) {
 
   // Unit holding the first page this wave would take: the last b with
   // nkvg * prefix[b] <= x (never an empty sequence, since x < total).
-  const int64_t xs = back ? x0 + n_range - 1 : x0;
+  const int64_t xs = back && n_range > 0 ? x0 + n_range - 1 : x0;
   int b = 0;
   {
     int lo = 0, hi = B - 1;
@@ -1214,7 +1244,7 @@ void paged_decode_kernel(const Params p) {
       lt += __shfl_xor(lt, 16);
       lt += __shfl_xor(lt, 32);
       const int head = lane & 15;
-      if (cnt == npg) {
+      if (cnt == npg && !p.local) {
         if (head < hpu) {  // the whole unit: normalise and write
           const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
           f16* const dst = p.out + ((int64_t)b * p.hq + h0 + head) * D + 4 * mg;
@@ -1233,14 +1263,15 @@ void paged_decode_kernel(const Params p) {
         }
       } else if (head < hpu) {
         // Cut unit: the unnormalised partial, slot chosen as below.
+        // (Local mode: this wave's LDS slot.)
         const bool holds_start = back ? !pending : first_unit;
-        const int64_t slot = 2 * vw + (holds_start ? 0 : 1);
-        float* const dst = p.part_o + (slot * hpu + head) * D + 4 * mg;
+        const int64_t slot = p.local ? w : 2 * vw + (holds_start ? 0 : 1);
+        float* const dst = (p.local ? s_lo : p.part_o) + (slot * hpu + head) * D + 4 * mg;
 #pragma unroll
         for (int i = 0; i < D / 16; ++i)
           *reinterpret_cast<float4*>(dst + 16 * i) =
               make_float4(ob[i][0], ob[i][1], ob[i][2], ob[i][3]);
-        if (mg == 0) p.part_ml[slot * hpu + head] = make_float2(m[0], lt);
+        if (mg == 0) (p.local ? s_lml : p.part_ml)[slot * hpu + head] = make_float2(m[0], lt);
       }
     } else {
     // Fold the wave's key subsets (metal_kernels.py:63-81); every lane then
@@ -1265,7 +1296,7 @@ void paged_decode_kernel(const Params p) {
         for (int i = 0; i < OPL; ++i) o[g][i] = subset_sum<R>(o[g][i]);
       }
     }
-    if (cnt == npg) {
+    if (cnt == npg && !p.local) {
       // The whole unit is here: normalise and write (metal_kernels.py:87-91).
 #pragma unroll
       for (int g = 0; g < G; ++g) {
@@ -1305,17 +1336,19 @@ void paged_decode_kernel(const Params p) {
       // Cut unit: unnormalised partial (metal_kernels.py:93-101) in slot 0 if
       // the unit holds the first page of this wave's final range (the first
       // wave's first unit, the second wave's last), else in slot 1.
+      // (Local mode: this wave's LDS slot.)
       const bool holds_start = back ? !pending : first_unit;
-      const int64_t slot = 2 * vw + (holds_start ? 0 : 1);
+      const int64_t slot = p.local ? w : 2 * vw + (holds_start ? 0 : 1);
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         if (g % kWriters != writer || !writes) continue;
-        float* dst = p.part_o + (slot * G + g) * D + e0;
+        float* dst = (p.local ? s_lo : p.part_o) + (slot * G + g) * D + e0;
 #pragma unroll
         for (int i = 0; i < OPL; i += 4)
           *reinterpret_cast<float4*>(dst + estride * (i / 8) + i % 8) =
               make_float4(o[g][i], o[g][i + 1], o[g][i + 2], o[g][i + 3]);
-        if ((PV2 ? r2 : r) == 0) p.part_ml[slot * G + g] = make_float2(m[g], l[g]);
+        if ((PV2 ? r2 : r) == 0)
+          (p.local ? s_lml : p.part_ml)[slot * G + g] = make_float2(m[g], l[g]);
       }
     }
     }  // not MF
@@ -1345,8 +1378,42 @@ void paged_decode_kernel(const Params p) {
       pa = npg - 1;
     }
   }
-  // The first wave of the pair records the meeting point for the merge.
-  if (!back && lane == 0) p.meet[pair] = taken;
+  if (!p.local) {
+    // The first wave of the pair records the meeting point for the merge.
+    if (!back && lane == 0) p.meet[pair] = taken;
+    return;
+  }
+  // Local mode: the workgroup's unit from its waves' pieces, the same
+  // log-sum-exp merge as the merge kernel (metal_kernels.py:103-124), waves
+  // folded in a fixed order.
+  __syncthreads();
+  const int ub = blockIdx.x / nkvg;
+  const int ukvg = blockIdx.x - ub * nkvg;
+  const int ukvh = ukvg / p.nhg;
+  const int uh0 = ukvh * p.gtot + (ukvg - ukvh * p.nhg) * hpu_k;
+  for (int i = tid; i < hpu_k * D; i += kThreads) {
+    const int head = i / D;
+    const int d = i - head * D;
+    if (d >= hd) continue;
+    float top = -INFINITY;
+    for (int x = 0; x < kWaves; ++x) top = fmaxf(top, s_lml[x * hpu_k + head].x);
+    float sum = 0.0f, acc = 0.0f;
+    if (top != -INFINITY) {
+      for (int x = 0; x < kWaves; ++x) {
+        const float2 ml = s_lml[x * hpu_k + head];
+        if (ml.x == -INFINITY) continue;
+        const float wt = __builtin_amdgcn_exp2f(ml.x - top);
+        sum = __builtin_fmaf(wt, ml.y, sum);
+        acc = __builtin_fmaf(wt, s_lo[(x * hpu_k + head) * D + d], acc);
+      }
+    }
+    const float y = sum > 0.0f ? acc / sum : 0.0f;
+    f16* const dst = p.out + ((int64_t)ub * p.hq + uh0 + head) * hd + d;
+    if constexpr (BF)
+      *dst = __builtin_bit_cast(f16, (bf16)y);
+    else
+      *dst = (f16)y;
+  }
 }
 
 // The pieces of one unit for the merge kernels. The unit's pages [s, e) of
@@ -1621,12 +1688,14 @@ struct KernelPair {
   KernelFn merge = nullptr;
   KernelFn merge_sliced = nullptr;  // one 64-element slice per workgroup
   int split_waves = kSplitWaves;    // waves of a split workgroup
+  int ring = kNbuf;                 // K/V steps in flight per wave
 };
 
 template <int D, int G, bool Q8, bool BF, bool GEN = false, bool MF = false>
 KernelPair make_pair() {
   return {paged_decode_kernel<D, G, Q8, BF, GEN, MF>, paged_decode_merge_kernel<D, G, BF, GEN>,
-          paged_decode_merge_sliced_kernel<D, G, BF, GEN>, split_waves(D, MF)};
+          paged_decode_merge_sliced_kernel<D, G, BF, GEN>, split_waves(D, MF),
+          ring_depth(D, G, Q8, GEN, MF)};
 }
 
 template <int D, bool Q8, bool BF, bool GEN = false>

@@ -320,6 +320,45 @@ MergeShape merge_shape(const Plan& pl, int dim, int grid_pairs, int64_t heads) {
           (int)std::max<int64_t>(1, std::min<int64_t>(kMergeMaxWaves, mw))};
 }
 
+// Local mode: one split workgroup per unit, its waves' pieces merged in
+// LDS at the end, no merge pass. It saves the merge's launch, its gap
+// after the split kernel and its dependent loads (~6.5 us between events),
+// but a unit's pages go to one workgroup's waves instead of being spread
+// over the whole GPU, so it is chosen where that costs a wave few more
+// pages than the stream gives it, scaled by the steps its ring keeps in
+// flight (ring / 4 x 2.5 times): config 4's windows with the 4-deep VALU
+// ring (128 units of ~65 pages: 8 pages a wave against 4; 39.8 -> 37.2 us),
+// not at 8 bits (the 1-deep matrix-core ring: 31.6 -> 33.3 us) nor config 1
+// (16 units of 65 pages: 8 against 0.5; 17.5 -> 18.1 us). At most
+// kLocalMaxUnits units of at most kLocalMaxUnitBytes of K/V each (from
+// `longest`), pieces within kLocalMaxLds bytes of LDS. PDA_DECODE_LOCAL=0/1
+// forces the choice where the pieces fit (for measurements). Returns the
+// dynamic LDS bytes of the local kernel launch, or 0 for the stream.
+constexpr int64_t kLocalMaxUnits = 512;
+constexpr int64_t kLocalMaxUnitBytes = int64_t(3) << 19;  // 1.5 MiB
+constexpr size_t kLocalMaxLds = size_t(64) << 10;
+
+size_t local_lds(const Plan& pl, int batch, int kv_heads, int dim, int elem, int page_size,
+                 int waves, int ring, int grid_pairs) {
+  const size_t lds = (size_t)pda_decode::local_lds_offset(batch) * sizeof(int32_t) +
+                     (size_t)waves * pl.unit_heads * (dim * sizeof(float) + sizeof(float2));
+  if (lds > kLocalMaxLds) return 0;
+  static const int force = [] {
+    const char* e = getenv("PDA_DECODE_LOCAL");
+    return e && *e ? atoi(e) : -1;
+  }();
+  if (force >= 0) return force > 0 ? lds : 0;
+  const int64_t units = (int64_t)batch * kv_heads * pl.nhg;
+  const int64_t unit_bytes = pl.unit_pages_max * page_size * (int64_t)dim * elem * 2;
+  // Pages a wave takes: unit_pages_max / waves here, pages_est / (2 pairs)
+  // in the stream.
+  const int64_t pairs = std::max<int64_t>(
+      1, std::min<int64_t>(grid_pairs, (pl.pages_est + 2 * pl.min_pages - 1) /
+                                           (2 * pl.min_pages)));
+  const bool short_waves = 16 * pl.unit_pages_max * pairs <= 5 * ring * waves * pl.pages_est;
+  return units <= kLocalMaxUnits && unit_bytes <= kLocalMaxUnitBytes && short_waves ? lds : 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -535,6 +574,10 @@ int decode(int passes, const void* queries, const void* keys, const void* values
   prm.grid_pairs = groups * wg_pairs;
   prm.min_pages = pl.min_pages;
   prm.fixed = (flags & PDA_DECODE_FIXED_SPLIT) ? 1 : 0;
+  const int dim = pl.mf ? head_dim : kernel_dim(head_dim, q8);  // the partials' row length
+  const size_t lds_local = local_lds(pl, batch, kv_heads, dim, elem, page_size,
+                                     kp.split_waves, kp.ring, groups * wg_pairs);
+  prm.local = lds_local > 0 ? 1 : 0;
   prm.ragged = page_size % (pl.mf ? 16 : keys_per_step(head_dim, q8)) ? 1 : 0;
   prm.scale_log2 = scale * kLog2e;
   prm.softcap = softcap;
@@ -544,13 +587,15 @@ int decode(int passes, const void* queries, const void* keys, const void* values
   const hipStream_t st = static_cast<hipStream_t>(stream);
   void* args[] = {&prm};
   hipError_t err = hipSuccess;
-  if (passes & kPassSplit)
-    err = hipLaunchKernel(reinterpret_cast<const void*>(kp.split), dim3(groups),
-                          dim3(64 * kp.split_waves), args, lds, st);
-  if (err == hipSuccess && (passes & kPassMerge)) {
+  if (passes & kPassSplit) {
+    // Local mode: a workgroup per unit (the merge happens inside it).
+    const unsigned grid = prm.local ? (unsigned)(batch * kv_heads * pl.nhg) : (unsigned)groups;
+    err = hipLaunchKernel(reinterpret_cast<const void*>(kp.split), dim3(grid),
+                          dim3(64 * kp.split_waves), args, prm.local ? lds_local : lds, st);
+  }
+  if (err == hipSuccess && (passes & kPassMerge) && !prm.local) {
     const int heads = kv_heads * pl.nhg * pl.unit_heads;
-    const MergeShape ms = merge_shape(pl, pl.mf ? head_dim : kernel_dim(head_dim, q8),
-                                      prm.grid_pairs, (int64_t)heads * batch);
+    const MergeShape ms = merge_shape(pl, dim, prm.grid_pairs, (int64_t)heads * batch);
     err = hipLaunchKernel(reinterpret_cast<const void*>(ms.sliced ? kp.merge_sliced : kp.merge),
                           dim3(heads * ms.slices, batch), dim3(64 * ms.waves), args, 0, st);
   }

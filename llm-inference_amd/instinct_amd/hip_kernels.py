@@ -87,16 +87,47 @@ _MERGE_SLICED_ROUND = 64
 _MERGE_SLICED_MAX_GROUPS = 4096
 
 
+# Local mode (csrc/pda_kernels.hip ``local_lds``): a workgroup per unit, no
+# merge pass, for at most 512 units of at most 1.5 MiB of K/V, pieces within
+# 64 KiB of LDS.
+_LOCAL_MAX_UNITS = 512
+_LOCAL_MAX_UNIT_BYTES = 3 << 19
+_LOCAL_MAX_LDS = 64 << 10
+
+
+def _unit_pages_max(longest, page_size, table_width, window) -> int:
+    """Visible pages of one unit at most (``make_plan``'s estimate)."""
+    pages_max = table_width
+    if window > 0:
+        pages_max = min(pages_max, (window - 1) // page_size + 2)
+    if longest > 0:
+        pages_max = min(pages_max, -(-longest // page_size) + 1)
+    return pages_max
+
+
+def _local(dim, heads, units, *, batch, longest, page_size, table_width, window, elem,
+           waves, ring, grid_pairs, split_pages=0) -> bool:
+    """Whether the call runs in local mode: the library's rule."""
+    lds = ((2 * batch + 1 + 3) & ~3) * 4 + waves * heads * (dim * 4 + 8)
+    if lds > _LOCAL_MAX_LDS:
+        return False
+    force = os.environ.get("PDA_DECODE_LOCAL", "")
+    if force:
+        return int(force) > 0
+    est = _unit_pages_max(longest, page_size, table_width, window)
+    pages_est = batch * units * est
+    min_pages = split_pages if split_pages > 0 else 1
+    pairs = max(1, min(grid_pairs, -(-pages_est // (2 * min_pages))))
+    return (batch * units <= _LOCAL_MAX_UNITS
+            and est * page_size * dim * elem * 2 <= _LOCAL_MAX_UNIT_BYTES
+            and 16 * est * pairs <= 5 * ring * waves * pages_est)
+
+
 def _merge_sliced(dim, heads, units, *, batch, longest, page_size, table_width, window,
                   split_pages, grid_pairs=_GRID_PAIRS) -> bool:
     """Whether the merge runs row-sliced (one 64-element slice of a head per
     workgroup): the library's rule, from the same page estimates."""
-    pages_max = table_width
-    if window > 0:
-        pages_max = min(pages_max, (window - 1) // page_size + 2)
-    est = pages_max
-    if longest > 0:
-        est = min(est, -(-longest // page_size) + 1)
+    est = _unit_pages_max(longest, page_size, table_width, window)
     pages_est = batch * units * est
     min_pages = split_pages if split_pages > 0 else 1
     pairs = max(1, min(grid_pairs, -(-pages_est // (2 * min_pages))))
@@ -119,8 +150,9 @@ def decode_kernel_names(q_heads: int, kv_heads: int, head_dim: int, *, bits: int
     ``<D, G, Q8, BF, GEN, MF>`` of the split kernel and ``<D, G, BF, GEN>`` of
     the merge kernel (or its row-sliced form), whether the matrix cores run it, the query
     heads one unit serves and the units per kv head (each reads the kv
-    head's K/V once). The merge's row slicing depends on the batch, the
-    longest length and the table width (``batch`` 0: not sliced)."""
+    head's K/V once). Local mode (a workgroup per unit, merged in LDS, no
+    merge kernel: ``merge`` None) and the merge's row slicing depend on the
+    batch, the longest length and the table width (``batch`` 0: neither)."""
     group = q_heads // kv_heads
     min_mf = (int(os.environ.get("PDA_MFMA_MIN_GROUP", "0") or 0)
               or ((4 if bits == 8 else 1) if head_dim == 512 else _MF_MIN_GROUP[bits]))
@@ -131,15 +163,28 @@ def decode_kernel_names(q_heads: int, kv_heads: int, head_dim: int, *, bits: int
     dim = max(8, 1 << (head_dim - 1).bit_length()) if generic else head_dim
     slots = 16 if mf else heads
     units = kv_heads * (group // heads)
-    sliced = batch > 0 and _merge_sliced(
+    width = table_width or -(-max(longest, 1) // page_size)
+    four_wave = mf and dim == 512
+    # K/V steps in flight per wave (pda_decode.h ring_depth).
+    ring = (1 if mf and dim >= 256 else
+            4 if not mf and bits == 16 and not generic and dim >= 256 and heads <= 2 else 2)
+    local = batch > 0 and _local(
+        dim, heads, units, batch=batch, longest=longest, page_size=page_size,
+        table_width=width, window=window, elem=1 if bits == 8 else 2,
+        waves=4 if four_wave else 8, ring=ring,
+        grid_pairs=_GRID_PAIRS // 2 if four_wave else _GRID_PAIRS,
+        split_pages=split_pages)
+    sliced = batch > 0 and not local and _merge_sliced(
         dim, units * heads, units, batch=batch, longest=longest, page_size=page_size,
-        table_width=table_width or -(-max(longest, 1) // page_size), window=window,
-        split_pages=split_pages, grid_pairs=_GRID_PAIRS // 2 if mf and dim == 512 else _GRID_PAIRS)
+        table_width=width, window=window, split_pages=split_pages,
+        grid_pairs=_GRID_PAIRS // 2 if four_wave else _GRID_PAIRS)
     b = lambda x: str(bool(x)).lower()  # noqa: E731
     targs = f"{dim},{slots},{b(bits == 8)},{b(bf16)},{b(generic)},{b(mf)}"
     return {"split": f"paged_decode_kernel<{targs}>",
-            "merge": (f"paged_decode_merge{'_sliced' if sliced else ''}_kernel<{dim},{slots},"
+            "merge": (None if local else
+                      f"paged_decode_merge{'_sliced' if sliced else ''}_kernel<{dim},{slots},"
                       f"{b(bf16)},{b(generic)}>"),
+            "local": local,
             "merge_row_sliced": sliced,
             "matrix_cores": mf, "heads_per_unit": heads,
             "head_groups_per_kv_head": group // heads}
