@@ -171,7 +171,10 @@ int pda_paged_decode_attention_noalloc(const void* queries, const void* keys,
  * time them separately; the reference's host wrapper launches the same two
  * kernels (metal_kernels.py:228-239 split, :240-247 merge). Call
  * pda_decode_split, then pda_decode_merge with the same arguments on the same
- * stream (or after it); the output is complete only after the merge. */
+ * stream (or after it); the output is complete only after the merge. Calls
+ * of few, short units run in one pass (a workgroup per unit, merged inside
+ * it): their split pass writes the output and their merge pass launches
+ * nothing. */
 int pda_decode_split(const void* queries, const void* keys, const void* values,
                      const int32_t* tables, const int32_t* lengths, void* out,
                      int32_t batch, int32_t q_heads, int32_t kv_heads,
