@@ -39,9 +39,7 @@ typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 constexpr float kLog2e = 1.44269504088896340736f;
 // Lazy rescale threshold (log2 units): probabilities stay below 2^8.
 constexpr float kSlack = 8.0f;
-constexpr int kSplitWaves = 8;                 // waves per split workgroup
-constexpr int kSplitThreads = kSplitWaves * 64;
-constexpr int kPairs = kSplitWaves / 2;        // wave pairs per workgroup
+constexpr int kSplitWaves = 8;                 // waves per split workgroup (but see split_waves)
 // K/V steps in flight per wave (see the split kernel): two; one for the
 // matrix-core kernels at D >= 256; four for the VALU kernels at D >= 256
 // with at most 2 heads per unit.
