@@ -59,8 +59,13 @@ def parse():
                          "tables and K/V with a larger or smaller GQA group, for the "
                          "matrix-core vs VALU study")
     ap.add_argument("--split-pages", type=int, default=0)
-    ap.add_argument("--deterministic", action="store_true",
-                    help="fixed split points (PDA_DECODE_FIXED_SPLIT): bitwise reproducible")
+    ap.add_argument("--deterministic", action="store_true", default=True,
+                    help="fixed split points (PDA_DECODE_FIXED_SPLIT; the default): bitwise "
+                         "reproducible output")
+    ap.add_argument("--racing", dest="deterministic", action="store_false",
+                    help="racing wave pairs instead of fixed split points: the two waves of "
+                         "a pair meet wherever their shared counter runs out (output bits may "
+                         "differ between calls)")
     ap.add_argument("--latency-configs", default="1,3,4,5",
                     help="other configs timed in the same run, comma-separated ('' = none): "
                          "GPU call time (flushed) beside the CPU baseline on the same "
@@ -669,8 +674,7 @@ def main():
                          int(w.tables.shape[1]), w.longest, w.window, args.split_pages)
     names = decode_kernel_names(w.q_heads, w.kv_heads, w.head_dim, bits=args.kv_bits,
                                 bf16=bf16, split_pages=args.split_pages, **merge_shape_of(w))
-    traffic_key = (f"{w.name}/{w.layout}/{'bf16' if bf16 else 'f16'}/kv{args.kv_bits}"
-                   f"{'/fixed' if args.deterministic else ''}")
+    traffic_key = f"{w.name}/{w.layout}/{'bf16' if bf16 else 'f16'}/kv{args.kv_bits}"
     traffic = None
     if TRAFFIC_FILE.exists():
         traffic = json.loads(TRAFFIC_FILE.read_text()).get(traffic_key, {}).get(

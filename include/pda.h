@@ -104,6 +104,39 @@ int pda_plan(int32_t batch, int32_t q_heads, int32_t kv_heads,
              int32_t longest, int32_t window, int32_t split_pages,
              int32_t* waves, int32_t* pages_per_wave);
 
+/* What a decode call of this shape launches, as the library's own dispatch
+ * chooses it: for labels, profiles and measurements (no reference
+ * counterpart; the reference's wrapper picks its kernels inline,
+ * metal_kernels.py:193-247). The arguments are those of the decode call
+ * (`kv_bits` 16 or 8, `bf16` 1 for bf16 queries with 16-bit K/V); the split
+ * grid is the current device's, or MI355X's 256 workgroups when no device is
+ * visible. Local mode (`local` 1) and the merge shape depend on `batch`,
+ * `longest` and the table width as the call's do. */
+typedef struct pda_decode_info {
+  int32_t kernel_dim;        /* D: head_dim, or the generic kernel's width     */
+  int32_t head_slots;        /* G: head slots of a unit (16 on matrix cores)   */
+  int32_t kv_bits;           /* 16 or 8                                        */
+  int32_t bf16;              /* 1: bf16 queries, K/V and output                */
+  int32_t generic;           /* 1: generic kernel (head dim without its own)   */
+  int32_t matrix_cores;      /* 1: S and O products on the matrix cores        */
+  int32_t unit_heads;        /* query heads one K/V read serves                */
+  int32_t units_per_kv_head; /* units (head groups) per kv head                */
+  int32_t split_waves;       /* waves per split workgroup                      */
+  int32_t ring;              /* K/V steps in flight per wave                   */
+  int32_t grid_groups;       /* split workgroups of a stream-mode launch       */
+  int32_t local;             /* 1: a workgroup per unit, merged in LDS         */
+  int32_t merge;             /* 0: none (local), 1: whole-row, 2: row-sliced   */
+  int32_t merge_waves;       /* waves per merge workgroup                      */
+  char split_kernel[96];     /* the split kernel's name and template arguments */
+  char merge_kernel[96];     /* the merge kernel's ("" in local mode)          */
+} pda_decode_info;
+
+int pda_decode_describe(int32_t batch, int32_t q_heads, int32_t kv_heads,
+                        int32_t head_dim, int32_t page_size,
+                        int32_t table_stride, int32_t longest, int32_t window,
+                        int32_t split_pages, int32_t kv_bits, int32_t bf16,
+                        pda_decode_info* info);
+
 /* Paged decode attention for one new token per sequence.
  * Replaces paged_decode_attention (metal_kernels.py:164-248): same inputs and
  * meaning. `scale` multiplies q.k; `softcap` > 0 applies

@@ -97,6 +97,7 @@ struct Params {
   int32_t grid_pairs; // wave pairs of the split kernel's grid
   int32_t min_pages;  // fewest pages per wave before the stream uses fewer pairs
   int32_t fixed;      // 1: each wave of a pair takes a fixed half of the range
+  int32_t balance;    // fixed mode: the wave that is behind its partner raises its priority
   int32_t ragged;     // 1: page_size is not a multiple of the keys per step
   int32_t local;      // 1: one workgroup per unit, its pieces merged in LDS (no merge pass)
   float scale_log2;   // scale * log2(e)
@@ -416,6 +417,7 @@ void paged_decode_kernel(const Params p) {
   constexpr int NBUF = ring_depth(D, G, Q8, GEN, MF);
   extern __shared__ __align__(16) int s_dyn[];
   __shared__ int s_ticket[kWgPairs];
+  __shared__ int s_prog[kWaves];  // fixed mode: pages each wave has started
   // Matrix-core kernels: each wave's V tile of one step, [16 keys][kVRow].
   constexpr int kVRow = mf_vrow(D);
   __shared__ __align__(16) f16 s_vt[MF ? kWaves * 16 * kVRow : 1];
@@ -454,6 +456,7 @@ void paged_decode_kernel(const Params p) {
   constexpr int kElem = Q8 ? 1 : 2;  // bytes per K/V element
 
   if (tid < kWgPairs) s_ticket[tid] = 0;
+  if (tid < kWaves) s_prog[tid] = 0;
   build_prefix<kThreads>(p, s_prefix, s_len);  // ends with a barrier
   if (blockIdx.x == 0)
     for (int i = tid; i <= B; i += kThreads) p.prefix[i] = s_prefix[i];
@@ -510,12 +513,31 @@ void paged_decode_kernel(const Params p) {
   // where units are cut, and with it every output bit, depends on the
   // inputs and the grid only (the reference's split ranges are fixed too,
   // metal_kernels.py:32-36). The shared counter is still bumped by 0.
+  //
+  // The SIMD's issue arbiter favours the older wave of a pair, so with fixed
+  // halves one wave would finish early and idle. With p.balance the waves
+  // publish the pages they have started in LDS, and at each page the wave
+  // that is behind its partner (in fractions of their halves, as seen one
+  // page earlier) raises its issue priority (s_setprio 1), the other lowers
+  // it; this moves only timing, never a cut point.
   const int quota = p.fixed ? (back ? n_range - n_range / 2 : n_range / 2) : n_range;
+  const int partner_quota = n_range - quota;
+  const int partner = back ? w - kWgPairs : w + kWgPairs;
   int own_tickets = 0;
+  int seen = 0;  // the partner's pages, read at the previous ticket
   auto take_ticket = [&]() -> int {
     const int shared = __hip_atomic_fetch_add(&s_ticket[pl], (lane == 0 && !p.fixed) ? 1 : 0,
                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     const int own = own_tickets++;
+    if (p.fixed && p.balance) {
+      if ((int64_t)own * partner_quota < (int64_t)uniform(seen) * quota)
+        __builtin_amdgcn_s_setprio(1);
+      else
+        __builtin_amdgcn_s_setprio(0);
+      __hip_atomic_fetch_add(&s_prog[w], lane == 0 ? 1 : 0, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_WORKGROUP);
+      seen = __hip_atomic_load(&s_prog[partner], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
     return p.fixed ? own : shared;
   };
   auto granted = [&](int t) -> bool { return uniform(t) < quota; };
@@ -1687,13 +1709,20 @@ struct KernelPair {
   KernelFn merge_sliced = nullptr;  // one 64-element slice per workgroup
   int split_waves = kSplitWaves;    // waves of a split workgroup
   int ring = kNbuf;                 // K/V steps in flight per wave
+  // The split kernel's template arguments <D, G, Q8, BF, GEN, MF> (the
+  // merge kernels take <D, G, BF, GEN>), as instantiated.
+  int d = 0, g = 0;
+  bool q8 = false, bf = false, gen = false, mf = false;
 };
 
 template <int D, int G, bool Q8, bool BF, bool GEN = false, bool MF = false>
 KernelPair make_pair() {
-  return {paged_decode_kernel<D, G, Q8, BF, GEN, MF>, paged_decode_merge_kernel<D, G, BF, GEN>,
-          paged_decode_merge_sliced_kernel<D, G, BF, GEN>, split_waves(D, MF),
-          ring_depth(D, G, Q8, GEN, MF)};
+  return {paged_decode_kernel<D, G, Q8, BF, GEN, MF>,
+          paged_decode_merge_kernel<D, G, BF, GEN>,
+          paged_decode_merge_sliced_kernel<D, G, BF, GEN>,
+          split_waves(D, MF),
+          ring_depth(D, G, Q8, GEN, MF),
+          D, G, Q8, BF, GEN, MF};
 }
 
 template <int D, bool Q8, bool BF, bool GEN = false>

@@ -57,6 +57,7 @@
 #include <stddef.h>
 #include <stdint.h>
 #include <stdio.h>
+#include <string.h>
 #include <utility>
 
 #include "pda.h"
@@ -455,6 +456,44 @@ WorkspaceLayout workspace_layout(int batch, int G, int dim, int64_t pairs, int64
   return w;
 }
 
+// What a call launches: the kernels (the library's dispatch), the split
+// grid, the local-mode choice and the merge shape. The grid comes from the
+// current device's occupancy query; without a device (`need_device` false,
+// pda_decode_describe) it is MI355X's: one split workgroup on each of 256
+// CUs.
+struct LaunchPlan {
+  KernelPair kp;
+  int groups = 0;          // split workgroups
+  int dim = 0;             // the partials' row length
+  size_t lds = 0;          // dynamic LDS of a stream-mode split launch
+  size_t lds_local = 0;    // dynamic LDS of a local-mode launch, 0: stream mode
+  MergeShape ms{false, 1, 1};
+};
+
+int plan_launch(const Plan& pl, int32_t batch, int32_t kv_heads, int32_t head_dim,
+                int32_t page_size, bool q8, bool bf16, bool need_device, LaunchPlan* out) {
+  LaunchPlan lp;
+  lp.kp = pl.mf ? (head_dim == 512 ? kernels_mf512(q8, bf16)
+                   : q8 ? kernels_mf_q8(head_dim)
+                        : kernels_mf(head_dim, bf16))
+                : kernels_for(head_dim, pl.G, q8, bf16);
+  if (!lp.kp.split) return fail(PDA_ERR_HEAD_DIM, "head_dim %d has no kernel", head_dim);
+  lp.lds = (size_t)(2 * batch + 1) * sizeof(int32_t);
+  lp.groups = resident_groups(lp.kp.split, 64 * lp.kp.split_waves, lp.lds);
+  if (lp.groups < 0) {
+    if (need_device) return fail(PDA_ERR_HIP, "device query failed");
+    lp.groups = 256;
+  }
+  const int grid_pairs = lp.groups * (lp.kp.split_waves / 2);
+  lp.dim = pl.mf ? head_dim : kernel_dim(head_dim, q8);
+  lp.lds_local = local_lds(pl, batch, kv_heads, lp.dim, q8 ? 1 : 2, page_size,
+                           lp.kp.split_waves, lp.kp.ring, grid_pairs);
+  const int heads = kv_heads * pl.nhg * pl.unit_heads;
+  lp.ms = merge_shape(pl, lp.dim, grid_pairs, (int64_t)heads * batch);
+  *out = lp;
+  return PDA_OK;
+}
+
 // Validates, plans and launches the split pass, the merge pass or both.
 // key_scales / value_scales non-null: 8-bit K/V (int8 arenas); bf16: q, K/V
 // and out in bf16 instead of fp16.
@@ -503,15 +542,13 @@ int decode(int passes, const void* queries, const void* keys, const void* values
       return fail(PDA_ERR_ALIGNMENT, "workspace must be 256-byte aligned");
   }
 
-  const KernelPair kp = pl.mf ? (head_dim == 512 ? kernels_mf512(q8, bf16)
-                                 : q8 ? kernels_mf_q8(head_dim)
-                                      : kernels_mf(head_dim, bf16))
-                              : kernels_for(head_dim, pl.G, q8, bf16);
-  if (!kp.split) return fail(PDA_ERR_HEAD_DIM, "head_dim %d has no kernel", head_dim);
-  const size_t lds = (size_t)(2 * batch + 1) * sizeof(int32_t);
+  LaunchPlan lp;
+  rc = plan_launch(pl, batch, kv_heads, head_dim, page_size, q8, bf16, true, &lp);
+  if (rc) return rc;
+  const KernelPair& kp = lp.kp;
+  const size_t lds = lp.lds;
   const int wg_pairs = kp.split_waves / 2;
-  const int groups = resident_groups(kp.split, 64 * kp.split_waves, lds);
-  if (groups < 0) return fail(PDA_ERR_HIP, "device query failed");
+  const int groups = lp.groups;
 
   // Caller's workspace: the layout pda_workspace_bytes sizes (any grid).
   // Scratch: the same layout packed for this device's grid and this call's
@@ -574,9 +611,12 @@ int decode(int passes, const void* queries, const void* keys, const void* values
   prm.grid_pairs = groups * wg_pairs;
   prm.min_pages = pl.min_pages;
   prm.fixed = (flags & PDA_DECODE_FIXED_SPLIT) ? 1 : 0;
-  const int dim = pl.mf ? head_dim : kernel_dim(head_dim, q8);  // the partials' row length
-  const size_t lds_local = local_lds(pl, batch, kv_heads, dim, elem, page_size,
-                                     kp.split_waves, kp.ring, groups * wg_pairs);
+  static const int balance = [] {
+    const char* e = getenv("PDA_FIXED_BALANCE");
+    return e && *e ? atoi(e) : 1;
+  }();
+  prm.balance = balance;
+  const size_t lds_local = lp.lds_local;
   prm.local = lds_local > 0 ? 1 : 0;
   prm.ragged = page_size % (pl.mf ? 16 : keys_per_step(head_dim, q8)) ? 1 : 0;
   prm.scale_log2 = scale * kLog2e;
@@ -595,7 +635,7 @@ int decode(int passes, const void* queries, const void* keys, const void* values
   }
   if (err == hipSuccess && (passes & kPassMerge) && !prm.local) {
     const int heads = kv_heads * pl.nhg * pl.unit_heads;
-    const MergeShape ms = merge_shape(pl, dim, prm.grid_pairs, (int64_t)heads * batch);
+    const MergeShape& ms = lp.ms;
     err = hipLaunchKernel(reinterpret_cast<const void*>(ms.sliced ? kp.merge_sliced : kp.merge),
                           dim3(heads * ms.slices, batch), dim3(64 * ms.waves), args, 0, st);
   }
@@ -635,6 +675,51 @@ extern "C" {
       batch, q_heads, kv_heads, head_dim, page_size, table_stride, arena_rows, \
       layout, longest, scale, window, softcap, split_pages, flags, workspace,  \
       workspace_bytes, stream
+
+int pda_decode_describe(int32_t batch, int32_t q_heads, int32_t kv_heads, int32_t head_dim,
+                        int32_t page_size, int32_t table_stride, int32_t longest,
+                        int32_t window, int32_t split_pages, int32_t kv_bits, int32_t bf16,
+                        pda_decode_info* info) {
+  if (!info) return fail(PDA_ERR_INVALID_ARGUMENT, "info is null");
+  if (kv_bits != 16 && kv_bits != 8)
+    return fail(PDA_ERR_INVALID_ARGUMENT, "kv_bits must be 16 or 8, got %d", kv_bits);
+  if (bf16 && kv_bits == 8)
+    return fail(PDA_ERR_INVALID_ARGUMENT, "8-bit K/V takes fp16 queries");
+  const bool q8 = kv_bits == 8;
+  Plan pl;
+  int rc = make_plan(batch, q_heads, kv_heads, head_dim, page_size, table_stride, longest,
+                     window, split_pages, &pl, q8);
+  if (rc) return rc;
+  LaunchPlan lp;
+  rc = plan_launch(pl, std::max(batch, 1), kv_heads, head_dim, page_size, q8, bf16 != 0, false,
+                   &lp);
+  if (rc) return rc;
+  const KernelPair& kp = lp.kp;
+  pda_decode_info d;
+  memset(&d, 0, sizeof(d));
+  d.kernel_dim = kp.d;
+  d.head_slots = kp.g;
+  d.kv_bits = kv_bits;
+  d.bf16 = kp.bf;
+  d.generic = kp.gen;
+  d.matrix_cores = kp.mf;
+  d.unit_heads = pl.unit_heads;
+  d.units_per_kv_head = pl.nhg;
+  d.split_waves = kp.split_waves;
+  d.ring = kp.ring;
+  d.grid_groups = lp.groups;
+  d.local = lp.lds_local > 0;
+  d.merge = d.local ? 0 : lp.ms.sliced ? 2 : 1;
+  d.merge_waves = d.local ? 0 : lp.ms.waves;
+  auto tf = [](bool x) { return x ? "true" : "false"; };
+  snprintf(d.split_kernel, sizeof(d.split_kernel), "paged_decode_kernel<%d,%d,%s,%s,%s,%s>",
+           kp.d, kp.g, tf(kp.q8), tf(kp.bf), tf(kp.gen), tf(kp.mf));
+  if (!d.local)
+    snprintf(d.merge_kernel, sizeof(d.merge_kernel), "paged_decode_merge%s_kernel<%d,%d,%s,%s>",
+             lp.ms.sliced ? "_sliced" : "", kp.d, kp.g, tf(kp.bf), tf(kp.gen));
+  *info = d;
+  return ok();
+}
 
 int pda_paged_decode_attention(PDA_DECODE_PARAMS) {
   return decode(kPassSplit | kPassMerge, PDA_DECODE_ARGS(false));

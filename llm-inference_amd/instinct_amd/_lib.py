@@ -90,6 +90,23 @@ SIGNATURES["pda_rope_append_q8"] = (
     [c_void_p] * 10 + [c_int32] * 5 + [c_int64, c_int32, c_int32, c_void_p, c_void_p],
 )
 
+
+
+class DecodeInfo(ctypes.Structure):
+    """``pda_decode_info`` (pda.h): what a decode call of a shape launches."""
+
+    _fields_ = [(name, c_int32) for name in (
+        "kernel_dim", "head_slots", "kv_bits", "bf16", "generic", "matrix_cores",
+        "unit_heads", "units_per_kv_head", "split_waves", "ring", "grid_groups", "local",
+        "merge", "merge_waves")] + [("split_kernel", ctypes.c_char * 96),
+                                    ("merge_kernel", ctypes.c_char * 96)]
+
+
+SIGNATURES["pda_decode_describe"] = (
+    ctypes.c_int,
+    [c_int32] * 11 + [ctypes.POINTER(DecodeInfo)],
+)
+
 _lib: ctypes.CDLL | None = None
 
 
@@ -157,3 +174,17 @@ def plan(batch, q_heads, kv_heads, head_dim, page_size, table_stride, longest, w
                              longest, window, split_pages, ctypes.byref(pages),
                              ctypes.byref(splits)))
     return pages.value, splits.value
+
+
+def describe(batch, q_heads, kv_heads, head_dim, page_size, table_stride, longest, window,
+             split_pages=0, kv_bits=16, bf16=False) -> dict:
+    """``pda_decode_describe``: the kernels, grid, local mode and merge shape
+    the library launches for a decode call of this shape."""
+    info = DecodeInfo()
+    check(library().pda_decode_describe(batch, q_heads, kv_heads, head_dim, page_size,
+                                        table_stride, longest, window, split_pages, kv_bits,
+                                        int(bool(bf16)), ctypes.byref(info)))
+    out = {name: getattr(info, name) for name, _ in DecodeInfo._fields_}
+    out["split_kernel"] = info.split_kernel.decode()
+    out["merge_kernel"] = info.merge_kernel.decode() or None
+    return out

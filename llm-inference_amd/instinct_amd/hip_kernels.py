@@ -28,6 +28,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+from collections import OrderedDict
 from typing import Any
 
 import numpy as np
@@ -35,15 +36,27 @@ import torch
 
 from . import _lib
 
-_workspaces: dict[tuple[int, int], torch.Tensor] = {}
+# Cached workspaces, most recently used last: at most _WORKSPACE_STREAMS
+# streams keep one; the least recently used one is dropped past that.
+_workspaces: "OrderedDict[tuple[int, int], torch.Tensor]" = OrderedDict()
+_WORKSPACE_STREAMS = 4
+
+
+def new_workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    """A workspace for the library's calls: ``nbytes`` of device memory (it
+    needs no initialisation; the caching allocator's blocks are 512-byte
+    aligned)."""
+    return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
 
 
 def stream_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """A cached, 256-byte aligned device workspace of at least ``nbytes`` for
-    the current stream of ``device``, grown on demand and shared by calls of
-    any shape on that stream (it holds nothing between calls, and calls on
-    one stream never overlap). Calls on different streams get different
-    buffers.
+    """A cached, 256-byte aligned device workspace of at least ``nbytes``
+    for the current stream of ``device``, grown on demand and
+    shared by calls of any shape on that stream (calls on one stream never
+    overlap). Calls on different streams get different buffers; the cache
+    keeps those of the four streams used last (a dropped buffer goes back to
+    the caching allocator, which only reuses it for work ordered after it on
+    its stream).
 
     Growing replaces the stream's buffer; the caching allocator only reuses
     the old one for work ordered after the replacement on the same stream.
@@ -57,8 +70,11 @@ def stream_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
         size = max(nbytes, 1 << 20)
         if buf is not None:
             size = max(size, 2 * buf.numel())
-        buf = torch.empty(size, dtype=torch.uint8, device=device)
-        _workspaces[key] = buf
+        buf = new_workspace(size, device)
+    _workspaces[key] = buf
+    _workspaces.move_to_end(key)
+    while len(_workspaces) > _WORKSPACE_STREAMS:
+        _workspaces.popitem(last=False)
     return buf
 
 
@@ -74,120 +90,34 @@ def _given_workspace(ws: torch.Tensor, device: torch.device, nbytes: int) -> tor
     return ws
 
 
-_FAST_DIMS = {16: (64, 80, 96, 128, 256, 512), 8: (64, 128, 256, 512)}
-# Matrix-core kernels by K/V bits: head dims, and the fewest heads per kv head.
-_MF_DIMS = {16: (64, 96, 128, 256, 512), 8: (64, 128, 256, 512)}
-_MF_MIN_GROUP = {16: 5, 8: 1}
-# Merge launch (csrc/pda_kernels.hip ``merge_shape``) on MI355X: 256 CUs x
-# one split workgroup of four wave pairs (two for the matrix-core kernels at
-# D = 512); the row-sliced merge for units of more than 64 pieces, in grids
-# of 4096 workgroups at most.
-_GRID_PAIRS = 1024
-_MERGE_SLICED_ROUND = 64
-_MERGE_SLICED_MAX_GROUPS = 4096
-
-
-# Local mode (csrc/pda_kernels.hip ``local_lds``): a workgroup per unit, no
-# merge pass, for at most 512 units of at most 1.5 MiB of K/V, pieces within
-# 64 KiB of LDS.
-_LOCAL_MAX_UNITS = 512
-_LOCAL_MAX_UNIT_BYTES = 3 << 19
-_LOCAL_MAX_LDS = 64 << 10
-
-
-def _unit_pages_max(longest, page_size, table_width, window) -> int:
-    """Visible pages of one unit at most (``make_plan``'s estimate)."""
-    pages_max = table_width
-    if window > 0:
-        pages_max = min(pages_max, (window - 1) // page_size + 2)
-    if longest > 0:
-        pages_max = min(pages_max, -(-longest // page_size) + 1)
-    return pages_max
-
-
-def _local(dim, heads, units, *, batch, longest, page_size, table_width, window, elem,
-           waves, ring, grid_pairs, split_pages=0) -> bool:
-    """Whether the call runs in local mode: the library's rule."""
-    lds = ((2 * batch + 1 + 3) & ~3) * 4 + waves * heads * (dim * 4 + 8)
-    if lds > _LOCAL_MAX_LDS:
-        return False
-    force = os.environ.get("PDA_DECODE_LOCAL", "")
-    if force:
-        return int(force) > 0
-    est = _unit_pages_max(longest, page_size, table_width, window)
-    pages_est = batch * units * est
-    min_pages = split_pages if split_pages > 0 else 1
-    pairs = max(1, min(grid_pairs, -(-pages_est // (2 * min_pages))))
-    return (batch * units <= _LOCAL_MAX_UNITS
-            and est * page_size * dim * elem * 2 <= _LOCAL_MAX_UNIT_BYTES
-            and 16 * est * pairs <= 5 * ring * waves * pages_est)
-
-
-def _merge_sliced(dim, heads, units, *, batch, longest, page_size, table_width, window,
-                  split_pages, grid_pairs=_GRID_PAIRS) -> bool:
-    """Whether the merge runs row-sliced (one 64-element slice of a head per
-    workgroup): the library's rule, from the same page estimates."""
-    est = _unit_pages_max(longest, page_size, table_width, window)
-    pages_est = batch * units * est
-    min_pages = split_pages if split_pages > 0 else 1
-    pairs = max(1, min(grid_pairs, -(-pages_est // (2 * min_pages))))
-    per_pair = max(1, pages_est // pairs)
-    pieces = 2 * (est // per_pair + 2)
-    chunks = -(-dim // 64)
-    force = os.environ.get("PDA_MERGE_SLICED", "")
-    if force:
-        return int(force) > 0
-    return pieces > _MERGE_SLICED_ROUND and batch * heads * chunks <= _MERGE_SLICED_MAX_GROUPS
-
-
 def decode_kernel_names(q_heads: int, kv_heads: int, head_dim: int, *, bits: int = 16,
                         bf16: bool = False, batch: int = 0, longest: int = 0,
                         page_size: int = 16, table_width: int = 0, window: int = 0,
                         split_pages: int = 0) -> dict[str, Any]:
-    """The kernels a decode call of this shape launches, as the library's
-    dispatch picks them (csrc/pda_kernels.hip ``make_plan``, ``kernels_for``,
-    ``heads_per_group``, ``use_mf``, ``merge_shape``): template arguments
-    ``<D, G, Q8, BF, GEN, MF>`` of the split kernel and ``<D, G, BF, GEN>`` of
-    the merge kernel (or its row-sliced form), whether the matrix cores run it, the query
-    heads one unit serves and the units per kv head (each reads the kv
-    head's K/V once). Local mode (a workgroup per unit, merged in LDS, no
-    merge kernel: ``merge`` None) and the merge's row slicing depend on the
-    batch, the longest length and the table width (``batch`` 0: neither)."""
-    group = q_heads // kv_heads
-    min_mf = (int(os.environ.get("PDA_MFMA_MIN_GROUP", "0") or 0)
-              or ((4 if bits == 8 else 1) if head_dim == 512 else _MF_MIN_GROUP[bits]))
-    mf = head_dim in _MF_DIMS[bits] and group >= min_mf
-    cap = 16 if mf else 8
-    heads = next(g for g in range(min(group, cap), 0, -1) if group % g == 0)
-    generic = head_dim not in _FAST_DIMS[bits]
-    dim = max(8, 1 << (head_dim - 1).bit_length()) if generic else head_dim
-    slots = 16 if mf else heads
-    units = kv_heads * (group // heads)
+    """The kernels a decode call of this shape launches, as the library
+    reports them (``pda_decode_describe``, the dispatch the call itself runs):
+    the split kernel ``<D, G, Q8, BF, GEN, MF>`` and the merge kernel
+    ``<D, G, BF, GEN>`` or its row-sliced form (None in local mode, where one
+    workgroup per unit merges in LDS), whether the matrix cores run it, the
+    query heads one unit serves, the units per kv head (each reads the kv
+    head's K/V once), the ring depth and the grid. Local mode and the merge
+    shape depend on the batch, the longest length and the table width;
+    ``batch`` 0 reports the shape's split kernel only (``merge`` None, no
+    local mode)."""
     width = table_width or -(-max(longest, 1) // page_size)
-    four_wave = mf and dim == 512
-    # K/V steps in flight per wave (pda_decode.h ring_depth).
-    ring = (1 if mf and dim >= 256 else
-            4 if not mf and bits == 16 and not generic and dim >= 256 and heads <= 2 else 2)
-    local = batch > 0 and _local(
-        dim, heads, units, batch=batch, longest=longest, page_size=page_size,
-        table_width=width, window=window, elem=1 if bits == 8 else 2,
-        waves=4 if four_wave else 8, ring=ring,
-        grid_pairs=_GRID_PAIRS // 2 if four_wave else _GRID_PAIRS,
-        split_pages=split_pages)
-    sliced = batch > 0 and not local and _merge_sliced(
-        dim, units * heads, units, batch=batch, longest=longest, page_size=page_size,
-        table_width=width, window=window, split_pages=split_pages,
-        grid_pairs=_GRID_PAIRS // 2 if four_wave else _GRID_PAIRS)
-    b = lambda x: str(bool(x)).lower()  # noqa: E731
-    targs = f"{dim},{slots},{b(bits == 8)},{b(bf16)},{b(generic)},{b(mf)}"
-    return {"split": f"paged_decode_kernel<{targs}>",
-            "merge": (None if local else
-                      f"paged_decode_merge{'_sliced' if sliced else ''}_kernel<{dim},{slots},"
-                      f"{b(bf16)},{b(generic)}>"),
-            "local": local,
-            "merge_row_sliced": sliced,
-            "matrix_cores": mf, "heads_per_unit": heads,
-            "head_groups_per_kv_head": group // heads}
+    info = _lib.describe(max(batch, 1), q_heads, kv_heads, head_dim, page_size, width,
+                         longest, window, split_pages, kv_bits=bits, bf16=bf16)
+    real = batch > 0
+    return {"split": info["split_kernel"],
+            "merge": info["merge_kernel"] if real else None,
+            "local": real and bool(info["local"]),
+            "merge_row_sliced": real and info["merge"] == 2,
+            "matrix_cores": bool(info["matrix_cores"]),
+            "heads_per_unit": info["unit_heads"],
+            "head_groups_per_kv_head": info["units_per_kv_head"],
+            "ring": info["ring"], "split_waves": info["split_waves"],
+            "grid_groups": info["grid_groups"],
+            "merge_waves": info["merge_waves"] if real else 0}
 
 
 def decode_workspace_bytes(queries_shape: tuple[int, int, int], keys: torch.Tensor, *,
@@ -217,7 +147,7 @@ def paged_decode_attention(
     out: torch.Tensor | None = None,
     passes: str = "both",
     workspace: torch.Tensor | None = None,
-    deterministic: bool = False,
+    deterministic: bool = True,
 ) -> torch.Tensor:
     """Attention for one new token per sequence over its paged keys
     (metal_kernels.py:164-186). ``split_pages`` is the fewest pages a wave
@@ -226,11 +156,13 @@ def paged_decode_attention(
     one of the two kernels only (the output is complete after the merge).
     ``workspace``: a uint8 device tensor the caller owns (at least
     :func:`decode_workspace_bytes`), else the stream's cached one.
-    ``deterministic``: fixed split points (``PDA_DECODE_FIXED_SPLIT``), so
-    repeated calls on the same inputs give bitwise-identical outputs, as the
-    reference's fixed split ranges do (metal_kernels.py:32-36); without it
-    the split points follow the waves' progress and the last bits of a
-    sequence's output can differ from call to call (within the parity bar).
+    ``deterministic`` (default): fixed split points
+    (``PDA_DECODE_FIXED_SPLIT``), so repeated calls on the same inputs give
+    bitwise-identical outputs, as the reference's fixed split ranges do
+    (metal_kernels.py:32-36). ``deterministic=False`` lets the two waves
+    that share a stretch of pages split it wherever they meet (the faster
+    takes more), so the last bits of a sequence's output can differ from
+    call to call (within the parity bar).
     Any even ``head_dim`` up to 512 and any ``page_size`` are accepted, as by
     the reference op (metal_kernels.py:28-30,204).
 

@@ -14,7 +14,9 @@ Nothing of the step crosses PCIe except those inputs, and no kernel is
 launched from Python.
 
 Results do not depend on ``longest`` (a sizing hint of the decode call), so
-one capture serves every later step whose sequences stay within the arenas.
+one capture serves every later step whose sequences stay within the arenas;
+two replays on the same inputs give the same bits (the decode call's split
+points are fixed by the inputs).
 """
 
 from __future__ import annotations
@@ -24,8 +26,8 @@ from typing import Any
 
 import torch
 
-from .hip_kernels import (decode_workspace_bytes, pack_decode_step, paged_decode_attention,
-                          rope_append)
+from .hip_kernels import (decode_workspace_bytes, new_workspace, pack_decode_step,
+                          paged_decode_attention, rope_append)
 
 
 class DecodeStepGraph:
@@ -74,7 +76,7 @@ class DecodeStepGraph:
         # be shared with calls outside it (whose workspace may be replaced).
         need = decode_workspace_bytes((batch, q_heads, head_dim), keys, page_size=page_size,
                                       table_width=width, longest=longest, window=window)
-        self.workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+        self.workspace = new_workspace(need, dev)
         self.graph: torch.cuda.CUDAGraph | None = None
 
     def run(self) -> None:

@@ -278,3 +278,60 @@ def test_prefill_q8_validation():
     assert call(ks=FAKE + 1) == _lib.PDA_ERR_ALIGNMENT
     assert call(head_dim=79) == _lib.PDA_ERR_HEAD_DIM
     assert call(count=0, ks=None, vs=None) == _lib.PDA_OK
+
+
+# What each BASELINE configuration launches, as pda_decode_describe reports it
+# without a device (MI355X's 256-workgroup grid); these are the kernel names
+# the rocprofv3 traces under profiles/ show for the same calls.
+DESCRIBED = [
+    # (q_heads, kv_heads, head_dim, batch, longest, table_width, window, bits, bf16)
+    ((14, 2, 64, 8, 1024, 64, 0, 16, False),  # config 1
+     "paged_decode_kernel<64,16,false,false,false,true>",
+     "paged_decode_merge_sliced_kernel<64,16,false,false>"),
+    ((28, 4, 128, 64, 8138, 512, 0, 16, False),  # config 2
+     "paged_decode_kernel<128,16,false,false,false,true>",
+     "paged_decode_merge_kernel<128,16,false,false>"),
+    ((32, 8, 128, 1, 32768, 2048, 0, 16, False),  # config 3, B=1 x 32K
+     "paged_decode_kernel<128,4,false,false,false,false>",
+     "paged_decode_merge_sliced_kernel<128,4,false,false>"),
+    ((32, 8, 128, 4, 131072, 8192, 0, 16, False),  # config 3, B=4 x 131K
+     "paged_decode_kernel<128,4,false,false,false,false>",
+     "paged_decode_merge_sliced_kernel<128,4,false,false>"),
+    ((8, 4, 256, 32, 32768, 2048, 1024, 16, False),  # config 4: local mode
+     "paged_decode_kernel<256,2,false,false,false,false>", None),
+    ((32, 8, 128, 256, 65536, 4096, 0, 16, False),  # config 5
+     "paged_decode_kernel<128,4,false,false,false,false>",
+     "paged_decode_merge_kernel<128,4,false,false>"),
+    ((16, 2, 512, 1, 261840, 16365, 0, 16, True),  # the reference's published layer, bf16
+     "paged_decode_kernel<512,16,false,true,false,true>",
+     "paged_decode_merge_sliced_kernel<512,16,true,false>"),
+    ((28, 4, 128, 64, 8138, 512, 0, 8, False),  # config 2 over an 8-bit cache
+     "paged_decode_kernel<128,16,true,false,false,true>",
+     "paged_decode_merge_kernel<128,16,false,false>"),
+]
+
+
+@pytest.mark.parametrize("shape, split, merge", DESCRIBED)
+def test_describe_reports_each_configuration(shape, split, merge):
+    hq, hkv, d, batch, longest, width, window, bits, bf16 = shape
+    info = _lib.describe(batch, hq, hkv, d, 16, width, longest, window, kv_bits=bits, bf16=bf16)
+    assert info["split_kernel"] == split
+    assert info["merge_kernel"] == merge
+    assert info["local"] == (merge is None)
+    assert info["merge"] == (0 if merge is None else 2 if "sliced" in merge else 1)
+    assert info["matrix_cores"] == split.endswith("true>")
+    assert info["grid_groups"] == 256
+
+
+def test_describe_validation():
+    with pytest.raises(_lib.PdaError):
+        _lib.describe(4, 28, 4, 128, 16, 64, 1000, 0, kv_bits=4)
+    with pytest.raises(_lib.PdaError):
+        _lib.describe(4, 28, 4, 128, 16, 64, 1000, 0, kv_bits=8, bf16=True)
+    with pytest.raises(ValueError):
+        _lib.describe(4, 30, 4, 128, 16, 64, 1000, 0)
+    # Generic head dims report their padded kernel; units of large groups.
+    info = _lib.describe(2, 8, 1, 80, 16, 64, 1000, 0, kv_bits=8)
+    assert info["split_kernel"] == "paged_decode_kernel<128,8,true,false,true,false>"
+    info = _lib.describe(2, 32, 1, 128, 16, 64, 1000, 0)
+    assert (info["unit_heads"], info["units_per_kv_head"], info["head_slots"]) == (16, 2, 16)

@@ -21,7 +21,7 @@ def test_help_lists_the_legs():
     r = run_bench("--help")
     assert r.returncode == 0, r.stderr
     for option in ("--published", "--latency-configs", "--kv-bits", "--prefill-wide",
-                   "--deterministic", "--copy-calibration"):
+                   "--deterministic", "--racing", "--copy-calibration"):
         assert option in r.stdout
 
 

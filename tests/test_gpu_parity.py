@@ -352,3 +352,39 @@ def test_decode_batch_writes_then_attends(gpu, layout):
             q.cpu().numpy(), keys.cpu().numpy(), values.cpu().numpy(), packed,
             positions + 1, page_size=page, scale=128 ** -0.5, window=group.window)
         assert_parity(out.view(5, 16, 128), expected, f"layer{layer}")
+
+
+def test_decode_batch_repeats_bit_for_bit(gpu):
+    """Two identical decode steps through DecodeBatch give bitwise-equal
+    outputs (the default fixed split points; the reference's split ranges are
+    fixed too, metal_kernels.py:32-36, and its engine compares token streams
+    exactly, tests/test_mlx_engine.py:225-237). Long sequences, so every unit
+    is cut over many waves, on the matrix-core (7 heads per kv head) and the
+    VALU (4 heads) kernels."""
+    from instinct_amd.batches import DecodeBatch
+    from instinct_amd.paged_kv import KVCache, KVGroup
+
+    page = 16
+    groups = [KVGroup("g7", (0,), kv_heads=4, head_dim=128),
+              KVGroup("g4", (1,), kv_heads=8, head_dim=128)]
+    cache = KVCache(groups, page_size=page, capacities={"g7": 2048, "g4": 2048}, device=gpu)
+    positions = np.array([4000, 1234, 7000, 333, 5555, 2600, 16, 6100])
+    tables = {}
+    for name in ("g7", "g4"):
+        pool = cache.pools[name]
+        tables[name] = [np.array([pool.allocate(reserved=False)
+                                  for _ in range(p // page + 1)]) for p in positions]
+    gen = torch.Generator(device=gpu).manual_seed(3)
+    for layer in range(2):
+        cache.keys[layer].normal_(generator=gen)
+        cache.values[layer].normal_(generator=gen)
+    batch = DecodeBatch(cache, torch.zeros(8, device=gpu), positions=positions, tables=tables)
+    for layer, hq in ((0, 28), (1, 32)):
+        hkv = cache.layer_group[layer].kv_heads
+        q = torch.randn((8, hq, 128), generator=gen, device=gpu).half()
+        k = torch.randn((8, hkv, 128), generator=gen, device=gpu).half()
+        v = torch.randn((8, hkv, 128), generator=gen, device=gpu).half()
+        first = batch.attend(layer, q, k, v, scale=128 ** -0.5).clone()
+        for step in range(4):
+            again = batch.attend(layer, q, k, v, scale=128 ** -0.5)
+            assert torch.equal(again, first), f"layer {layer}: step {step + 1} differs"
