@@ -511,12 +511,14 @@ def cpu_model() -> str:
     return "unknown"
 
 
-def cpu_baseline(w, budget_s, dense=False):
+def cpu_baseline(w, budget_s, splitk=False):
     """A CPU restatement of the reference's decode path on a sample of
     sequences of the same workload, all host cores; returns the dict for the
-    JSON line. Default: the C++ float32 split-K restatement of the Metal
-    kernel; `dense`: the C++ restatement of the portable path (gather, then
-    dense attention; float64)."""
+    JSON line. Default: the path BASELINE.json names, the reference's MLX CPU
+    (portable) decode: gather the visible rows, then dense attention in
+    float32 (portable.py:155-205, batches.py:228-246), C++ over std::thread.
+    `splitk`: the C++ float32 restatement of the Metal split-K kernel
+    (metal_kernels.py:18-124), a second record."""
     import numpy as np
 
     from oracle import cpu_oracle
@@ -525,7 +527,7 @@ def cpu_baseline(w, budget_s, dense=False):
     q, k, v, t, n = w.numpy()
     spans = w.spans()
     per_seq = spans * w.kv_heads * w.head_dim * 4  # K+V bytes per sequence
-    fn = cpu_oracle.decode_f64 if dense else cpu_oracle.decode_splitk
+    fn = cpu_oracle.decode_splitk if splitk else cpu_oracle.decode_f32
     # Calibrate on one sequence, then size the sample to the budget.
     def run(idx):
         t0 = time.perf_counter()
@@ -545,11 +547,11 @@ def cpu_baseline(w, budget_s, dense=False):
         total_t += run(idx)
         total_b += int(per_seq[idx].sum())
         reps += 1
-    what = ("C++ float64 restatement of the reference's portable path (gather, then dense "
-            "attention; portable.py:155-205, batches.py:228-246), std::thread over "
-            "(sequence, head)" if dense else
-            "C++ float32 restatement of the reference split-K kernel "
-            "(metal_kernels.py:18-124), std::thread over (sequence, kv head, split)")
+    what = ("C++ float32 restatement of the reference split-K kernel "
+            "(metal_kernels.py:18-124), std::thread over (sequence, kv head, split)" if splitk else
+            "C++ float32 restatement of the reference's MLX CPU (portable) decode path: gather "
+            "the visible rows, then dense float32 attention (portable.py:155-205, "
+            "batches.py:228-246), std::thread over (sequence, kv head)")
     return {
         "value": round(total_b / total_t / 1e9, 3),
         "unit": "GB/s",
@@ -733,7 +735,7 @@ def main():
     # The CPU baselines time the fp16 oracle; a bf16 run has none.
     if not args.no_cpu and args.kv_bits == 16 and not bf16:
         line["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
-        line["cpu_baseline_dense"] = cpu_baseline(w, args.cpu_seconds / 2, dense=True)
+        line["cpu_baseline_splitk"] = cpu_baseline(w, args.cpu_seconds / 2, splitk=True)
     others = [int(c) for c in args.latency_configs.split(",") if c.strip()]
     if args.kv_bits == 16 and not bf16:
         line["other_configs"] = {str(c): config_leg(c, args, flushing)

@@ -190,6 +190,17 @@ class PagePool:
             raise RuntimeError("cannot share a page that is not allocated")
         self._refs[unique] += counts
 
+    def held_only_by(self, counts: np.ndarray) -> int:
+        """Pages that would come free if ``counts[page]`` of each page's
+        references were dropped: those held by exactly that many references
+        (the reference's contract, paged_kv.py:150-153; its prefix cache
+        weighs evictions with it, prefix_cache.py:193). ``counts`` is indexed
+        by page id; entries past the pool's capacity are ignored."""
+        counts = np.asarray(counts, dtype=np.int64).ravel()
+        n = min(counts.size, self.capacity)
+        wanted = counts[:n]
+        return int(np.count_nonzero((wanted > 0) & (self._refs[:n] == wanted)))
+
     def release(self, pages: Iterable[int]) -> None:
         """Drop one reference per listed occurrence; pages left with none
         become free."""

@@ -2,7 +2,7 @@
 // INFRASTRUCTURE ONLY (the checker and the timed CPU baseline). Only tests/,
 // __graft_entry__.smoke() and bench.py's CPU-baseline leg load it.
 //
-// Two entry points, both threaded over (sequence, kv head[, split]) with
+// Three entry points, each threaded over (sequence, kv head[, split]) with
 // std::thread on the cores they are given:
 //
 //  oracle_decode_f64    The portable ("MLX CPU") decode path: gather the
@@ -11,6 +11,10 @@
 //                       product and sum in float64.
 //                       python/instinct/backends/portable.py:155-205 and
 //                       python/instinct/batches.py:183-189,228-246.
+//  oracle_decode_f32    The same portable path in float32, as the reference
+//                       computes it (_attention_plain: float32 scores,
+//                       softmax and product, fp16 output): the timed CPU
+//                       baseline.
 //  oracle_decode_splitk The Metal kernel's split-K algorithm in float32:
 //                       per (sequence, kv head, split) the per-key online
 //                       softmax update, unnormalised partials, then the
@@ -204,6 +208,64 @@ void oracle_decode_f64(const uint16_t* q, const uint16_t* k, const uint16_t* v,
       for (int d = 0; d < D; ++d)
         out[((int64_t)b * HQ + kvh * G + g) * D + d] =
             sum[g] > 0.0 ? acc[(size_t)g * D + d] / sum[g] : 0.0;
+  });
+}
+
+// Float32 portable path (the "MLX CPU" decode the reference's engine runs
+// without Metal kernels): gather the visible rows, then
+// _attention_plain (portable.py:173-188) in float32: scores = (q * scale) .
+// K^T, softcap, masked (released pages, portable.py:202-204), softmax
+// (max, exp, sum, divide), probabilities @ V, cast to fp16. out [B, HQ, D]
+// fp16 bits.
+void oracle_decode_f32(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                       const int32_t* tables, const int32_t* lengths, uint16_t* out,
+                       int B, int HQ, int HKV, int D, int P, int stride,
+                       int64_t arena_rows, float scale, int window, float softcap,
+                       int threads) {
+  const Args a{q, k, v, tables, lengths, B, HQ, HKV, D, P, stride, arena_rows, scale, window, softcap};
+  const int G = HQ / HKV;
+  const float* t16 = tab().v;
+  parallel_for((int64_t)B * HKV, threads, [&](int64_t item) {
+    const int b = (int)(item / HKV), kvh = (int)(item % HKV);
+    int first, len;
+    std::vector<int64_t> rows;
+    visible_rows(a, b, first, len, rows);
+    const int n = (int)rows.size();
+    // The gather: the visible K and V rows of this kv head, in float32.
+    std::vector<float> kg((size_t)n * D), vg((size_t)n * D);
+    for (int i = 0; i < n; ++i) {
+      const int64_t r = rows[i] < 0 ? 0 : rows[i];
+      const uint16_t* kp = k + (r * HKV + kvh) * D;
+      const uint16_t* vp = v + (r * HKV + kvh) * D;
+      for (int d = 0; d < D; ++d) kg[(size_t)i * D + d] = t16[kp[d]];
+      for (int d = 0; d < D; ++d) vg[(size_t)i * D + d] = t16[vp[d]];
+    }
+    std::vector<float> qs(D), s(n), acc(D);
+    for (int g = 0; g < G; ++g) {
+      const int64_t h = (int64_t)b * HQ + kvh * G + g;
+      for (int d = 0; d < D; ++d) qs[d] = t16[q[h * D + d]] * scale;
+      float top = -INFINITY;
+      for (int i = 0; i < n; ++i) {
+        float dot = 0.0f;
+        const float* kr = &kg[(size_t)i * D];
+        for (int d = 0; d < D; ++d) dot += qs[d] * kr[d];
+        if (softcap > 0.0f) dot = std::tanh(dot / softcap) * softcap;
+        s[i] = rows[i] < 0 ? -INFINITY : dot;
+        top = std::max(top, s[i]);
+      }
+      float sum = 0.0f;
+      for (int i = 0; i < n; ++i) {
+        s[i] = top == -INFINITY ? 0.0f : std::exp(s[i] - top);
+        sum += s[i];
+      }
+      std::fill(acc.begin(), acc.end(), 0.0f);
+      for (int i = 0; i < n; ++i) {
+        const float p = sum > 0.0f ? s[i] / sum : 0.0f;
+        const float* vr = &vg[(size_t)i * D];
+        for (int d = 0; d < D; ++d) acc[d] += p * vr[d];
+      }
+      for (int d = 0; d < D; ++d) out[h * D + d] = float_to_half(acc[d]);
+    }
   });
 }
 

@@ -2,9 +2,11 @@
 
 ``decode_f64`` is the fast, threaded float64 restatement of the reference's
 portable decode path (portable.py:155-205, batches.py:228-246), used to check
-full-size configurations; ``decode_splitk`` is the float32 restatement of the
-Metal split-K kernel (metal_kernels.py:18-124) that bench.py times as the CPU
-baseline. Both are pinned against paged_attention.py (tests/test_oracle.py).
+full-size configurations; ``decode_f32`` is the same path in float32, as the
+reference computes it, which bench.py times as the CPU baseline;
+``decode_splitk`` is the float32 restatement of the Metal split-K kernel
+(metal_kernels.py:18-124), timed beside it. All three are pinned against
+paged_attention.py (tests/test_oracle.py).
 Only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg use it.
 """
 
@@ -32,6 +34,9 @@ def library():
         lib.oracle_decode_f64.restype = None
         lib.oracle_decode_f64.argtypes = [c_void_p] * 6 + [c_int] * 6 + [
             c_int64, c_double, c_int, c_double, c_int]
+        lib.oracle_decode_f32.restype = None
+        lib.oracle_decode_f32.argtypes = [c_void_p] * 6 + [c_int] * 6 + [
+            c_int64, c_float, c_int, c_float, c_int]
         lib.oracle_decode_splitk.restype = None
         lib.oracle_decode_splitk.argtypes = [c_void_p] * 6 + [c_int] * 6 + [
             c_int64, c_float, c_int, c_float, c_int, c_int]
@@ -64,6 +69,24 @@ def decode_f64(q, keys, values, tables, lengths, *, page_size, scale, window=0,
         raise ValueError("query heads must be a multiple of kv heads")
     out = np.zeros((batch, hq, dim), dtype=np.float64)
     library().oracle_decode_f64(
+        q.ctypes.data, keys.ctypes.data, values.ctypes.data, tables.ctypes.data,
+        lengths.ctypes.data, out.ctypes.data, batch, hq, hkv, dim, page_size,
+        tables.shape[1], keys.shape[0], scale, window, softcap,
+        threads or host_cores())
+    return out
+
+
+def decode_f32(q, keys, values, tables, lengths, *, page_size, scale, window=0,
+               softcap=0.0, threads=None) -> np.ndarray:
+    """Float32 restatement of the portable path (gather, then dense
+    attention in float32, portable.py:155-205); ``[B, HQ, D]`` fp16."""
+    q, keys, values, tables, lengths = _args(q, keys, values, tables, lengths)
+    batch, hq, dim = q.shape
+    hkv = keys.shape[1]
+    if hq % hkv:
+        raise ValueError("query heads must be a multiple of kv heads")
+    out = np.zeros((batch, hq, dim), dtype=np.float16)
+    library().oracle_decode_f32(
         q.ctypes.data, keys.ctypes.data, values.ctypes.data, tables.ctypes.data,
         lengths.ctypes.data, out.ctypes.data, batch, hq, hkv, dim, page_size,
         tables.shape[1], keys.shape[0], scale, window, softcap,

@@ -85,6 +85,8 @@ def test_closed_form_from_cuda_tests():
     np.testing.assert_allclose(c64[0, 0], expected, rtol=0, atol=1e-12)
     c16 = cpu_oracle.decode_splitk(q, keys, values, tables, lengths, **kw)
     np.testing.assert_allclose(c16[0, 0].astype(np.float64), expected, atol=4e-3)
+    c32 = cpu_oracle.decode_f32(q, keys, values, tables, lengths, **kw)
+    np.testing.assert_allclose(c32[0, 0].astype(np.float64), expected, atol=4e-3)
 
 
 @pytest.mark.parametrize("seed", range(4))
@@ -290,6 +292,35 @@ def test_c_oracles_match_the_numpy_restatement(seed):
                                        softcap=softcap, splits=splits)
         err_max, err_mean = pa.error_stats(c16, ref)
         assert err_max <= 2e-3 and err_mean <= 2e-4, (err_max, err_mean)
+    c32 = cpu_oracle.decode_f32(*case, page_size=16, scale=scale, window=window,
+                                softcap=softcap)
+    err_max, err_mean = pa.error_stats(c32, ref)
+    assert err_max <= 2e-3 and err_mean <= 2e-4, (err_max, err_mean)
+    # The float32 path step by step in NumPy (gather, scores, softmax, then
+    # the product, each in float32): equal up to the summation order of the
+    # float32 dot products, i.e. within one fp16 ulp.
+    q, keys, values, tables, lengths = case
+    want = np.zeros(q.shape, dtype=np.float16)
+    group = q.shape[1] // keys.shape[1]
+    for b in range(q.shape[0]):
+        n = int(lengths[b])
+        first = max(0, n - window) if window else 0
+        pos = np.arange(first, n)
+        pages = tables[b, pos // 16]
+        ok = pages >= 0
+        rows = np.where(ok, pages * 16 + pos % 16, 0)
+        for h in range(q.shape[1]):
+            kr = keys[rows, h // group].astype(np.float32)
+            vr = values[rows, h // group].astype(np.float32)
+            s = kr @ (q[b, h].astype(np.float32) * np.float32(scale))
+            if softcap:
+                s = np.tanh(s / np.float32(softcap)) * np.float32(softcap)
+            s = np.where(ok, s, -np.inf).astype(np.float32)
+            e = np.exp(s - s.max()).astype(np.float32)
+            p = (e / e.sum(dtype=np.float32)).astype(np.float32)
+            want[b, h] = (p @ vr).astype(np.float16)
+    ulp = np.spacing(np.abs(want).astype(np.float16)).astype(np.float64)
+    assert (np.abs(c32.astype(np.float64) - want.astype(np.float64)) <= ulp + 1e-7).all()
 
 
 def test_fp16_conversions_round_to_nearest_even():

@@ -41,7 +41,14 @@ class PoolModel:
         return got
 
 
-def agrees(pool, model):
+def agrees(pool, model, rng=None):
+    if rng is not None:
+        # held_only_by: the pages whose references are all among the given
+        # counts, against a count over the model.
+        counts = np.array([rng.randint(0, 3) for _ in range(len(model.refs))], dtype=np.int64)
+        want = sum(1 for r, c in zip(model.refs, counts) if c > 0 and r == c)
+        assert pool.held_only_by(counts) == want
+        assert pool.held_only_by(np.asarray(model.refs)) == sum(r > 0 for r in model.refs)
     assert pool.free == model.free
     assert pool.used == pool.capacity - model.free
     assert pool.reserved == model.reserved
@@ -95,7 +102,7 @@ def test_pool_follows_the_brute_force_model(capacity, seed):
             n = rng.randint(0, model.reserved)
             pool.unreserve(n)
             model.reserved -= n
-        agrees(pool, model)
+        agrees(pool, model, rng)
     pool.release(held)
     assert pool.free == capacity and pool.used == 0
 
