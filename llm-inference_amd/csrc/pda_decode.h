@@ -767,34 +767,51 @@ void paged_decode_kernel(const Params p) {
       } else {
         s_real[u] = false;
       }
-      // Once the unit is done the ring keeps reloading the last step (cache
-      // hits, never used), so every slot always has one load in flight.
+      // Once the unit is done the ring keeps reloading the last step (never
+      // used), so every slot always has one load in flight and the wait
+      // counts stay those of a steady ring. Those reloads drop the lanes'
+      // offsets: every lane of an instruction reads the same 16 bytes, one
+      // cache line per instruction instead of a whole step (at one page per
+      // wave, a 2-deep ring otherwise doubles the L2 reads, an 8-deep one
+      // multiplies them by 8).
+      // Every per-lane term goes: the lane's column and row offsets, the
+      // ragged shifts (which move rows back by up to the lane's own row, so
+      // without the row they would point before the page) and the second
+      // key row of a pair. What stays is the step's first row (inside the
+      // page) plus chunk offsets inside that row.
+      const bool dummy = !s_real[u];
+      const uint32_t lm = dummy ? 0u : ~0u;
+      const int dk = dummy ? 0 : last_dk;                 // K row shift
+      const int dv0 = dummy ? 0 : last_dv0;               // first value row of the pair
+      const int dv1 = dummy ? 0 : 1 + last_dv1;           // second value row of the pair
+      const int dvo = dummy ? 0 : (hi ? last_dv1 : last_dv0);  // this lane's value row shift
+      const int dvx = dummy ? 0 : (hi ? last_dv0 : last_dv1);  // the other key's
       const int rb = p.row_bytes;
-      const char* kq = kbase + last_off + lane_off + last_dk * rb;
-      const char* vq = vbase + last_off + v_off;
+      const char* kq = kbase + last_off + (lane_off & lm) + dk * rb;
+      const char* vq = vbase + last_off + (v_off & lm);
       if constexpr (GEN) {
         // Four element pairs of this lane's key row, K then V.
-        const char* vk = vq + last_dk * rb;
+        const char* vk = vq + dk * rb;
         if constexpr (Q8) {
           uint32_t kw[4], vw[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            kw[i] = *reinterpret_cast<const uint16_t*>(kq + pair_off[i]);
-            vw[i] = *reinterpret_cast<const uint16_t*>(vk + pair_off[i]);
+            kw[i] = *reinterpret_cast<const uint16_t*>(kq + (pair_off[i] & lm));
+            vw[i] = *reinterpret_cast<const uint16_t*>(vk + (pair_off[i] & lm));
           }
           kb[u][0] = __builtin_bit_cast(
               f16x8, i32x4{(int)(kw[0] | kw[1] << 16), (int)(kw[2] | kw[3] << 16), 0, 0});
           vb[u][0] = __builtin_bit_cast(
               f16x8, i32x4{(int)(vw[0] | vw[1] << 16), (int)(vw[2] | vw[3] << 16), 0, 0});
-          const int so = last_dk * p.scale_row;
-          ksb[u] = p.kscale[last_soff + ks_off + so];
-          vs_own_b[u] = p.vscale[last_soff + vs_own + so];
+          const int so = dk * p.scale_row;
+          ksb[u] = p.kscale[last_soff + (ks_off & lm) + so];
+          vs_own_b[u] = p.vscale[last_soff + (vs_own & lm) + so];
         } else {
           i32x4 kw, vw;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            kw[i] = *reinterpret_cast<const int*>(kq + pair_off[i]);
-            vw[i] = *reinterpret_cast<const int*>(vk + pair_off[i]);
+            kw[i] = *reinterpret_cast<const int*>(kq + (pair_off[i] & lm));
+            vw[i] = *reinterpret_cast<const int*>(vk + (pair_off[i] & lm));
           }
           kb[u][0] = __builtin_bit_cast(f16x8, kw);
           vb[u][0] = __builtin_bit_cast(f16x8, vw);
@@ -805,27 +822,27 @@ void paged_decode_kernel(const Params p) {
 #pragma unroll
         for (int j = 0; j < NV / 2; ++j) {
           kb[u][j] = *reinterpret_cast<const f16x8*>(kq + 64 * j);
-          vb[u][j] = *reinterpret_cast<const f16x8*>(vq + last_dk * rb + 64 * j);
+          vb[u][j] = *reinterpret_cast<const f16x8*>(vq + dk * rb + 64 * j);
         }
-        const int so = last_dk * p.scale_row;
-        ksb[u] = p.kscale[last_soff + ks_off + so];
-        vs_own_b[u] = p.vscale[last_soff + vs_own + so];
+        const int so = dk * p.scale_row;
+        ksb[u] = p.kscale[last_soff + (ks_off & lm) + so];
+        vs_own_b[u] = p.vscale[last_soff + (vs_own & lm) + so];
       } else if constexpr (Q8) {
         kb[u][0] = *reinterpret_cast<const f16x8*>(kq);
-        const uint2 va = *reinterpret_cast<const uint2*>(vq + last_dv0 * rb);
-        const uint2 vc = *reinterpret_cast<const uint2*>(vq + (1 + last_dv1) * rb);
+        const uint2 va = *reinterpret_cast<const uint2*>(vq + dv0 * rb);
+        const uint2 vc = *reinterpret_cast<const uint2*>(vq + dv1 * rb);
         vb[u][0] = __builtin_bit_cast(f16x8, i32x4{(int)va.x, (int)va.y, (int)vc.x, (int)vc.y});
         const f16* ks = p.kscale + last_soff;
         const f16* vs = p.vscale + last_soff;
-        ksb[u] = ks[ks_off + last_dk * p.scale_row];
-        vs_own_b[u] = vs[vs_own + (hi ? last_dv1 : last_dv0) * p.scale_row];
-        vs_other_b[u] = vs[vs_other + (hi ? last_dv0 : last_dv1) * p.scale_row];
+        ksb[u] = ks[(ks_off & lm) + dk * p.scale_row];
+        vs_own_b[u] = vs[(vs_own & lm) + dvo * p.scale_row];
+        vs_other_b[u] = vs[(vs_other & lm) + dvx * p.scale_row];
       } else {
 #pragma unroll
         for (int v = 0; v < NV; ++v) {
           kb[u][v] = *reinterpret_cast<const f16x8*>(kq + 2 * DC * v);
           vb[u][v] = *reinterpret_cast<const f16x8*>(
-              PV2 ? vq + (v + (v ? last_dv1 : last_dv0)) * rb : vq + last_dk * rb + 2 * DC * v);
+              PV2 ? vq + (v ? dv1 : dv0) * rb : vq + dk * rb + 2 * DC * v);
         }
       }
     };
