@@ -108,7 +108,7 @@ int pda_plan(int32_t batch, int32_t q_heads, int32_t kv_heads,
  * chooses it: for labels, profiles and measurements (no reference
  * counterpart; the reference's wrapper picks its kernels inline,
  * metal_kernels.py:193-247). The arguments are those of the decode call
- * (`kv_bits` 16 or 8, `bf16` 1 for bf16 queries with 16-bit K/V); the split
+ * (`kv_bits` 16 or 8, `bf16` 1 for bf16 queries and output); the split
  * grid is the current device's, or MI355X's 256 workgroups when no device is
  * visible. Local mode (`local` 1) and the merge shape depend on `batch`,
  * `longest` and the table width as the call's do. */
@@ -311,6 +311,47 @@ int pda_decode_merge_q8(const void* queries, const void* keys, const void* value
                         float scale, int32_t window, float softcap,
                         int32_t split_pages, int32_t flags, void* workspace,
                         size_t workspace_bytes, void* stream);
+
+/* 8-bit K/V under a bf16 model: the _q8 calls with bf16 queries and a bf16
+ * output. Replaces the reference's quantized kernel instantiated on
+ * T = queries.dtype (metal_kernels.py:134-141,196-206), which a bf16 model's
+ * 8-bit cache runs with bf16 queries and gets bf16 back. The int8 keys are
+ * exact in fp16, so the queries are taken to fp16 scaled by a power of two
+ * chosen per unit (the largest lands in [2^14, 2^15), so every bf16 value
+ * converts exactly and none overflows), and each score is scaled back by the
+ * same power of two; the arithmetic is then that of the _q8 calls and the
+ * output is rounded once, to bf16. Arguments, workspace and passes as for
+ * the _q8 calls. */
+int pda_paged_decode_attention_q8_bf16(const void* queries, const void* keys,
+                                       const void* values, const void* key_scales,
+                                       const void* value_scales,
+                                       const int32_t* tables, const int32_t* lengths,
+                                       void* out, int32_t batch, int32_t q_heads,
+                                       int32_t kv_heads, int32_t head_dim,
+                                       int32_t page_size, int32_t table_stride,
+                                       int64_t arena_rows, int32_t layout,
+                                       int32_t longest, float scale, int32_t window,
+                                       float softcap, int32_t split_pages, int32_t flags,
+                                       void* workspace, size_t workspace_bytes,
+                                       void* stream);
+int pda_decode_split_q8_bf16(const void* queries, const void* keys, const void* values,
+                             const void* key_scales, const void* value_scales,
+                             const int32_t* tables, const int32_t* lengths, void* out,
+                             int32_t batch, int32_t q_heads, int32_t kv_heads,
+                             int32_t head_dim, int32_t page_size, int32_t table_stride,
+                             int64_t arena_rows, int32_t layout, int32_t longest,
+                             float scale, int32_t window, float softcap,
+                             int32_t split_pages, int32_t flags, void* workspace,
+                             size_t workspace_bytes, void* stream);
+int pda_decode_merge_q8_bf16(const void* queries, const void* keys, const void* values,
+                             const void* key_scales, const void* value_scales,
+                             const int32_t* tables, const int32_t* lengths, void* out,
+                             int32_t batch, int32_t q_heads, int32_t kv_heads,
+                             int32_t head_dim, int32_t page_size, int32_t table_stride,
+                             int64_t arena_rows, int32_t layout, int32_t longest,
+                             float scale, int32_t window, float softcap,
+                             int32_t split_pages, int32_t flags, void* workspace,
+                             size_t workspace_bytes, void* stream);
 
 /* K/V append with rotary position embedding, one launch for n tokens.
  * Replaces, per attention layer and step, the reference's

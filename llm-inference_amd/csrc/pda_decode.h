@@ -402,7 +402,9 @@ void paged_decode_kernel(const Params p) {
   constexpr int kWaves = split_waves(D, MF);  // waves of this workgroup
   constexpr int kThreads = 64 * kWaves;
   constexpr int kWgPairs = kWaves / 2;
-  static_assert(!(Q8 && BF), "8-bit K/V is dequantized to fp16");
+  // Arithmetic in bf16 (bf16 K/V). Over 8-bit K/V, BF means bf16 queries
+  // and output with the fp16 arithmetic of the 8-bit kernels (see qscale).
+  constexpr bool BFM = BF && !Q8;
   static_assert(!MF || G == 16, "matrix-core kernels lay 16 head slots out");
   using Gm = Geom<D, Q8, GEN, MF>;
   constexpr int EPL = Gm::EPL, NV = Gm::NV, DC = Gm::DC, R = Gm::R, KPS = Gm::KPS;
@@ -529,7 +531,8 @@ void paged_decode_kernel(const Params p) {
     const int shared = __hip_atomic_fetch_add(&s_ticket[pl], (lane == 0 && !p.fixed) ? 1 : 0,
                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     const int own = own_tickets++;
-    if (p.fixed && p.balance) {
+    // (Four-wave workgroups run one wave per SIMD: no arbiter to steer.)
+    if (kWaves == 8 && p.fixed && p.balance) {
       if ((int64_t)own * partner_quota < (int64_t)uniform(seen) * quota)
         __builtin_amdgcn_s_setprio(1);
       else
@@ -628,6 +631,46 @@ void paged_decode_kernel(const Params p) {
           for (int i = 0; i < 4; ++i) q[g][4 * v + i] = f16x2{xq[2 * i], xq[2 * i + 1]};
         }
       }
+    }
+
+    // bf16 queries over 8-bit K/V (a bf16 model's 8-bit cache): the int8
+    // keys are exact in fp16, so the queries go to fp16 as well, scaled by a
+    // power of two chosen per unit that puts the largest in [2^14, 2^15).
+    // Every bf16 value (8 significant bits) then converts exactly, unless it
+    // is below 2^-17 of the largest (fp16 subnormals), and each score is
+    // multiplied back by the same power of two (qscale, folded into the key
+    // scale), which is exact. The rest runs as for fp16 queries; only the
+    // output is rounded to bf16. (Converting bf16 to fp16 unscaled would
+    // overflow past 65504 and lose the low bits below 2^-14.)
+    float qscale = 1.0f;
+    if constexpr (Q8 && BF) {
+      auto wide = [](f16 h) {
+        return __builtin_bit_cast(float, (uint32_t)__builtin_bit_cast(uint16_t, h) << 16);
+      };
+      float big = 0.0f;
+#pragma unroll
+      for (int c = 0; c < (MF ? NV : 0); ++c)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) big = fmaxf(big, fabsf(wide(qb[c][i])));
+#pragma unroll
+      for (int g = 0; g < (MF ? 0 : G); ++g)
+#pragma unroll
+        for (int i = 0; i < EPL / 2; ++i)
+          big = fmaxf(big, fmaxf(fabsf(wide(q[g][i][0])), fabsf(wide(q[g][i][1]))));
+      big = wave_max(big);
+      int ex = 0;
+      if (big > 0.0f && big < INFINITY) ex = __builtin_amdgcn_frexp_expf(big) - 15;
+      qscale = __builtin_ldexpf(1.0f, ex);
+      const float down = __builtin_ldexpf(1.0f, -ex);
+#pragma unroll
+      for (int c = 0; c < (MF ? NV : 0); ++c)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) qb[c][i] = (f16)(wide(qb[c][i]) * down);
+#pragma unroll
+      for (int g = 0; g < (MF ? 0 : G); ++g)
+#pragma unroll
+        for (int i = 0; i < EPL / 2; ++i)
+          q[g][i] = f16x2{(f16)(wide(q[g][i][0]) * down), (f16)(wide(q[g][i][1]) * down)};
     }
 
     // Matrix-core kernels keep one (max, sum) per lane, for head lane % 16,
@@ -778,8 +821,9 @@ void paged_decode_kernel(const Params p) {
       // ragged shifts (which move rows back by up to the lane's own row, so
       // without the row they would point before the page) and the second
       // key row of a pair. What stays is the step's first row (inside the
-      // page) plus chunk offsets inside that row.
-      const bool dummy = !s_real[u];
+      // page) plus chunk offsets inside that row. (A 1-deep ring reloads
+      // once per unit; it keeps the plain reload and its registers.)
+      const bool dummy = NBUF > 1 && !s_real[u];
       const uint32_t lm = dummy ? 0u : ~0u;
       const int dk = dummy ? 0 : last_dk;                 // K row shift
       const int dv0 = dummy ? 0 : last_dv0;               // first value row of the pair
@@ -938,7 +982,7 @@ void paged_decode_kernel(const Params p) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float pr = __builtin_amdgcn_exp2f(x[e]);
-        if constexpr (BF) {
+        if constexpr (BFM) {
           const bf16 r16 = (bf16)pr;
           pb[e] = __builtin_bit_cast(f16, r16);
           l[0] += (float)r16;
@@ -959,7 +1003,7 @@ void paged_decode_kernel(const Params p) {
       }
       const f16* const vr = vt + (4 * mg + ((lane & 15) >> 2)) * kVRow + 4 * (lane & 3);
 #pragma unroll
-      for (int i = 0; i < D / 16; ++i) ob[i] = mfma_k16<BF>(read_tr(vr + 16 * i), pb, ob[i]);
+      for (int i = 0; i < D / 16; ++i) ob[i] = mfma_k16<BFM>(read_tr(vr + 16 * i), pb, ob[i]);
     };
 
     // 8-bit matrix-core step with one step in flight (D >= 256), first part:
@@ -976,7 +1020,7 @@ void paged_decode_kernel(const Params p) {
       sacc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
       ks_own = 1.0f;
       if constexpr (Q8) {
-        ks_own = (float)ksb[u];
+        ks_own = (float)ksb[u] * qscale;
         const f16x2 vsc = {vs_own_b[u], vs_own_b[u]};
 #pragma unroll
         for (int j = 0; j < NV / 2; ++j) {
@@ -986,7 +1030,7 @@ void paged_decode_kernel(const Params p) {
             q8_chunk(kb[u][j], vb[u][j], h, vsc, kc, vc);
             *reinterpret_cast<f16x8*>(vt + lk * kVRow + mf_elem(2 * j + h)) =
                 zero_unless(vc, vok);
-            sacc = mfma_k32<BF>(kc, qb[2 * j + h], sacc);
+            sacc = mfma_k32<BFM>(kc, qb[2 * j + h], sacc);
           }
         }
       }
@@ -1020,8 +1064,8 @@ void paged_decode_kernel(const Params p) {
         // lane holds keys 4 mg .. 4 mg + 3 of head lane % 16.
         f32x4 sacc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int c = 0; c < NV; ++c) sacc = mfma_k32<BF>(kc[c], qb[c], sacc);
-        mf_back(sacc, t0, min(len, t0 + s_kin[u]), Q8 ? (float)ksb[u] : 1.0f, vc,
+        for (int c = 0; c < NV; ++c) sacc = mfma_k32<BFM>(kc[c], qb[c], sacc);
+        mf_back(sacc, t0, min(len, t0 + s_kin[u]), Q8 ? (float)ksb[u] * qscale : 1.0f, vc,
                 std::true_type{});
         return;
       } else {
@@ -1047,7 +1091,7 @@ void paged_decode_kernel(const Params p) {
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         float acc;
-        if constexpr (BF) {
+        if constexpr (BFM) {
           acc = dot2_first_bf16(__builtin_bit_cast(bf16x2, q[g][0]),
                                 __builtin_bit_cast(bf16x2, kp2[0]));
 #pragma unroll
@@ -1067,7 +1111,7 @@ void paged_decode_kernel(const Params p) {
       // metal_kernels.py:52 KEY_SCALE).
       float sl2 = p.scale_log2;
       if constexpr (Q8) {
-        const float ksf = (float)ksb[u];
+        const float ksf = (float)ksb[u] * qscale;
         sl2 *= ksf;
         if (p.softcap > 0.0f) {
 #pragma unroll
@@ -1191,7 +1235,7 @@ void paged_decode_kernel(const Params p) {
           // values, so the weights stay a normalised combination.
           const float pr = __builtin_amdgcn_exp2f(x[g]);
           const float other = pair_swap<R>(pr);
-          if constexpr (BF) {
+          if constexpr (BFM) {
             const bf16x2 pp = bf16x2{(bf16)pr, (bf16)other};
             l[g] = __builtin_amdgcn_fdot2_f32_bf16(pp, bf16x2{(bf16)1.0f, (bf16)1.0f}, l[g], false);
 #pragma unroll
@@ -1232,7 +1276,7 @@ void paged_decode_kernel(const Params p) {
 #pragma unroll
             for (int i = 0; i < 8; ++i)
               o[g][8 * v + i] = __builtin_fmaf(
-                  pr, BF ? (float)__builtin_bit_cast(bf16x8, vd[v])[i] : (float)vd[v][i],
+                  pr, BFM ? (float)__builtin_bit_cast(bf16x8, vd[v])[i] : (float)vd[v][i],
                   o[g][8 * v + i]);
           }
         }
@@ -1417,7 +1461,8 @@ void paged_decode_kernel(const Params p) {
   }
   if (!p.local) {
     // The first wave of the pair records the meeting point for the merge.
-    if (!back && lane == 0) p.meet[pair] = taken;
+    // (Fixed split: the merge knows the point without it.)
+    if (!back && lane == 0 && !p.fixed) p.meet[pair] = taken;
     return;
   }
   // Local mode: the workgroup's unit from its waves' pieces, the same
@@ -1468,7 +1513,9 @@ struct UnitPieces {
     const int q = qa + (j >> 1);
     const int64_t X = range_start(q, total, pairs);
     const int64_t Xn = range_start(q + 1, total, pairs);
-    const int64_t M = X + p.meet[q];
+    // Fixed split: the first wave took the first half (no load, so the
+    // merge saves a dependent trip).
+    const int64_t M = X + (p.fixed ? (Xn - X) / 2 : p.meet[q]);
     if ((j & 1) == 0)
       return X < M && X < e && M > s ? 2 * (2 * q) + (X >= s ? 0 : 1) : -1;
     return M < Xn && M < e && Xn > s ? 2 * (2 * q + 1) + (M >= s ? 0 : 1) : -1;
@@ -1762,15 +1809,19 @@ KernelPair pair_for_g(int g) {
 KernelPair kernels_f16(int d, int g);
 KernelPair kernels_bf16(int d, int g);
 KernelPair kernels_q8(int d, int g);
+// 8-bit K/V with bf16 queries and output (bf16 models).
+KernelPair kernels_q8_bf16(int d, int g);
 // Generic kernels for any other even head dim up to 512, padded to `dp`, a
 // power of two from 8 to 512.
 KernelPair kernels_gen_f16(int dp, int g);
 KernelPair kernels_gen_bf16(int dp, int g);
 KernelPair kernels_gen_q8(int dp, int g);
+KernelPair kernels_gen_q8_bf16(int dp, int g);
 // Matrix-core kernels (5 to 16 query heads per unit): head dims 64, 96,
 // 128, 256 in fp16 and bf16; 64, 128, 256 over 8-bit K/V.
 KernelPair kernels_mf(int d, bool bf16);
 KernelPair kernels_mf_q8(int d);
+KernelPair kernels_mf_q8_bf16(int d);
 // Matrix-core kernels at D = 512 (fp16, bf16 and 8-bit): four-wave
 // workgroups, accumulators in AGPRs; a translation unit built without the
 // VGPR-only matrix-core form.

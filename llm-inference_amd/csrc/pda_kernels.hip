@@ -118,9 +118,13 @@ int workspace_dim(int d) { return std::max(kernel_dim(d, false), kernel_dim(d, t
 
 KernelPair kernels_for(int d, int g, bool q8, bool bf16 = false) {
   if (d <= 0 || d > 512 || d % 2) return {};
-  if (fast_dim(d, q8)) return bf16 ? kernels_bf16(d, g) : q8 ? kernels_q8(d, g) : kernels_f16(d, g);
+  if (fast_dim(d, q8)) {
+    if (q8) return bf16 ? kernels_q8_bf16(d, g) : kernels_q8(d, g);
+    return bf16 ? kernels_bf16(d, g) : kernels_f16(d, g);
+  }
   const int dp = generic_dim(d);
-  return bf16 ? kernels_gen_bf16(dp, g) : q8 ? kernels_gen_q8(dp, g) : kernels_gen_f16(dp, g);
+  if (q8) return bf16 ? kernels_gen_q8_bf16(dp, g) : kernels_gen_q8(dp, g);
+  return bf16 ? kernels_gen_bf16(dp, g) : kernels_gen_f16(dp, g);
 }
 
 // Keys one wave step covers for a head dim (generic kernels: 8 elements per
@@ -474,7 +478,7 @@ int plan_launch(const Plan& pl, int32_t batch, int32_t kv_heads, int32_t head_di
                 int32_t page_size, bool q8, bool bf16, bool need_device, LaunchPlan* out) {
   LaunchPlan lp;
   lp.kp = pl.mf ? (head_dim == 512 ? kernels_mf512(q8, bf16)
-                   : q8 ? kernels_mf_q8(head_dim)
+                   : q8 ? (bf16 ? kernels_mf_q8_bf16(head_dim) : kernels_mf_q8(head_dim))
                         : kernels_mf(head_dim, bf16))
                 : kernels_for(head_dim, pl.G, q8, bf16);
   if (!lp.kp.split) return fail(PDA_ERR_HEAD_DIM, "head_dim %d has no kernel", head_dim);
@@ -670,8 +674,8 @@ extern "C" {
       int32_t longest, float scale, int32_t window, float softcap,             \
       int32_t split_pages, int32_t flags, void *workspace,                     \
       size_t workspace_bytes, void *stream
-#define PDA_DECODE_ARGS_Q8                                                     \
-  queries, keys, values, key_scales, value_scales, false, tables, lengths, out,\
+#define PDA_DECODE_ARGS_Q8(BF16)                                               \
+  queries, keys, values, key_scales, value_scales, BF16, tables, lengths, out, \
       batch, q_heads, kv_heads, head_dim, page_size, table_stride, arena_rows, \
       layout, longest, scale, window, softcap, split_pages, flags, workspace,  \
       workspace_bytes, stream
@@ -683,8 +687,6 @@ int pda_decode_describe(int32_t batch, int32_t q_heads, int32_t kv_heads, int32_
   if (!info) return fail(PDA_ERR_INVALID_ARGUMENT, "info is null");
   if (kv_bits != 16 && kv_bits != 8)
     return fail(PDA_ERR_INVALID_ARGUMENT, "kv_bits must be 16 or 8, got %d", kv_bits);
-  if (bf16 && kv_bits == 8)
-    return fail(PDA_ERR_INVALID_ARGUMENT, "8-bit K/V takes fp16 queries");
   const bool q8 = kv_bits == 8;
   Plan pl;
   int rc = make_plan(batch, q_heads, kv_heads, head_dim, page_size, table_stride, longest,
@@ -752,19 +754,37 @@ int pda_decode_merge_bf16(PDA_DECODE_PARAMS) { return decode(kPassMerge, PDA_DEC
 int pda_paged_decode_attention_q8(PDA_DECODE_PARAMS_Q8) {
   if (!key_scales || !value_scales)
     return fail(PDA_ERR_INVALID_ARGUMENT, "8-bit K/V needs key and value scales");
-  return decode(kPassSplit | kPassMerge, PDA_DECODE_ARGS_Q8);
+  return decode(kPassSplit | kPassMerge, PDA_DECODE_ARGS_Q8(false));
 }
 
 int pda_decode_split_q8(PDA_DECODE_PARAMS_Q8) {
   if (!key_scales || !value_scales)
     return fail(PDA_ERR_INVALID_ARGUMENT, "8-bit K/V needs key and value scales");
-  return decode(kPassSplit, PDA_DECODE_ARGS_Q8);
+  return decode(kPassSplit, PDA_DECODE_ARGS_Q8(false));
 }
 
 int pda_decode_merge_q8(PDA_DECODE_PARAMS_Q8) {
   if (!key_scales || !value_scales)
     return fail(PDA_ERR_INVALID_ARGUMENT, "8-bit K/V needs key and value scales");
-  return decode(kPassMerge, PDA_DECODE_ARGS_Q8);
+  return decode(kPassMerge, PDA_DECODE_ARGS_Q8(false));
+}
+
+int pda_paged_decode_attention_q8_bf16(PDA_DECODE_PARAMS_Q8) {
+  if (!key_scales || !value_scales)
+    return fail(PDA_ERR_INVALID_ARGUMENT, "8-bit K/V needs key and value scales");
+  return decode(kPassSplit | kPassMerge, PDA_DECODE_ARGS_Q8(true));
+}
+
+int pda_decode_split_q8_bf16(PDA_DECODE_PARAMS_Q8) {
+  if (!key_scales || !value_scales)
+    return fail(PDA_ERR_INVALID_ARGUMENT, "8-bit K/V needs key and value scales");
+  return decode(kPassSplit, PDA_DECODE_ARGS_Q8(true));
+}
+
+int pda_decode_merge_q8_bf16(PDA_DECODE_PARAMS_Q8) {
+  if (!key_scales || !value_scales)
+    return fail(PDA_ERR_INVALID_ARGUMENT, "8-bit K/V needs key and value scales");
+  return decode(kPassMerge, PDA_DECODE_ARGS_Q8(true));
 }
 
 }  // extern "C"

@@ -60,6 +60,7 @@ SIGNATURES["pda_paged_decode_attention_noalloc"] = (
 _DECODE_ARGS_Q8 = _DECODE_ARGS[:3] + [c_void_p, c_void_p] + _DECODE_ARGS[3:]
 for _name in ("pda_paged_decode_attention_q8", "pda_decode_split_q8", "pda_decode_merge_q8"):
     SIGNATURES[_name] = (ctypes.c_int, _DECODE_ARGS_Q8)
+    SIGNATURES[_name + "_bf16"] = (ctypes.c_int, _DECODE_ARGS_Q8)
 SIGNATURES["pda_rope_append"] = (
     ctypes.c_int,
     [c_void_p] * 8 + [c_int32] * 5 + [c_int64, c_int32, c_int32, c_void_p, c_void_p],

@@ -112,7 +112,7 @@ class DecodeBatch:
                         softcap: float) -> torch.Tensor:
         group = self.cache.layer_group[layer]
         out = paged_decode_attention(
-            q.to(self.cache.compute_dtype).contiguous(),
+            q.to(self.cache.decode_dtype).contiguous(),
             self.cache.keys[layer],
             self.cache.values[layer],
             self._tables[group.name],

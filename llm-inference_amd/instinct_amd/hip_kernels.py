@@ -169,7 +169,10 @@ def paged_decode_attention(
     ``scales`` = (key_scales, value_scales) selects 8-bit K/V
     (metal_kernels.py:134-141): ``keys``/``values`` are int8 arenas and the
     scales fp16, one per (row, kv head): ``[rows, kv_heads]`` beside a row
-    arena, ``[pages, kv_heads, page_size]`` beside a page-tile arena."""
+    arena, ``[pages, kv_heads, page_size]`` beside a page-tile arena. The
+    queries are fp16 or bf16 (a bf16 model's 8-bit cache) and the output
+    takes their dtype, as the reference's quantized kernel does
+    (metal_kernels.py:196-206)."""
     q8 = scales is not None
     batch, q_heads, head_dim = (int(n) for n in queries.shape)
     kv_heads = int(keys.shape[1])
@@ -185,9 +188,9 @@ def paged_decode_attention(
                          "[pages, kv_heads, page_size, head_dim]")
     if q_heads % kv_heads:
         raise ValueError("query heads must be a multiple of kv heads")
-    # bf16 queries select bf16 K/V and output (the model dtype of bf16
-    # models); 8-bit K/V take fp16 queries.
-    bf16 = queries.dtype == torch.bfloat16 and not q8
+    # bf16 queries select a bf16 output and, at 16 bits, bf16 K/V (the model
+    # dtype of bf16 models); 8-bit K/V take fp16 or bf16 queries.
+    bf16 = queries.dtype == torch.bfloat16
     q_dtype = torch.bfloat16 if bf16 else torch.float16
     kv_dtype = torch.int8 if q8 else q_dtype
     for name, t, dtype in (("queries", queries, q_dtype), ("keys", keys, kv_dtype),
@@ -228,7 +231,7 @@ def paged_decode_attention(
     if out.dtype != q_dtype or tuple(out.shape) != tuple(queries.shape) or not out.is_cuda:
         raise ValueError("out must match the queries' shape and dtype")
     entry = {"both": "pda_paged_decode_attention", "split": "pda_decode_split",
-             "merge": "pda_decode_merge"}[passes] + ("_q8" if q8 else "_bf16" if bf16 else "")
+             "merge": "pda_decode_merge"}[passes] + ("_q8" if q8 else "") + ("_bf16" if bf16 else "")
     extra = (scales[0].data_ptr(), scales[1].data_ptr()) if q8 else ()
     rc = getattr(_lib.library(), entry)(
         queries.data_ptr(), keys.data_ptr(), values.data_ptr(), *extra, tables.data_ptr(),

@@ -272,10 +272,17 @@ class KVCache:
 
     @property
     def compute_dtype(self) -> torch.dtype:
-        """The element type the kernels take for queries and new K/V: the
-        model dtype at 16 bits; fp16 at 8 bits, whose kernels dequantize to
-        fp16."""
+        """The element type the append and prefill kernels take for queries
+        and new K/V: the model dtype at 16 bits; fp16 at 8 bits, whose
+        kernels dequantize to fp16."""
         return self.dtype if self.bits == 16 else torch.float16
+
+    @property
+    def decode_dtype(self) -> torch.dtype:
+        """The query and output type of the decode call: the model dtype, at
+        16 bits and at 8 (the reference's quantized kernel runs on the
+        queries' dtype, metal_kernels.py:196-206)."""
+        return self.dtype
 
     @property
     def _stores(self) -> tuple[dict[int, torch.Tensor], ...]:

@@ -326,8 +326,11 @@ def test_describe_reports_each_configuration(shape, split, merge):
 def test_describe_validation():
     with pytest.raises(_lib.PdaError):
         _lib.describe(4, 28, 4, 128, 16, 64, 1000, 0, kv_bits=4)
-    with pytest.raises(_lib.PdaError):
-        _lib.describe(4, 28, 4, 128, 16, 64, 1000, 0, kv_bits=8, bf16=True)
+    # bf16 queries over an 8-bit cache: the 8-bit kernels' arithmetic, bf16
+    # output (the merge kernels write bf16).
+    info = _lib.describe(4, 28, 4, 128, 16, 64, 1000, 0, kv_bits=8, bf16=True)
+    assert info["split_kernel"] == "paged_decode_kernel<128,16,true,true,false,true>"
+    assert info["merge_kernel"].endswith("<128,16,true,false>")
     with pytest.raises(ValueError):
         _lib.describe(4, 30, 4, 128, 16, 64, 1000, 0)
     # Generic head dims report their padded kernel; units of large groups.
