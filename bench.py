@@ -12,8 +12,10 @@ and another 1 GiB read, so the 256 MB Infinity Cache and the L2s hold none of
 the arena and no dirty lines (flushed = HBM numbers); a second pass without
 the flush is reported as "warm".
 value = algorithmic K/V bytes / median call time (GB/s). The CPU baseline is
-the oracle's threaded C++ restatement of the reference's split-K algorithm,
-timed on a bounded sample of the same workload on this host's cores.
+the oracle's threaded C++ float32 restatement of the reference's MLX CPU
+(portable) decode path, gather then dense attention, timed on a bounded
+sample of the same workload on this host's cores; the restatement of the
+reference's split-K algorithm is timed beside it as a second record.
 Also reported: the step before the call, RoPE of the new queries and keys
 plus the K/V append into the arena (one launch, "append"), and one layer's
 decode attention step (append then call, "layer_step_us"), both flushed, and
@@ -60,7 +62,7 @@ def parse():
                          "matrix-core vs VALU study")
     ap.add_argument("--split-pages", type=int, default=0)
     ap.add_argument("--deterministic", action="store_true", default=True,
-                    help="fixed split points (PDA_DECODE_FIXED_SPLIT; the default): bitwise "
+                    help="fixed split points (the library's default, flags 0): bitwise "
                          "reproducible output")
     ap.add_argument("--racing", dest="deterministic", action="store_false",
                     help="racing wave pairs instead of fixed split points: the two waves of "
@@ -677,6 +679,8 @@ def main():
     names = decode_kernel_names(w.q_heads, w.kv_heads, w.head_dim, bits=args.kv_bits,
                                 bf16=bf16, split_pages=args.split_pages, **merge_shape_of(w))
     traffic_key = f"{w.name}/{w.layout}/{'bf16' if bf16 else 'f16'}/kv{args.kv_bits}"
+    if not args.deterministic:
+        traffic_key += "/racing"
     traffic = None
     if TRAFFIC_FILE.exists():
         traffic = json.loads(TRAFFIC_FILE.read_text()).get(traffic_key, {}).get(

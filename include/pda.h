@@ -67,8 +67,11 @@ extern "C" {
 #define PDA_ERR_HIP (-8)              /* a HIP runtime call failed            */
 
 /* Flags of the decode calls (the `flags` argument, 0 = none). */
-#define PDA_DECODE_FIXED_SPLIT 1 /* fixed split points: bitwise reproducible
-                                    output (see pda_paged_decode_attention) */
+#define PDA_DECODE_FIXED_SPLIT 1 /* fixed split points, bitwise reproducible
+                                    output: the default, also taken with
+                                    flags = 0 (see pda_paged_decode_attention) */
+#define PDA_DECODE_RACING 2      /* opt-in: racing wave pairs, output bits may
+                                    differ between calls on the same inputs */
 
 /* K/V arena layouts (the `layout` argument of the decode calls). */
 #define PDA_LAYOUT_ROWS 0  /* [rows, kv_heads, head_dim], the reference's   */
@@ -151,14 +154,15 @@ int pda_decode_describe(int32_t batch, int32_t q_heads, int32_t kv_heads,
  * (its IN_HEAD guard and PAGE template, metal_kernels.py:28-30,204), any even
  * head_dim up to 512 and any page_size are accepted: head dims 64, 80, 96,
  * 128, 256, 512 run tuned kernels, the others a generic one.
- * `flags`: 0, or PDA_DECODE_FIXED_SPLIT. Without it the two waves that share
- * a stretch of pages split it wherever their shared counter runs out (the
- * faster wave takes more), so where a sequence is cut, and the rounding of
- * its partial results, can differ between two calls on the same inputs
- * (within the parity bar). With it the split points are fixed by the
- * shapes, the lengths and the device's CU count, and repeated calls give
- * bitwise-identical output, as the reference's fixed split ranges do
- * (metal_kernels.py:32-36).
+ * `flags`: 0 (or PDA_DECODE_FIXED_SPLIT, the same) or PDA_DECODE_RACING.
+ * By default the split points are fixed by the shapes, the lengths and the
+ * device's CU count, and repeated calls give bitwise-identical output, as
+ * the reference's fixed split ranges do (metal_kernels.py:32-36). With
+ * PDA_DECODE_RACING the two waves that share a stretch of pages split it
+ * wherever their shared counter runs out (the faster wave takes more), so
+ * where a sequence is cut, and the rounding of its partial results, can
+ * differ between two calls on the same inputs (within the parity bar).
+ * Both flags at once, or any other bit, is PDA_ERR_INVALID_ARGUMENT.
  * Launches a split kernel and a merge kernel on `stream`; calls that share a
  * workspace must not overlap. */
 int pda_paged_decode_attention(const void* queries, const void* keys,

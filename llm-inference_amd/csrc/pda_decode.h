@@ -637,7 +637,8 @@ void paged_decode_kernel(const Params p) {
     // keys are exact in fp16, so the queries go to fp16 as well, scaled by a
     // power of two chosen per unit that puts the largest in [2^14, 2^15).
     // Every bf16 value (8 significant bits) then converts exactly, unless it
-    // is below 2^-17 of the largest (fp16 subnormals), and each score is
+    // is more than 2^31 times smaller than the largest (below 2^-17 after
+    // scaling, where fp16 subnormals hold fewer than 8 bits), and each score is
     // multiplied back by the same power of two (qscale, folded into the key
     // scale), which is exact. The rest runs as for fp16 queries; only the
     // output is rounded to bf16. (Converting bf16 to fp16 unscaled would

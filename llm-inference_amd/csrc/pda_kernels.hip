@@ -522,8 +522,10 @@ int decode(int passes, const void* queries, const void* keys, const void* values
                 (long long)arena_rows);
   if (layout != PDA_LAYOUT_ROWS && layout != PDA_LAYOUT_PAGES)
     return fail(PDA_ERR_INVALID_ARGUMENT, "unknown K/V layout %d", layout);
-  if (flags & ~PDA_DECODE_FIXED_SPLIT)
+  if (flags & ~(PDA_DECODE_FIXED_SPLIT | PDA_DECODE_RACING))
     return fail(PDA_ERR_INVALID_ARGUMENT, "unknown decode flags 0x%x", flags);
+  if ((flags & PDA_DECODE_FIXED_SPLIT) && (flags & PDA_DECODE_RACING))
+    return fail(PDA_ERR_INVALID_ARGUMENT, "PDA_DECODE_FIXED_SPLIT and PDA_DECODE_RACING together");
   const int elem = q8 ? 1 : 2;  // bytes per K/V element
   const int64_t page_bytes = (int64_t)page_size * kv_heads * head_dim * elem;
   if (page_bytes > INT32_MAX)
@@ -614,7 +616,7 @@ int decode(int passes, const void* queries, const void* keys, const void* values
   prm.window = window;
   prm.grid_pairs = groups * wg_pairs;
   prm.min_pages = pl.min_pages;
-  prm.fixed = (flags & PDA_DECODE_FIXED_SPLIT) ? 1 : 0;
+  prm.fixed = (flags & PDA_DECODE_RACING) ? 0 : 1;
   static const int balance = [] {
     const char* e = getenv("PDA_FIXED_BALANCE");
     return e && *e ? atoi(e) : 1;

@@ -28,6 +28,7 @@ PDA_ERR_HIP = -8
 
 # Decode flags (pda.h).
 PDA_DECODE_FIXED_SPLIT = 1  # fixed split points: bitwise reproducible output
+PDA_DECODE_RACING = 2  # racing wave pairs (opt-in): output bits may differ between calls
 
 # K/V arena layouts (pda.h).
 PDA_LAYOUT_ROWS = 0   # [rows, kv_heads, head_dim], the reference's arena

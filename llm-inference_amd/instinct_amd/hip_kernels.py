@@ -156,13 +156,13 @@ def paged_decode_attention(
     one of the two kernels only (the output is complete after the merge).
     ``workspace``: a uint8 device tensor the caller owns (at least
     :func:`decode_workspace_bytes`), else the stream's cached one.
-    ``deterministic`` (default): fixed split points
-    (``PDA_DECODE_FIXED_SPLIT``), so repeated calls on the same inputs give
-    bitwise-identical outputs, as the reference's fixed split ranges do
-    (metal_kernels.py:32-36). ``deterministic=False`` lets the two waves
-    that share a stretch of pages split it wherever they meet (the faster
-    takes more), so the last bits of a sequence's output can differ from
-    call to call (within the parity bar).
+    ``deterministic`` (default): fixed split points (the library's default,
+    flags 0), so repeated calls on the same inputs give bitwise-identical
+    outputs, as the reference's fixed split ranges do
+    (metal_kernels.py:32-36). ``deterministic=False`` passes
+    ``PDA_DECODE_RACING``: the two waves that share a stretch of pages split
+    it wherever they meet (the faster takes more), so the last bits of a
+    sequence's output can differ from call to call (within the parity bar).
     Any even ``head_dim`` up to 512 and any ``page_size`` are accepted, as by
     the reference op (metal_kernels.py:28-30,204).
 
@@ -238,7 +238,7 @@ def paged_decode_attention(
         lengths.data_ptr(), out.data_ptr(), batch, q_heads, kv_heads, head_dim,
         int(page_size), stride, arena_rows, layout, int(longest), float(scale),
         int(window), float(softcap), int(split_pages),
-        _lib.PDA_DECODE_FIXED_SPLIT if deterministic else 0, ws.data_ptr(),
+        0 if deterministic else _lib.PDA_DECODE_RACING, ws.data_ptr(),
         ws.numel(), ctypes.c_void_p(stream))
     _lib.check(rc)
     return out

@@ -171,7 +171,9 @@ void decode_validation(bool may_reach_hip) {
         {[](DecodeArgs& a) { a.ws = buf(32768 + 16); }, PDA_ERR_ALIGNMENT},
         {[](DecodeArgs& a) { a.scale = 0.0f / 0.0f; }, PDA_ERR_INVALID_ARGUMENT},
         {[](DecodeArgs& a) { a.softcap = -1.0f; }, PDA_ERR_INVALID_ARGUMENT},
-        {[](DecodeArgs& a) { a.flags = 2; }, PDA_ERR_INVALID_ARGUMENT},
+        {[](DecodeArgs& a) { a.flags = 4; }, PDA_ERR_INVALID_ARGUMENT},
+        {[](DecodeArgs& a) { a.flags = PDA_DECODE_FIXED_SPLIT | PDA_DECODE_RACING; },
+         PDA_ERR_INVALID_ARGUMENT},
         {[](DecodeArgs& a) { a.window = -1; }, PDA_ERR_INVALID_ARGUMENT},
     };
     for (const Bad& b : bad) {
@@ -186,6 +188,8 @@ void decode_validation(bool may_reach_hip) {
       EXPECT(a.call(f) == PDA_ERR_HIP);
       a.d = 80;
       a.flags = PDA_DECODE_FIXED_SPLIT;
+      EXPECT(a.call(f) == PDA_ERR_HIP);
+      a.flags = PDA_DECODE_RACING;
       EXPECT(a.call(f) == PDA_ERR_HIP);
     }
   }

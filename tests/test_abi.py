@@ -47,7 +47,8 @@ def decode(**overrides):
     (dict(head_dim=7), _lib.PDA_ERR_HEAD_DIM),
     (dict(head_dim=514), _lib.PDA_ERR_HEAD_DIM),
     (dict(head_dim=0), _lib.PDA_ERR_INVALID_ARGUMENT),
-    (dict(flags=2), _lib.PDA_ERR_INVALID_ARGUMENT),
+    (dict(flags=4), _lib.PDA_ERR_INVALID_ARGUMENT),
+    (dict(flags=_lib.PDA_DECODE_FIXED_SPLIT | _lib.PDA_DECODE_RACING), _lib.PDA_ERR_INVALID_ARGUMENT),
     (dict(kv_heads=0), _lib.PDA_ERR_INVALID_ARGUMENT),
     (dict(batch=-1), _lib.PDA_ERR_INVALID_ARGUMENT),
     (dict(window=-1), _lib.PDA_ERR_INVALID_ARGUMENT),

@@ -10,9 +10,10 @@ step per page. All of it is checked against the float64 oracle (bar: the
 north star's max-abs 2e-3 / mean-abs 2e-4 for fp16; bf16 and 8-bit as in
 their own test files), in both arena layouts.
 
-PDA_DECODE_FIXED_SPLIT (``deterministic=True``) fixes where the wave pairs
-cut the page stream, so repeated calls are bitwise identical, as the
-reference's fixed split ranges make its output (metal_kernels.py:32-36).
+Fixed split points (``deterministic=True``, the default; flags 0 at the
+C-ABI) fix where the wave pairs cut the page stream, so repeated calls are
+bitwise identical, as the reference's fixed split ranges make its output
+(metal_kernels.py:32-36); ``deterministic=False`` passes PDA_DECODE_RACING.
 """
 
 import math
@@ -242,7 +243,7 @@ def test_ragged_pages_with_window_released_pages_and_poison(gpu):
     ("config5", dict(batch=48, low=16, high=16384, shared=8, prefix=1024)),
 ])
 def test_fixed_split_is_bitwise_reproducible(gpu, name, kw):
-    """Five calls with PDA_DECODE_FIXED_SPLIT give the same bits, within the
+    """Five calls with fixed split points give the same bits, within the
     parity bar of the oracle; config 3 carries the planted x8 keys whose
     large logits make the merge's rescaling matter most."""
     w = getattr(workloads, name)(device=gpu, **kw).to_layout("pages")

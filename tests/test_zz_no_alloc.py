@@ -66,16 +66,19 @@ def test_noalloc_matches_the_workspace_call_on_two_calls(gpu):
     small = workloads.config2(device=gpu, seed=9, batch=5, low=100, high=900)
     for name, w in (("first (B=32)", big), ("second (B=5, smaller)", small)):
         want = oracle(w)
-        rc, fixed = noalloc(w, _lib.PDA_DECODE_FIXED_SPLIT)
+        rc, fixed = noalloc(w, 0)  # the default: fixed split points
         _lib.check(rc)
         ref_fixed = with_workspace(w, True)
         assert torch.equal(fixed, ref_fixed), f"{name}: fixed split differs from the workspace call"
         within_bar(fixed, want, f"{name} fixed vs oracle")
-        rc, free = noalloc(w, 0)
+        rc, explicit = noalloc(w, _lib.PDA_DECODE_FIXED_SPLIT)
+        _lib.check(rc)
+        assert torch.equal(explicit, fixed), f"{name}: PDA_DECODE_FIXED_SPLIT differs from flags 0"
+        rc, free = noalloc(w, _lib.PDA_DECODE_RACING)
         _lib.check(rc)
         within_bar(free.float().cpu().numpy(), ref_fixed.float().cpu().numpy(),
-                   f"{name} default vs workspace call")
-        within_bar(free, want, f"{name} default vs oracle")
+                   f"{name} racing vs workspace call")
+        within_bar(free, want, f"{name} racing vs oracle")
 
 
 def test_noalloc_at_512_wide_heads_on_four_wave_workgroups(gpu):
