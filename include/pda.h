@@ -59,7 +59,7 @@ extern "C" {
 #define PDA_OK 0
 #define PDA_ERR_INVALID_ARGUMENT (-1) /* null pointer, non-positive size, ... */
 #define PDA_ERR_HEAD_RATIO (-2)       /* q_heads is not a multiple of kv_heads */
-#define PDA_ERR_HEAD_DIM (-3)         /* head_dim odd, or above 512           */
+#define PDA_ERR_HEAD_DIM (-3)         /* head_dim not in 1..512               */
 #define PDA_ERR_PAGE_SIZE (-4)        /* (no longer returned: any page size)  */
 #define PDA_ERR_WORKSPACE (-5)        /* workspace missing or too small       */
 #define PDA_ERR_ALIGNMENT (-6)        /* fp16 buffers must be 16-byte aligned */
@@ -151,9 +151,11 @@ int pda_decode_describe(int32_t batch, int32_t q_heads, int32_t kv_heads,
  * beyond rounding). `arena_rows` is the row count of the keys/values arenas
  * (pages x page_size) and `layout` is PDA_LAYOUT_ROWS or PDA_LAYOUT_PAGES (the
  * reference has one layout, rows); batch <= 8184. Like the reference op
- * (its IN_HEAD guard and PAGE template, metal_kernels.py:28-30,204), any even
+ * (its IN_HEAD guard and PAGE template, metal_kernels.py:28-30,204), any
  * head_dim up to 512 and any page_size are accepted: head dims 64, 80, 96,
- * 128, 256, 512 run tuned kernels, the others a generic one.
+ * 128, 256, 512 run tuned kernels, the other even ones a generic one, odd
+ * ones (rows 2-byte aligned) a generic one that moves single elements and
+ * serves one query head per unit.
  * `flags`: 0 (or PDA_DECODE_FIXED_SPLIT, the same) or PDA_DECODE_RACING.
  * By default the split points are fixed by the shapes, the lengths and the
  * device's CU count, and repeated calls give bitwise-identical output, as
@@ -279,9 +281,9 @@ int pda_decode_merge_bf16(const void* queries, const void* keys, const void* val
  * Here K rows are converted exactly to fp16 and each score is multiplied by
  * its key's scale; V rows are dequantized to fp16(int8 x scale), the value
  * the reference's gather hands its portable path (paged_kv.py:285-292).
- * Any even head_dim up to 512 (64, 128, 256 on the matrix cores at any GQA
+ * Any head_dim up to 512 (64, 128, 256 on the matrix cores at any GQA
  * group, 512 on them from 4 heads per kv head and tuned VALU kernels below,
- * the others, 80 included, generic); every other
+ * the others, 80 and the odd ones included, generic); every other
  * argument as for the fp16 call, which
  * shares the workspace sizing (pda_workspace_bytes). The split and merge
  * passes exist as for fp16; merge with the _q8 entry after a _q8 split. */
@@ -468,10 +470,11 @@ int pda_prefill_workspace_bytes(int32_t start, int32_t count, int32_t q_heads,
  * num_images is 0) lists image-token spans [begin, end) of positions: a
  * query inside a span also sees every key of that span up to the chunk's
  * end, whatever the causal limit and the window (batches.py:107-118).
- * Any even head_dim up to 512, as for the decode call: 64, 96, 128, 256 and
- * 512 (the 512-wide heads of Gemma 4's global layers, docs/roadmap.md:36)
- * run kernels of their own, the others the next wider one with the dims
- * past head_dim zero; odd or larger head dims return PDA_ERR_HEAD_DIM.
+ * Any head_dim up to 512, as for the decode call: 64, 96, 128, 256 and 512
+ * (the 512-wide heads of Gemma 4's global layers, docs/roadmap.md:36) run
+ * kernels of their own, the others the next wider one with the dims past
+ * head_dim zero (odd ones moving single elements); larger head dims return
+ * PDA_ERR_HEAD_DIM.
  * With more than one key range
  * (see pda_prefill_workspace_bytes; results do not depend on `splits`
  * beyond fp32 rounding) the ranges' partials go to `workspace` (256-byte

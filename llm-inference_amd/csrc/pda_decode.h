@@ -126,7 +126,10 @@ constexpr int next_pow2(int x) {
 // key, loaded as four element pairs (four 4-byte loads at 16 bits, four
 // 2-byte loads at 8 bits, since rows of an odd number of pairs are not
 // 16-byte aligned); pairs at or past the real head dim are not loaded and
-// read as zero. p.v runs on FMAs.
+// read as zero. p.v runs on FMAs. Odd head dims (ODD): rows are only 2-byte
+// aligned (1-byte at 8 bits), so every element is its own load; the element
+// past the head dim reloads the last one, whose query element is zero and
+// whose output is never written.
 //
 // Matrix-core kernels (MF; use_mf in pda_kernels.hip picks the groups each
 // head dim takes them at): a step is 16 keys; lane l loads key l % 16,
@@ -136,7 +139,7 @@ constexpr int next_pow2(int x) {
 // (MF and Q8, D a multiple of 64) chunk c = 2 j + h holds elements
 // [64 j + 16 (l / 16) + 8 h, + 8) instead, so that one 16-byte load brings
 // a lane's int8 elements of two chunks; the queries follow the same order.
-template <int D, bool Q8 = false, bool GEN = false, bool MF = false>
+template <int D, bool Q8 = false, bool GEN = false, bool MF = false, bool ODD = false>
 struct Geom {
   static constexpr int EPL =
       MF ? D / 4 : GEN ? 8 : Q8 ? 16 : ((D >= 80 && D % 16 == 0) ? 16 : 8);  // per lane
@@ -155,8 +158,12 @@ struct Geom {
   // key scale and the pair's two value scales (8-bit); generic: four pieces
   // of K and of V, plus the key's two scales at 8 bits.
   // Matrix-core kernels at 8 bits: NV / 2 pieces of K and of V, the key's
-  // two scales.
-  static constexpr int LOADS = MF ? (Q8 ? NV + 2 : 2 * NV) : GEN ? (Q8 ? 10 : 8) : Q8 ? 6 : 2 * NV;
+  // two scales. Odd head dims (ODD, generic only): every element on its own,
+  // eight of K and eight of V, plus the two scales at 8 bits.
+  static constexpr int LOADS = MF ? (Q8 ? NV + 2 : 2 * NV)
+                               : GEN ? (ODD ? (Q8 ? 18 : 16) : (Q8 ? 10 : 8))
+                               : Q8 ? 6 : 2 * NV;
+  static_assert(!ODD || GEN, "odd head dims run the generic kernels");
   static_assert(!MF || (D % 32 == 0 && !GEN && (!Q8 || D % 64 == 0)),
                 "matrix-core kernels: D % 32 == 0 (8-bit: D % 64 == 0), no generic dims");
   static_assert(D % EPL == 0 && DC % 8 == 0, "head_dim must be a multiple of 8");
@@ -395,10 +402,9 @@ __device__ void build_prefix(const Params& p, int* s_prefix, int* s_len) {
 // GEN: generic kernel for a head dim p.head_dim below the padded D (Geom).
 // MF: matrix-core kernel for a GQA group of 5 to 16 query heads per unit
 // (G = 16 slots, p.unit_heads real heads; see mf_step).
-template <int D, int G, bool Q8, bool BF, bool GEN, bool MF>
-__global__ __launch_bounds__(64 * split_waves(D, MF))
-__attribute__((amdgpu_waves_per_eu(split_waves(D, MF) / 4)))
-void paged_decode_kernel(const Params p) {
+// ODD: generic kernel for an odd head dim (paged_decode_odd_kernel).
+template <int D, int G, bool Q8, bool BF, bool GEN, bool MF, bool ODD>
+__device__ __forceinline__ void split_body(const Params p) {
   constexpr int kWaves = split_waves(D, MF);  // waves of this workgroup
   constexpr int kThreads = 64 * kWaves;
   constexpr int kWgPairs = kWaves / 2;
@@ -406,7 +412,7 @@ void paged_decode_kernel(const Params p) {
   // and output with the fp16 arithmetic of the 8-bit kernels (see qscale).
   constexpr bool BFM = BF && !Q8;
   static_assert(!MF || G == 16, "matrix-core kernels lay 16 head slots out");
-  using Gm = Geom<D, Q8, GEN, MF>;
+  using Gm = Geom<D, Q8, GEN, MF, ODD>;
   constexpr int EPL = Gm::EPL, NV = Gm::NV, DC = Gm::DC, R = Gm::R, KPS = Gm::KPS;
   constexpr bool PV2 = Gm::PV2;
   constexpr int OPL = Gm::OPL;
@@ -467,7 +473,9 @@ void paged_decode_kernel(const Params p) {
   for (int bz = blockIdx.x; bz < B; bz += gridDim.x) {
     if (s_prefix[bz + 1] != s_prefix[bz]) continue;
     f16* const dz = p.out + (int64_t)bz * p.hq * hd;
-    if constexpr (GEN) {  // rows of an odd number of pairs: 4-byte stores
+    if constexpr (ODD) {  // rows of an odd number of elements: 2-byte stores
+      for (int i = tid; i < p.hq * hd; i += kThreads) dz[i] = (f16)0.0f;
+    } else if constexpr (GEN) {  // rows of an odd number of pairs: 4-byte stores
       for (int i = tid * 2; i < p.hq * hd; i += kThreads * 2)
         *reinterpret_cast<uint32_t*>(dz + i) = 0u;
     } else {
@@ -611,7 +619,10 @@ void paged_decode_kernel(const Params p) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int e = d0 + 2 * i;
-          q[g][i] = e < hd ? *reinterpret_cast<const f16x2*>(qp + e) : f16x2{};
+          if constexpr (ODD)  // 2-byte aligned rows: one element at a time
+            q[g][i] = f16x2{e < hd ? qp[e] : (f16)0.0f, e + 1 < hd ? qp[e + 1] : (f16)0.0f};
+          else
+            q[g][i] = e < hd ? *reinterpret_cast<const f16x2*>(qp + e) : f16x2{};
         }
       } else if constexpr (Q8) {
         // Elements [r * 16, r * 16 + 16), the slice of the int8 key row.
@@ -719,6 +730,12 @@ void paged_decode_kernel(const Params p) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       pair_off[i] = d0 + 2 * i < hd ? (uint32_t)((d0 + 2 * i) * kElem) : 0u;
+    // Odd head dims: the pair's second element, or its first again past the
+    // head dim (in the row; its query element is zero).
+    uint32_t pair_off2[ODD ? 4 : 1];
+#pragma unroll
+    for (int i = 0; i < (ODD ? 4 : 0); ++i)
+      pair_off2[i] = d0 + 2 * i + 1 < hd ? pair_off[i] + kElem : pair_off[i];
 
     // Page-table window: lane i holds the physical id of unit page
     // win + dir * i (lanes past the unit's ends hold an end entry and are
@@ -837,7 +854,23 @@ void paged_decode_kernel(const Params p) {
       if constexpr (GEN) {
         // Four element pairs of this lane's key row, K then V.
         const char* vk = vq + dk * rb;
-        if constexpr (Q8) {
+        if constexpr (Q8 && ODD) {
+          uint32_t kw[4], vw[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const uint8_t* k8 = reinterpret_cast<const uint8_t*>(kq);
+            const uint8_t* v8 = reinterpret_cast<const uint8_t*>(vk);
+            kw[i] = (uint32_t)k8[pair_off[i] & lm] | (uint32_t)k8[pair_off2[i] & lm] << 8;
+            vw[i] = (uint32_t)v8[pair_off[i] & lm] | (uint32_t)v8[pair_off2[i] & lm] << 8;
+          }
+          kb[u][0] = __builtin_bit_cast(
+              f16x8, i32x4{(int)(kw[0] | kw[1] << 16), (int)(kw[2] | kw[3] << 16), 0, 0});
+          vb[u][0] = __builtin_bit_cast(
+              f16x8, i32x4{(int)(vw[0] | vw[1] << 16), (int)(vw[2] | vw[3] << 16), 0, 0});
+          const int so = dk * p.scale_row;
+          ksb[u] = p.kscale[last_soff + (ks_off & lm) + so];
+          vs_own_b[u] = p.vscale[last_soff + (vs_own & lm) + so];
+        } else if constexpr (Q8) {
           uint32_t kw[4], vw[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
@@ -851,6 +884,19 @@ void paged_decode_kernel(const Params p) {
           const int so = dk * p.scale_row;
           ksb[u] = p.kscale[last_soff + (ks_off & lm) + so];
           vs_own_b[u] = p.vscale[last_soff + (vs_own & lm) + so];
+        } else if constexpr (ODD) {
+          i32x4 kw, vw;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const uint16_t* k16a = reinterpret_cast<const uint16_t*>(kq + (pair_off[i] & lm));
+            const uint16_t* k16b = reinterpret_cast<const uint16_t*>(kq + (pair_off2[i] & lm));
+            const uint16_t* v16a = reinterpret_cast<const uint16_t*>(vk + (pair_off[i] & lm));
+            const uint16_t* v16b = reinterpret_cast<const uint16_t*>(vk + (pair_off2[i] & lm));
+            kw[i] = (int)((uint32_t)*k16a | (uint32_t)*k16b << 16);
+            vw[i] = (int)((uint32_t)*v16a | (uint32_t)*v16b << 16);
+          }
+          kb[u][0] = __builtin_bit_cast(f16x8, kw);
+          vb[u][0] = __builtin_bit_cast(f16x8, vw);
         } else {
           i32x4 kw, vw;
 #pragma unroll
@@ -1384,7 +1430,20 @@ void paged_decode_kernel(const Params p) {
       for (int g = 0; g < G; ++g) {
         if (g % kWriters != writer || !writes) continue;
         const float inv = l[g] > 0.0f ? 1.0f / l[g] : 0.0f;
-        if constexpr (GEN) {
+        if constexpr (ODD) {
+          // Elements below the real head dim, 2-byte stores.
+          f16* dst = p.out + ((int64_t)b * p.hq + h0 + g) * hd;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            if (e0 + i >= hd) continue;
+            const float y = o[g][i] * inv;
+            if constexpr (BF)
+              dst[e0 + i] = __builtin_bit_cast(f16, (bf16)y);
+            else
+              dst[e0 + i] = (f16)y;
+          }
+          continue;
+        } else if constexpr (GEN) {
           // Element pairs below the real head dim, 4-byte stores.
           f16* dst = p.out + ((int64_t)b * p.hq + h0 + g) * hd;
 #pragma unroll
@@ -1497,6 +1556,26 @@ void paged_decode_kernel(const Params p) {
     else
       *dst = (f16)y;
   }
+}
+
+// Pass one (metal_kernels.py:18-101): the split kernel of every even head
+// dim, template arguments as split_body's.
+template <int D, int G, bool Q8, bool BF, bool GEN, bool MF>
+__global__ __launch_bounds__(64 * split_waves(D, MF))
+__attribute__((amdgpu_waves_per_eu(split_waves(D, MF) / 4)))
+void paged_decode_kernel(const Params p) {
+  split_body<D, G, Q8, BF, GEN, MF, false>(p);
+}
+
+// Pass one at an odd head dim (the reference's IN_HEAD guard takes any,
+// metal_kernels.py:28-30): the generic kernel of padded width D with
+// element-wise loads and stores, one query head per unit (a rare shape: its
+// GQA groups read K/V once per head).
+template <int D, bool Q8, bool BF>
+__global__ __launch_bounds__(64 * split_waves(D, false))
+__attribute__((amdgpu_waves_per_eu(split_waves(D, false) / 4)))
+void paged_decode_odd_kernel(const Params p) {
+  split_body<D, 1, Q8, BF, true, false, true>(p);
 }
 
 // The pieces of one unit for the merge kernels. The unit's pages [s, e) of
@@ -1775,9 +1854,10 @@ struct KernelPair {
   int split_waves = kSplitWaves;    // waves of a split workgroup
   int ring = kNbuf;                 // K/V steps in flight per wave
   // The split kernel's template arguments <D, G, Q8, BF, GEN, MF> (the
-  // merge kernels take <D, G, BF, GEN>), as instantiated.
+  // merge kernels take <D, G, BF, GEN>), as instantiated; odd: the split
+  // kernel is paged_decode_odd_kernel<D, Q8, BF> (G = 1, GEN).
   int d = 0, g = 0;
-  bool q8 = false, bf = false, gen = false, mf = false;
+  bool q8 = false, bf = false, gen = false, mf = false, odd = false;
 };
 
 template <int D, int G, bool Q8, bool BF, bool GEN = false, bool MF = false>
@@ -1788,6 +1868,17 @@ KernelPair make_pair() {
           split_waves(D, MF),
           ring_depth(D, G, Q8, GEN, MF),
           D, G, Q8, BF, GEN, MF};
+}
+
+// Odd head dims: one query head per unit, the generic merges.
+template <int D, bool Q8, bool BF>
+KernelPair make_odd_pair() {
+  return {paged_decode_odd_kernel<D, Q8, BF>,
+          paged_decode_merge_kernel<D, 1, BF, true>,
+          paged_decode_merge_sliced_kernel<D, 1, BF, true>,
+          split_waves(D, false),
+          ring_depth(D, 1, Q8, true, false),
+          D, 1, Q8, BF, true, false, true};
 }
 
 template <int D, bool Q8, bool BF, bool GEN = false>
@@ -1818,6 +1909,9 @@ KernelPair kernels_gen_f16(int dp, int g);
 KernelPair kernels_gen_bf16(int dp, int g);
 KernelPair kernels_gen_q8(int dp, int g);
 KernelPair kernels_gen_q8_bf16(int dp, int g);
+// Odd head dims, padded to `dp` (a power of two from 8 to 512), one query
+// head per unit: fp16 and bf16 queries over 16-bit or 8-bit K/V.
+KernelPair kernels_odd(int dp, bool q8, bool bf16);
 // Matrix-core kernels (5 to 16 query heads per unit): head dims 64, 96,
 // 128, 256 in fp16 and bf16; 64, 128, 256 over 8-bit K/V.
 KernelPair kernels_mf(int d, bool bf16);

@@ -95,8 +95,9 @@ using pda_internal::ok;
 
 // Head dims with a compiled fast path: 16-bit 64, 80, 96, 128, 256, 512;
 // 8-bit 64, 128, 256, 512 (the dims whose p.v runs on key pairs). Every
-// other even head dim up to 512 runs a generic kernel padded to a power of
-// two (any dim at 8 bits that has no fast path, 80 included).
+// other head dim up to 512 runs a generic kernel padded to a power of two
+// (any dim at 8 bits that has no fast path, 80 included; odd ones the odd
+// variant, one query head per unit).
 bool fast_dim(int d, bool q8) {
   if (q8) return d == 64 || d == 128 || d == 256 || d == 512;
   return d == 64 || d == 80 || d == 96 || d == 128 || d == 256 || d == 512;
@@ -117,7 +118,8 @@ int kernel_dim(int d, bool q8) { return fast_dim(d, q8) ? d : generic_dim(d); }
 int workspace_dim(int d) { return std::max(kernel_dim(d, false), kernel_dim(d, true)); }
 
 KernelPair kernels_for(int d, int g, bool q8, bool bf16 = false) {
-  if (d <= 0 || d > 512 || d % 2) return {};
+  if (d <= 0 || d > 512) return {};
+  if (d % 2) return g == 1 ? kernels_odd(generic_dim(d), q8, bf16) : KernelPair{};
   if (fast_dim(d, q8)) {
     if (q8) return bf16 ? kernels_q8_bf16(d, g) : kernels_q8(d, g);
     return bf16 ? kernels_bf16(d, g) : kernels_f16(d, g);
@@ -226,8 +228,8 @@ int make_plan(int32_t batch, int32_t q_heads, int32_t kv_heads, int32_t head_dim
                 window, split_pages);
   if (q_heads % kv_heads)
     return fail(PDA_ERR_HEAD_RATIO, "query heads must be a multiple of kv heads");
-  if (head_dim > 512 || head_dim % 2)
-    return fail(PDA_ERR_HEAD_DIM, "head_dim %d is not an even number up to 512", head_dim);
+  if (head_dim > 512)
+    return fail(PDA_ERR_HEAD_DIM, "head_dim %d is above 512", head_dim);
   if ((int64_t)table_stride * page_size > INT32_MAX)
     return fail(PDA_ERR_TOO_LONG, "table_stride * page_size exceeds 2^31");
   if (batch > kMaxBatch)
@@ -235,7 +237,8 @@ int make_plan(int32_t batch, int32_t q_heads, int32_t kv_heads, int32_t head_dim
   Plan pl;
   const int gtot = q_heads / kv_heads;
   pl.mf = use_mf(gtot, head_dim, q8);
-  pl.unit_heads = pl.mf ? mf_unit_heads(gtot) : heads_per_group(gtot);
+  // Odd head dims: one query head per unit (the only odd instantiation).
+  pl.unit_heads = head_dim % 2 ? 1 : pl.mf ? mf_unit_heads(gtot) : heads_per_group(gtot);
   pl.G = pl.mf ? 16 : pl.unit_heads;
   pl.nhg = gtot / pl.unit_heads;
   // The workspace holds the widest slot layout either cache type could use
@@ -716,8 +719,12 @@ int pda_decode_describe(int32_t batch, int32_t q_heads, int32_t kv_heads, int32_
   d.merge = d.local ? 0 : lp.ms.sliced ? 2 : 1;
   d.merge_waves = d.local ? 0 : lp.ms.waves;
   auto tf = [](bool x) { return x ? "true" : "false"; };
-  snprintf(d.split_kernel, sizeof(d.split_kernel), "paged_decode_kernel<%d,%d,%s,%s,%s,%s>",
-           kp.d, kp.g, tf(kp.q8), tf(kp.bf), tf(kp.gen), tf(kp.mf));
+  if (kp.odd)
+    snprintf(d.split_kernel, sizeof(d.split_kernel), "paged_decode_odd_kernel<%d,%s,%s>", kp.d,
+             tf(kp.q8), tf(kp.bf));
+  else
+    snprintf(d.split_kernel, sizeof(d.split_kernel), "paged_decode_kernel<%d,%d,%s,%s,%s,%s>",
+             kp.d, kp.g, tf(kp.q8), tf(kp.bf), tf(kp.gen), tf(kp.mf));
   if (!d.local)
     snprintf(d.merge_kernel, sizeof(d.merge_kernel), "paged_decode_merge%s_kernel<%d,%d,%s,%s>",
              lp.ms.sliced ? "_sliced" : "", kp.d, kp.g, tf(kp.bf), tf(kp.gen));

@@ -44,7 +44,8 @@
 //  * Other even head dims up to 512 (GEN) run the kernel of the next of
 //    those widths: rows are gathered as element pairs (the row length is a
 //    multiple of 4 bytes only), the pairs past the head dim are zero in Q, K
-//    and V, and only the real dims are written.
+//    and V, and only the real dims are written. Odd head dims (ODD) do the
+//    same one element at a time (paged_prefill_odd_kernel).
 
 #include <hip/hip_runtime.h>
 
@@ -159,9 +160,12 @@ constexpr int blocks_per_tile() { return D <= 128 ? 2 : 1; }
 // BF: queries, K/V and output in bf16 (bf16 models); every 16-bit value is
 // moved as raw bits and only the matrix-core steps, the probabilities and the
 // output rounding differ.
-// GEN: head dim p.head_dim (even) below D; D-wide tiles, zero past it.
-template <int D, bool Q8, bool BF, bool GEN>
-__global__ __launch_bounds__(64 * waves_for(D)) void paged_prefill_kernel(const PrefillParams p) {
+// GEN: head dim p.head_dim below D; D-wide tiles, zero past it.
+// ODD (with GEN): an odd head dim; rows are 2-byte aligned (1-byte at 8
+// bits), so the queries, the gather and the output move single elements.
+template <int D, bool Q8, bool BF, bool GEN, bool ODD>
+__device__ __forceinline__ void prefill_body(const PrefillParams p) {
+  static_assert(!ODD || GEN, "odd head dims run the generic kernels");
   static_assert(!(Q8 && BF), "8-bit K/V dequantizes to fp16");
   constexpr int KB = blocks_per_tile<D>();  // 32-key blocks per tile
   constexpr int kKeys = 32 * KB;            // keys per tile
@@ -245,8 +249,14 @@ __global__ __launch_bounds__(64 * waves_for(D)) void paged_prefill_kernel(const 
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int d = sl * kDW + 16 * c + 8 * hh + 2 * j;
-        const int y = *reinterpret_cast<const int*>(qp + min(d, hd - 2));
-        x[j] = q_live && d < hd ? y : 0;
+        if constexpr (ODD) {
+          const uint16_t* q16 = reinterpret_cast<const uint16_t*>(qp);
+          const uint32_t lo = q16[min(d, hd - 1)], hi = q16[min(d + 1, hd - 1)];
+          x[j] = (int)((q_live && d < hd ? lo : 0u) | (q_live && d + 1 < hd ? hi : 0u) << 16);
+        } else {
+          const int y = *reinterpret_cast<const int*>(qp + min(d, hd - 2));
+          x[j] = q_live && d < hd ? y : 0;
+        }
       }
       qf[c] = __builtin_bit_cast(f16x8, x);
     }
@@ -330,11 +340,45 @@ __global__ __launch_bounds__(64 * waves_for(D)) void paged_prefill_kernel(const 
   // GEN: dim of element pair j of piece i, clamped into the row (pairs past
   // the head dim reload the last pair; trim zeroes them).
   auto pair_dim = [&](int i, int j) { return min(8 * (gp + kTpk * i) + 2 * j, p.head_dim - 2); };
+  // ODD: dim of element e of piece i, clamped into the row (elements past
+  // the head dim reload the last one; trim zeroes them).
+  auto elem_dim = [&](int i, int e) { return min(8 * (gp + kTpk * i) + e, p.head_dim - 1); };
   auto fetch = [&](int page, bool in, int row_off, int scale_off) {
     gok = in && page >= 0 && page < p.arena_pages;
     const uint32_t pg = (uint32_t)(gok ? page : 0);
     const uint64_t at = (uint64_t)pg * (uint64_t)p.page_elems + row_off;
-    if constexpr (GEN && Q8) {
+    if constexpr (ODD && Q8) {
+      const uint8_t* kb = static_cast<const uint8_t*>(p.k) + at;
+      const uint8_t* vb = static_cast<const uint8_t*>(p.v) + at;
+#pragma unroll
+      for (int i = 0; i < kPieces; ++i) {
+        uint32_t kw[2] = {0u, 0u}, vw[2] = {0u, 0u};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          kw[e / 4] |= (uint32_t)kb[elem_dim(i, e)] << (8 * (e % 4));
+          vw[e / 4] |= (uint32_t)vb[elem_dim(i, e)] << (8 * (e % 4));
+        }
+        kr[i] = uint2{kw[0], kw[1]};
+        vr[i] = uint2{vw[0], vw[1]};
+      }
+      const uint64_t sat = (uint64_t)pg * (uint64_t)p.scale_page + scale_off;
+      ksc = p.kscale[sat];
+      vsc = p.vscale[sat];
+    } else if constexpr (ODD) {
+      const uint16_t* kb = reinterpret_cast<const uint16_t*>(static_cast<const f16*>(p.k) + at);
+      const uint16_t* vb = reinterpret_cast<const uint16_t*>(static_cast<const f16*>(p.v) + at);
+#pragma unroll
+      for (int i = 0; i < kPieces; ++i) {
+        i32x4 kw, vw;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          kw[j] = (int)((uint32_t)kb[elem_dim(i, 2 * j)] | (uint32_t)kb[elem_dim(i, 2 * j + 1)] << 16);
+          vw[j] = (int)((uint32_t)vb[elem_dim(i, 2 * j)] | (uint32_t)vb[elem_dim(i, 2 * j + 1)] << 16);
+        }
+        kr[i] = __builtin_bit_cast(f16x8, kw);
+        vr[i] = __builtin_bit_cast(f16x8, vw);
+      }
+    } else if constexpr (GEN && Q8) {
       const uint8_t* kb = static_cast<const uint8_t*>(p.k) + at;
       const uint8_t* vb = static_cast<const uint8_t*>(p.v) + at;
 #pragma unroll
@@ -402,7 +446,10 @@ __global__ __launch_bounds__(64 * waves_for(D)) void paged_prefill_kernel(const 
       (void)scale;
       y = x;
     }
-    if constexpr (GEN) {  // zero the pairs past the head dim
+    if constexpr (ODD) {  // zero the elements past the head dim
+#pragma unroll
+      for (int e = 0; e < 8; ++e) y[e] = 8 * (gp + kTpk * i) + e < p.head_dim ? y[e] : (f16)0.0f;
+    } else if constexpr (GEN) {  // zero the pairs past the head dim
       i32x4 w4 = __builtin_bit_cast(i32x4, y);
 #pragma unroll
       for (int j = 0; j < 4; ++j) w4[j] = 8 * (gp + kTpk * i) + 2 * j < p.head_dim ? w4[j] : 0;
@@ -678,6 +725,19 @@ __global__ __launch_bounds__(64 * waves_for(D)) void paged_prefill_kernel(const 
     return;
   }
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+  if constexpr (ODD) {
+    // Rows of an odd number of elements: one element per store.
+    const int hd = p.head_dim;
+    f16* dst = p.out + ((int64_t)qi * p.hq + h) * hd;
+#pragma unroll
+    for (int b = 0; b < kDW / 32; ++b)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int d = sl * kDW + 32 * b + 8 * (v / 4) + 4 * hh + v % 4;
+        if (d < hd) dst[d] = round16<BF>(o[b][v] * inv);
+      }
+    return;
+  }
   if constexpr (GEN) {
     // Rows of head_dim elements: element pairs, the real dims only.
     const int hd = p.head_dim;
@@ -710,12 +770,27 @@ __global__ __launch_bounds__(64 * waves_for(D)) void paged_prefill_kernel(const 
   }
 }
 
+// The prefill kernel of every even head dim (template arguments as
+// prefill_body's).
+template <int D, bool Q8, bool BF, bool GEN>
+__global__ __launch_bounds__(64 * waves_for(D)) void paged_prefill_kernel(const PrefillParams p) {
+  prefill_body<D, Q8, BF, GEN, false>(p);
+}
+
+// Odd head dims (the reference's portable attention takes any): the generic
+// kernel of width D with element-wise queries, gather and output.
+template <int D, bool Q8, bool BF>
+__global__ __launch_bounds__(64 * waves_for(D)) void paged_prefill_odd_kernel(const PrefillParams p) {
+  prefill_body<D, Q8, BF, true, true>(p);
+}
+
 // Merge of the key ranges of a split prefill: for each (query, head),
 // M = max_s m_s, w_s = 2^(m_s - M) (0 for an empty range), out =
 // sum_s w_s o_s / sum_s w_s l_s (0 when nothing was visible). The same LSE
 // merge as the reference's decode merge (metal_kernels.py:103-124), in the
 // log2 domain. One thread per 4 dims, D / 4 threads per (query, head).
-// GEN: output rows of hd (even, below D) elements; partials stay D wide.
+// GEN: output rows of hd (below D) elements, written one element at a time
+// (an odd hd leaves rows 2-byte aligned); partials stay D wide.
 template <int D, bool BF, bool GEN>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restrict__ part_o,
                                                             const float2* __restrict__ part_ml,
@@ -749,8 +824,9 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restr
              round16<BF>(acc.w * inv)};
   if constexpr (GEN) {
     f16* row = out + pair * hd;
-    if (d < hd) *reinterpret_cast<f16x2*>(row + d) = f16x2{y[0], y[1]};
-    if (d + 2 < hd) *reinterpret_cast<f16x2*>(row + d + 2) = f16x2{y[2], y[3]};
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (d + j < hd) row[d + j] = y[j];
   } else {
     (void)hd;
     *reinterpret_cast<f16x4*>(out + pair * D + d) = y;
@@ -800,10 +876,10 @@ using pda_internal::fail;
 using pda_internal::ok;
 
 // The kernel width serving a head dim: the head dim itself when a kernel
-// has it, else the next wider one (GEN kernels); 0 for head dims the
-// library does not serve (odd, or above 512).
+// has it, else the next wider one (GEN kernels; odd head dims the odd
+// kernels); 0 for head dims the library does not serve (above 512).
 int prefill_dim(int head_dim) {
-  if (head_dim < 2 || head_dim > 512 || (head_dim & 1)) return 0;
+  if (head_dim < 1 || head_dim > 512) return 0;
   for (int d : {64, 96, 128, 256, 512})
     if (head_dim <= d) return d;
   return 0;
@@ -819,7 +895,17 @@ const void* prefill_kernel_for(int kdim) {
 }
 
 template <bool Q8, bool BF>
-const void* prefill_kernel_for(int kdim, bool gen) {
+const void* prefill_odd_kernel_for(int kdim) {
+  return kdim == 64    ? reinterpret_cast<const void*>(paged_prefill_odd_kernel<64, Q8, BF>)
+         : kdim == 96  ? reinterpret_cast<const void*>(paged_prefill_odd_kernel<96, Q8, BF>)
+         : kdim == 128 ? reinterpret_cast<const void*>(paged_prefill_odd_kernel<128, Q8, BF>)
+         : kdim == 256 ? reinterpret_cast<const void*>(paged_prefill_odd_kernel<256, Q8, BF>)
+                       : reinterpret_cast<const void*>(paged_prefill_odd_kernel<512, Q8, BF>);
+}
+
+template <bool Q8, bool BF>
+const void* prefill_kernel_for(int kdim, bool gen, bool odd) {
+  if (odd) return prefill_odd_kernel_for<Q8, BF>(kdim);
   return gen ? prefill_kernel_for<Q8, BF, true>(kdim) : prefill_kernel_for<Q8, BF, false>(kdim);
 }
 
@@ -854,9 +940,9 @@ int prefill(const void* queries, const void* keys, const void* values, const voi
     return fail(PDA_ERR_HEAD_RATIO, "query heads must be a multiple of kv heads");
   const int kdim = prefill_dim(head_dim);
   if (kdim == 0)
-    return fail(PDA_ERR_HEAD_DIM, "head_dim %d: prefill serves even head dims 2..512",
-                head_dim);
+    return fail(PDA_ERR_HEAD_DIM, "head_dim %d: prefill serves head dims 1..512", head_dim);
   const bool gen = kdim != head_dim;
+  const bool odd = head_dim & 1;
   if (count == 0) return ok();
   if (table_len == 0)
     return fail(PDA_ERR_INVALID_ARGUMENT, "an empty page table holds no keys of the chunk");
@@ -941,9 +1027,9 @@ int prefill(const void* queries, const void* keys, const void* values, const voi
   prm.cap_in = softcap > 0.0f ? 2.0f * kLog2e * scale / softcap : 0.0f;
   prm.cap_out = softcap * kLog2e;
   void* args[] = {&prm};
-  const void* fn = q8 ? prefill_kernel_for<true, false>(kdim, gen)
-                  : bf16_elems ? prefill_kernel_for<false, true>(kdim, gen)
-                               : prefill_kernel_for<false, false>(kdim, gen);
+  const void* fn = q8 ? prefill_kernel_for<true, false>(kdim, gen, odd)
+                  : bf16_elems ? prefill_kernel_for<false, true>(kdim, gen, odd)
+                               : prefill_kernel_for<false, false>(kdim, gen, odd);
   const hipStream_t hs = static_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)((int64_t)prm.tiles * q_heads * nsplit));
   hipError_t err = hipLaunchKernel(fn, grid, dim3(64 * waves_for(kdim)), args, 0, hs);
@@ -980,8 +1066,7 @@ int pda_prefill_workspace_bytes(int32_t start, int32_t count, int32_t q_heads,
                 count, start, q_heads, window, splits);
   const int kdim = prefill_dim(head_dim);
   if (kdim == 0)
-    return fail(PDA_ERR_HEAD_DIM, "head_dim %d: prefill serves even head dims 2..512",
-                head_dim);
+    return fail(PDA_ERR_HEAD_DIM, "head_dim %d: prefill serves head dims 1..512", head_dim);
   const int s = count == 0 ? 1 : prefill_splits(start, count, q_heads, kdim, window, splits);
   if (splits_used) *splits_used = s;
   *bytes = prefill_workspace(s, count, q_heads, kdim);

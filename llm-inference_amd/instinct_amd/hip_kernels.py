@@ -163,7 +163,7 @@ def paged_decode_attention(
     ``PDA_DECODE_RACING``: the two waves that share a stretch of pages split
     it wherever they meet (the faster takes more), so the last bits of a
     sequence's output can differ from call to call (within the parity bar).
-    Any even ``head_dim`` up to 512 and any ``page_size`` are accepted, as by
+    Any ``head_dim`` up to 512 and any ``page_size`` are accepted, as by
     the reference op (metal_kernels.py:28-30,204).
 
     ``scales`` = (key_scales, value_scales) selects 8-bit K/V

@@ -159,7 +159,7 @@ void decode_validation(bool may_reach_hip) {
         {[](DecodeArgs& a) { a.batch = -1; }, PDA_ERR_INVALID_ARGUMENT},
         {[](DecodeArgs& a) { a.batch = 9000; }, PDA_ERR_INVALID_ARGUMENT},
         {[](DecodeArgs& a) { a.hq = 30; }, PDA_ERR_HEAD_RATIO},
-        {[](DecodeArgs& a) { a.d = 7; }, PDA_ERR_HEAD_DIM},
+        {[](DecodeArgs& a) { a.d = 513; }, PDA_ERR_HEAD_DIM},
         {[](DecodeArgs& a) { a.d = 514; }, PDA_ERR_HEAD_DIM},
         {[](DecodeArgs& a) { a.page = 0; }, PDA_ERR_INVALID_ARGUMENT},
         {[](DecodeArgs& a) { a.layout = 2; }, PDA_ERR_INVALID_ARGUMENT},
@@ -245,7 +245,7 @@ void prefill_validation(bool may_reach_hip) {
     EXPECT(call(0, 28, 128, 16, 0, nullptr, 0, nullptr, 0, nullptr) == PDA_OK);
     EXPECT(call(-1, 28, 128, 16, 0, nullptr, 0, buf(), 0, nullptr) == PDA_ERR_INVALID_ARGUMENT);
     EXPECT(call(10, 30, 128, 16, 0, nullptr, 0, buf(), 0, nullptr) == PDA_ERR_HEAD_RATIO);
-    EXPECT(call(10, 28, 81, 16, 0, nullptr, 0, buf(), 0, nullptr) == PDA_ERR_HEAD_DIM);
+    EXPECT(call(10, 28, 513, 16, 0, nullptr, 0, buf(), 0, nullptr) == PDA_ERR_HEAD_DIM);
     EXPECT(call(10, 28, 0, 16, 0, nullptr, 0, buf(), 0, nullptr) == PDA_ERR_HEAD_DIM);
     EXPECT(call(10, 28, 128, 0, 0, nullptr, 0, buf(), 0, nullptr) == PDA_ERR_INVALID_ARGUMENT);
     EXPECT(call(10, 28, 128, 16, 4, nullptr, 0, buf(), 0, nullptr) == PDA_ERR_WORKSPACE);
@@ -291,7 +291,7 @@ void append_and_pack_validation(bool may_reach_hip) {
 
 void last_error_is_per_thread() {
   DecodeArgs a;
-  a.d = 7;
+  a.d = 513;
   EXPECT(a.call(pda_paged_decode_attention) == PDA_ERR_HEAD_DIM);
   const std::string mine = pda_last_error();
   std::string theirs = "unset";

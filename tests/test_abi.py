@@ -44,7 +44,7 @@ def decode(**overrides):
 
 @pytest.mark.parametrize("overrides, code", [
     (dict(q_heads=30), _lib.PDA_ERR_HEAD_RATIO),
-    (dict(head_dim=7), _lib.PDA_ERR_HEAD_DIM),
+    (dict(head_dim=513), _lib.PDA_ERR_HEAD_DIM),
     (dict(head_dim=514), _lib.PDA_ERR_HEAD_DIM),
     (dict(head_dim=0), _lib.PDA_ERR_INVALID_ARGUMENT),
     (dict(flags=4), _lib.PDA_ERR_INVALID_ARGUMENT),
@@ -197,7 +197,7 @@ def prefill(**overrides):
     (dict(splits=4, workspace=FAKE, workspace_bytes=1 << 20), _lib.PDA_ERR_WORKSPACE),
     (dict(splits=4, workspace=FAKE + 16, workspace_bytes=1 << 30), _lib.PDA_ERR_WORKSPACE),
     (dict(q_heads=30), _lib.PDA_ERR_HEAD_RATIO),
-    (dict(head_dim=81), _lib.PDA_ERR_HEAD_DIM),
+    (dict(head_dim=0), _lib.PDA_ERR_HEAD_DIM),
     (dict(head_dim=514), _lib.PDA_ERR_HEAD_DIM),
     (dict(start=(1 << 31) - 100), _lib.PDA_ERR_TOO_LONG),
     (dict(out=None), _lib.PDA_ERR_INVALID_ARGUMENT),
@@ -241,10 +241,12 @@ def test_prefill_split_plan():
     assert _lib.prefill_workspace_bytes(0, 100, 8, 64, splits=500)[0] == 64
     assert _lib.prefill_workspace_bytes(0, 0, 8, 64, splits=3) == (1, 0)
     # Head dims without a kernel of their own plan as the next wider kernel.
-    for d, width in ((80, 96), (4, 64), (200, 256), (510, 512), (66, 96), (98, 128)):
+    # Odd head dims too (element-wise kernels of the same widths).
+    for d, width in ((80, 96), (4, 64), (200, 256), (510, 512), (66, 96), (98, 128),
+                     (1, 64), (81, 96), (129, 256), (511, 512)):
         assert _lib.prefill_workspace_bytes(3000, 256, 8, d) == \
             _lib.prefill_workspace_bytes(3000, 256, 8, width)
-    for d in (0, 1, 81, 514, -2):
+    for d in (0, 513, 514, -2):
         with pytest.raises(_lib.PdaError):
             _lib.prefill_workspace_bytes(0, 10, 8, d)
     # 512-wide heads: 64 queries per workgroup, one workgroup per CU. A
@@ -277,7 +279,7 @@ def test_prefill_q8_validation():
     assert call(ks=None) == _lib.PDA_ERR_INVALID_ARGUMENT
     assert call(vs=None) == _lib.PDA_ERR_INVALID_ARGUMENT
     assert call(ks=FAKE + 1) == _lib.PDA_ERR_ALIGNMENT
-    assert call(head_dim=79) == _lib.PDA_ERR_HEAD_DIM
+    assert call(head_dim=513) == _lib.PDA_ERR_HEAD_DIM
     assert call(count=0, ks=None, vs=None) == _lib.PDA_OK
 
 
@@ -339,3 +341,13 @@ def test_describe_validation():
     assert info["split_kernel"] == "paged_decode_kernel<128,8,true,false,true,false>"
     info = _lib.describe(2, 32, 1, 128, 16, 64, 1000, 0)
     assert (info["unit_heads"], info["units_per_kv_head"], info["head_slots"]) == (16, 2, 16)
+    # Odd head dims (the reference's IN_HEAD guard takes any): the padded
+    # generic width, element-wise loads, one query head per unit.
+    for d, bits, bf16, dp in ((7, 16, False, 8), (129, 8, False, 256), (511, 16, True, 512),
+                              (1, 8, True, 8)):
+        info = _lib.describe(2, 8, 2, d, 16, 64, 1000, 0, kv_bits=bits, bf16=bf16)
+        q8, bf = ("true" if bits == 8 else "false"), ("true" if bf16 else "false")
+        assert info["split_kernel"] == f"paged_decode_odd_kernel<{dp},{q8},{bf}>"
+        assert info["merge_kernel"].endswith(f"<{dp},1,{bf},true>")
+        assert (info["unit_heads"], info["units_per_kv_head"], info["head_slots"]) == (1, 4, 1)
+        assert info["generic"] and not info["matrix_cores"]

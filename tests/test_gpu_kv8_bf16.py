@@ -10,8 +10,8 @@ the kernel against float32 attention over ``int8 * scale`` with max-abs
 over oracle/kv8.py's quantization, both pinned on the CPU), at the bf16 bar
 of this build: max-abs 1.6e-2, mean-abs 1.6e-3 (the fp16 bar times bf16's
 8x larger machine epsilon), on the reference's five kernel-test shapes
-(head_dim 512, 256, 80, 4: the matrix-core, VALU and generic kernels) and
-config 2's head shape, in both arena layouts. Two further checks:
+(head_dim 512, 256, 80, 4: the matrix-core, VALU and generic kernels),
+config 2's head shape and an odd head dim (7), in both arena layouts. Two further checks:
 
 * the bf16 call against the fp16 call (pda_paged_decode_attention_q8) on the
   same queries, which bf16 -> fp16 holds exactly at these magnitudes: the
@@ -70,6 +70,7 @@ SHAPES = [
     (8, 1, 80, [3, 300], 0, 30.0),
     (2, 1, 4, [9], 4, 0.0),
     (28, 4, 128, [3, 300, 4095, 8000], 0, 0.0),
+    (8, 2, 7, [3, 300, 1000], 0, 0.0),  # an odd head dim
 ]
 
 

@@ -1,9 +1,9 @@
-"""Prefill at every head dim the decode call takes: any even head_dim up to
-512 (the reference's PrefillBatch attends with whatever head dim the model
-has, batches.py:84-132, and its CUDA test prefills head_dim 4,
+"""Prefill at every head dim the decode call takes: any head_dim up to 512
+(the reference's PrefillBatch attends with whatever head dim the model has,
+batches.py:84-132, and its CUDA test prefills head_dim 4,
 tests/cuda_tests.cu:207-262). Head dims without a kernel of their own run
-the next wider one (64, 96, 128, 256, 512) with the pairs past the head dim
-zero. Checked against the float64 prefill oracle at the north star's fp16
+the next wider one (64, 96, 128, 256, 512) with the elements past the head
+dim zero; odd ones move single elements (paged_prefill_odd_kernel). Checked against the float64 prefill oracle at the north star's fp16
 bar (max-abs 2e-3, mean-abs 2e-4), bf16 at the bar of test_gpu_bf16.py, in
 both arena layouts, with key ranges, windows, softcap, images, 8-bit caches,
 and the reference's closed form at its own page size."""
@@ -70,7 +70,8 @@ def check(c, *, scale, window=0, softcap=0.0, splits=0, images=(), what="", bf16
 
 
 @pytest.mark.parametrize("layout", ["pages", "rows"])
-@pytest.mark.parametrize("d", [2, 4, 36, 48, 80, 100, 112, 160, 200, 320, 510])
+@pytest.mark.parametrize("d", [2, 4, 36, 48, 80, 100, 112, 160, 200, 320, 510,
+                               1, 3, 7, 65, 97, 129, 257, 511])
 def test_generic_head_dims(gpu, layout, d):
     hq, hkv = (12, 4) if d <= 256 else (8, 2)
     c = case(gpu, hq=hq, hkv=hkv, d=d, start=300, count=260, layout=layout, seed=d)
@@ -78,7 +79,7 @@ def test_generic_head_dims(gpu, layout, d):
     check(c, scale=d ** -0.5, splits=3, what=f"D{d} {layout} splits 3")
 
 
-@pytest.mark.parametrize("d", [80, 200])
+@pytest.mark.parametrize("d", [80, 200, 81])
 def test_generic_window_softcap_images(gpu, d):
     c = case(gpu, hq=8, hkv=2, d=d, start=1000, count=300, page=32, seed=40 + d)
     check(c, scale=d ** -0.5, window=100, softcap=30.0, what=f"D{d} window 100 softcap")
@@ -87,16 +88,18 @@ def test_generic_window_softcap_images(gpu, d):
     check(c, scale=d ** -0.5, splits=64, what=f"D{d} splits 64 (empty ranges)")
 
 
+@pytest.mark.parametrize("d", [80, 5])
 @pytest.mark.parametrize("page", [1, 5, 48])
-def test_generic_page_sizes(gpu, page):
-    c = case(gpu, hq=6, hkv=2, d=80, start=123, count=200, page=page, layout="rows",
-             seed=page)
-    check(c, scale=80 ** -0.5, what=f"D80 page {page}")
-    check(c, scale=80 ** -0.5, splits=2, what=f"D80 page {page} splits 2")
+def test_generic_page_sizes(gpu, page, d):
+    c = case(gpu, hq=6, hkv=2, d=d, start=123, count=200, page=page, layout="rows",
+             seed=page + d)
+    check(c, scale=d ** -0.5, what=f"D{d} page {page}")
+    check(c, scale=d ** -0.5, splits=2, what=f"D{d} page {page} splits 2")
 
 
 @pytest.mark.parametrize("layout", ["pages", "rows"])
-@pytest.mark.parametrize("d,splits", [(80, 0), (36, 3), (200, 2), (320, 0)])
+@pytest.mark.parametrize("d,splits", [(80, 0), (36, 3), (200, 2), (320, 0), (7, 0), (129, 3),
+                                      (511, 0)])
 def test_generic_8bit_cache(gpu, layout, d, splits):
     """int8 rows with one fp16 scale per (row, kv head), dequantized as the
     reference's gather does (oracle kv8.gather_dequantize)."""
@@ -129,7 +132,7 @@ def test_generic_8bit_cache(gpu, layout, d, splits):
     assert err_max <= MAX_ABS and err_mean <= MEAN_ABS
 
 
-@pytest.mark.parametrize("d,splits", [(80, 0), (200, 3), (4, 0)])
+@pytest.mark.parametrize("d,splits", [(80, 0), (200, 3), (4, 0), (33, 2), (257, 0)])
 def test_generic_bf16(gpu, d, splits):
     c = case(gpu, hq=8, hkv=2, d=d, start=700, count=200, seed=d, bf16=True)
     check(c, scale=d ** -0.5, splits=splits, bf16=True, what=f"bf16 D{d} splits {splits}")

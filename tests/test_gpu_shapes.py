@@ -184,6 +184,50 @@ def test_generic_head_dims_8bit(gpu, q_heads, kv_heads, head_dim, softcap):
     check8(w, f"8-bit {q_heads}/{kv_heads}/D{head_dim}")
 
 
+# --- odd head dims ---------------------------------------------------------------
+# The reference's IN_HEAD guard takes any head dim (metal_kernels.py:28-30).
+# Odd ones run paged_decode_odd_kernel: rows 2-byte aligned (1-byte at 8
+# bits), element-wise loads and stores, one query head per unit.
+
+ODD = [  # q_heads, kv_heads, head_dim
+    (2, 1, 1), (4, 2, 3), (7, 1, 5), (8, 2, 7), (14, 2, 33), (5, 5, 63), (8, 1, 129),
+    (4, 2, 255), (2, 2, 511), (6, 3, 97),
+]
+
+
+@pytest.mark.parametrize("q_heads,kv_heads,head_dim", ODD)
+def test_odd_head_dims(gpu, q_heads, kv_heads, head_dim):
+    w = make(gpu, q_heads=q_heads, kv_heads=kv_heads, head_dim=head_dim, page=16,
+             lengths=[1, 17, 300, 1234, 31], seed=head_dim)
+    check16(w, f"odd {q_heads}/{kv_heads}/D{head_dim}")
+    check16(w, f"odd {q_heads}/{kv_heads}/D{head_dim} split2", split_pages=2)
+
+
+@pytest.mark.parametrize("q_heads,kv_heads,head_dim,page,window,softcap", [
+    (8, 2, 7, 5, 40, 0.0), (4, 1, 33, 12, 0, 20.0), (6, 2, 129, 1, 300, 0.0),
+    (2, 2, 511, 24, 0, 5.0)])
+def test_odd_head_dims_pages_window_softcap(gpu, q_heads, kv_heads, head_dim, page, window,
+                                           softcap):
+    w = make(gpu, q_heads=q_heads, kv_heads=kv_heads, head_dim=head_dim, page=page,
+             lengths=[5, 999, 2100, 64], window=window, softcap=softcap, seed=3 * head_dim)
+    check16(w, f"odd D{head_dim} P{page} window={window} softcap={softcap}")
+
+
+@pytest.mark.parametrize("head_dim", [1, 7, 63, 129, 511])
+def test_odd_head_dims_bf16(gpu, head_dim):
+    w = make(gpu, q_heads=8, kv_heads=2, head_dim=head_dim, page=16,
+             lengths=[3, 700, 1500], seed=5 * head_dim)
+    check_bf16(w.to_layout("pages"), f"bf16 odd D{head_dim}")
+
+
+@pytest.mark.parametrize("q_heads,kv_heads,head_dim,softcap", [
+    (2, 1, 1, 0.0), (8, 1, 7, 30.0), (6, 2, 65, 0.0), (4, 2, 255, 0.0), (2, 1, 511, 0.0)])
+def test_odd_head_dims_8bit(gpu, q_heads, kv_heads, head_dim, softcap):
+    w = make(gpu, q_heads=q_heads, kv_heads=kv_heads, head_dim=head_dim, page=16,
+             lengths=[3, 300, 1800, 17], softcap=softcap, seed=7 * head_dim)
+    check8(w, f"8-bit odd {q_heads}/{kv_heads}/D{head_dim}")
+
+
 # --- any page size --------------------------------------------------------------
 
 @pytest.mark.parametrize("page", [1, 2, 4, 5, 12, 24, 40])
