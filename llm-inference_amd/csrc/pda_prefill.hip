@@ -666,7 +666,25 @@ __device__ __forceinline__ void prefill_body(const PrefillParams p) {
       // While every key so far is masked, m is -inf and so is every x.
       const float mu = m == -INFINITY ? 0.0f : m;
       // P^T as the B operand: 16-key step ks holds values 8 ks .. 8 ks + 7,
-      // i.e. keys 16 ks + 8 (t / 4) + 4 hh + t % 4.
+      // i.e. keys 16 ks + 8 (t / 4) + 4 hh + t % 4. O^T += V^T P^T, A
+      // operand of step ks for rows 32 b ..: keys 16 ks + 4 hh + 0..3 (first
+      // read) and + 8 (second read). The 512-wide kernels issue each step's
+      // products as soon as its probabilities exist, so that the matrix
+      // core works while the next step's exps run (1.6-2.5% faster there;
+      // at D <= 256, 1-2% slower than all exps first); the accumulation
+      // order per output block is the same either way.
+      constexpr bool kInterleave = kSlices > 1;
+      auto pv_step = [&](int ks, const f16x8& pk) {
+#pragma unroll
+        for (int b = 0; b < kDW / 32; ++b) {
+          const f16* vp = sv + v_lane + 16 * ks * kVRow + 32 * b;
+          const f16x4 lo4 = read_tr(vp);
+          const f16x4 hi4 = read_tr(vp + 8 * kVRow);
+          const f16x8 a = {lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+          o[b] = mfma16<BF>(a, pk, o[b]);
+        }
+      };
+      if constexpr (kInterleave) __builtin_amdgcn_s_setprio(1);
       f16x8 pb[2 * KB];
 #pragma unroll
       for (int ks = 0; ks < 2 * KB; ++ks) {
@@ -687,19 +705,20 @@ __device__ __forceinline__ void prefill_body(const PrefillParams p) {
             pb[ks][2 * t2 + 1] = ph[1];
           }
         }
+        if constexpr (kInterleave) pv_step(ks, pb[ks]);
       }
-      // O^T += V^T P^T. A operand of step ks for rows 32 b ..: keys
-      // 16 ks + 4 hh + 0..3 (first read) and + 8 (second read).
-      __builtin_amdgcn_s_setprio(1);
+      if constexpr (!kInterleave) {
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-      for (int b = 0; b < kDW / 32; ++b) {
+        for (int b = 0; b < kDW / 32; ++b) {
 #pragma unroll
-        for (int ks = 0; ks < 2 * KB; ++ks) {
-          const f16* vp = sv + v_lane + 16 * ks * kVRow + 32 * b;
-          const f16x4 lo4 = read_tr(vp);
-          const f16x4 hi4 = read_tr(vp + 8 * kVRow);
-          const f16x8 a = {lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
-          o[b] = mfma16<BF>(a, pb[ks], o[b]);
+          for (int ks = 0; ks < 2 * KB; ++ks) {
+            const f16* vp = sv + v_lane + 16 * ks * kVRow + 32 * b;
+            const f16x4 lo4 = read_tr(vp);
+            const f16x4 hi4 = read_tr(vp + 8 * kVRow);
+            const f16x8 a = {lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+            o[b] = mfma16<BF>(a, pb[ks], o[b]);
+          }
         }
       }
       __builtin_amdgcn_s_setprio(0);
