@@ -98,6 +98,7 @@ struct Params {
   int32_t min_pages;  // fewest pages per wave before the stream uses fewer pairs
   int32_t fixed;      // 1: each wave of a pair takes a fixed half of the range
   int32_t balance;    // fixed mode: the wave that is behind its partner raises its priority
+  int32_t front256;   // fixed mode: the first wave's share of its pair's range, in 256ths
   int32_t ragged;     // 1: page_size is not a multiple of the keys per step
   int32_t local;      // 1: one workgroup per unit, its pieces merged in LDS (no merge pass)
   float scale_log2;   // scale * log2(e)
@@ -346,6 +347,12 @@ __device__ __forceinline__ int stream_pairs(int64_t total, const Params& p) {
   return (int)min<int64_t>(want, p.grid_pairs);
 }
 
+// Fixed split points: pages of a pair's range of n pages that its first
+// wave takes (both kernels agree).
+__device__ __forceinline__ int fixed_front(int64_t n, const Params& p) {
+  return (int)(n * p.front256 >> 8);
+}
+
 // First page of pair q's range, and the pair whose range holds page x.
 __device__ __forceinline__ int64_t range_start(int q, int64_t total, int pairs) {
   return (int64_t)q * total / pairs;
@@ -530,7 +537,8 @@ __device__ __forceinline__ void split_body(const Params p) {
   // that is behind its partner (in fractions of their halves, as seen one
   // page earlier) raises its issue priority (s_setprio 1), the other lowers
   // it; this moves only timing, never a cut point.
-  const int quota = p.fixed ? (back ? n_range - n_range / 2 : n_range / 2) : n_range;
+  const int front_pages = fixed_front(n_range, p);
+  const int quota = p.fixed ? (back ? n_range - front_pages : front_pages) : n_range;
   const int partner_quota = n_range - quota;
   const int partner = back ? w - kWgPairs : w + kWgPairs;
   int own_tickets = 0;
@@ -1595,7 +1603,7 @@ struct UnitPieces {
     const int64_t Xn = range_start(q + 1, total, pairs);
     // Fixed split: the first wave took the first half (no load, so the
     // merge saves a dependent trip).
-    const int64_t M = X + (p.fixed ? (Xn - X) / 2 : p.meet[q]);
+    const int64_t M = X + (p.fixed ? fixed_front(Xn - X, p) : p.meet[q]);
     if ((j & 1) == 0)
       return X < M && X < e && M > s ? 2 * (2 * q) + (X >= s ? 0 : 1) : -1;
     return M < Xn && M < e && Xn > s ? 2 * (2 * q + 1) + (M >= s ? 0 : 1) : -1;

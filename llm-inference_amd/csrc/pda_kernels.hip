@@ -620,11 +620,30 @@ int decode(int passes, const void* queries, const void* keys, const void* values
   prm.grid_pairs = groups * wg_pairs;
   prm.min_pages = pl.min_pages;
   prm.fixed = (flags & PDA_DECODE_RACING) ? 0 : 1;
-  static const int balance = [] {
+  // Fixed split points: how a pair's range is cut between its two waves,
+  // and whether the wave that falls behind raises its issue priority. The
+  // SIMD's arbiter favours the older (first) wave of a pair; racing pairs
+  // meet at ~2/3 of the range on config 2's 16-bit matrix-core kernel and at
+  // ~55% on the 8-bit kernels (configs 2 and 5). 16-bit: equal halves with
+  // the priority steering (which keeps the pair's throughput: 112.2 vs 111.4
+  // us racing on config 2). 8-bit: the steering costs a fifth of the pair's
+  // throughput (the 8-bit kernel's issue mix runs slower when the priority
+  // flips), so it is off and the first wave takes 142/256 of the range
+  // (config 2: 87.3 -> 76.6 us, racing 75.7; config 5: 1235 -> 1055 us,
+  // racing 1032). Four-wave workgroups put a pair on two SIMDs: halves.
+  // PDA_FIXED_BALANCE=0/1 and PDA_FIXED_SHARE=1..255 override both
+  // (measurement knobs).
+  static const int balance_env = [] {
     const char* e = getenv("PDA_FIXED_BALANCE");
-    return e && *e ? atoi(e) : 1;
+    return e && *e ? atoi(e) : -1;
   }();
-  prm.balance = balance;
+  static const int share_env = [] {
+    const char* e = getenv("PDA_FIXED_SHARE");
+    return e && *e ? std::min(255, std::max(1, atoi(e))) : 0;
+  }();
+  const bool eight_waves = kp.split_waves == 8;
+  prm.balance = balance_env >= 0 ? balance_env : (q8 ? 0 : 1);
+  prm.front256 = share_env > 0 ? share_env : (q8 && eight_waves ? 142 : 128);
   const size_t lds_local = lp.lds_local;
   prm.local = lds_local > 0 ? 1 : 0;
   prm.ragged = page_size % (pl.mf ? 16 : keys_per_step(head_dim, q8)) ? 1 : 0;
