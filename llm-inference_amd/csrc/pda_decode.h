@@ -470,6 +470,17 @@ __device__ __forceinline__ void split_body(const Params p) {
   const int hd = GEN ? p.head_dim : D;
   constexpr int kElem = Q8 ? 1 : 2;  // bytes per K/V element
 
+  // Local mode: the unit of this workgroup. The p.nhg units of one kv head
+  // (head groups reading the same K/V) go to one XCD (workgroups go round
+  // robin over the 8 XCDs), so that the XCD's L2 serves their reads.
+  int lx = blockIdx.x;
+  if (p.local && p.nhg > 1) {
+    const int full = (int)(gridDim.x / p.nhg) / 8 * 8;
+    if (lx < full * p.nhg) {
+      const int xc = lx % 8, j = lx / 8;
+      lx = ((j / p.nhg) * 8 + xc) * p.nhg + j % p.nhg;
+    }
+  }
   if (tid < kWgPairs) s_ticket[tid] = 0;
   if (tid < kWaves) s_prog[tid] = 0;
   build_prefix<kThreads>(p, s_prefix, s_len);  // ends with a barrier
@@ -506,10 +517,10 @@ __device__ __forceinline__ void split_body(const Params p) {
   int64_t x0;
   int n_range;
   if (p.local) {
-    const int ub = blockIdx.x / nkvg;
+    const int ub = lx / nkvg;
     const int unpg = s_prefix[ub + 1] - s_prefix[ub];
     if (unpg == 0) return;  // the whole workgroup: zeroed above
-    const int64_t us = (int64_t)s_prefix[ub] * nkvg + (int64_t)(blockIdx.x - ub * nkvg) * unpg;
+    const int64_t us = (int64_t)s_prefix[ub] * nkvg + (int64_t)(lx - ub * nkvg) * unpg;
     x0 = us + (int64_t)unpg * pl / kWgPairs;
     n_range = (int)(us + (int64_t)unpg * (pl + 1) / kWgPairs - x0);
     if (lane < hpu_k) s_lml[w * hpu_k + lane] = make_float2(-INFINITY, 0.0f);
@@ -1537,8 +1548,8 @@ __device__ __forceinline__ void split_body(const Params p) {
   // log-sum-exp merge as the merge kernel (metal_kernels.py:103-124), waves
   // folded in a fixed order.
   __syncthreads();
-  const int ub = blockIdx.x / nkvg;
-  const int ukvg = blockIdx.x - ub * nkvg;
+  const int ub = lx / nkvg;
+  const int ukvg = lx - ub * nkvg;
   const int ukvh = ukvg / p.nhg;
   const int uh0 = ukvh * p.gtot + (ukvg - ukvh * p.nhg) * hpu_k;
   for (int i = tid; i < hpu_k * D; i += kThreads) {

@@ -477,7 +477,7 @@ struct LaunchPlan {
   MergeShape ms{false, 1, 1};
 };
 
-int plan_launch(const Plan& pl, int32_t batch, int32_t kv_heads, int32_t head_dim,
+int plan_launch(Plan& pl, int32_t batch, int32_t kv_heads, int32_t head_dim,
                 int32_t page_size, bool q8, bool bf16, bool need_device, LaunchPlan* out) {
   LaunchPlan lp;
   lp.kp = pl.mf ? (head_dim == 512 ? kernels_mf512(q8, bf16)
@@ -495,6 +495,31 @@ int plan_launch(const Plan& pl, int32_t batch, int32_t kv_heads, int32_t head_di
   lp.dim = pl.mf ? head_dim : kernel_dim(head_dim, q8);
   lp.lds_local = local_lds(pl, batch, kv_heads, lp.dim, q8 ? 1 : 2, page_size,
                            lp.kp.split_waves, lp.kp.ring, grid_pairs);
+  // Local mode on the VALU kernels, when a unit per GQA group leaves CUs
+  // idle: a unit per query head, as long as the units still fit one
+  // workgroup per resident slot. The units of one kv head read the same
+  // K/V; the split kernel puts them on one XCD, whose L2 serves the repeat
+  // reads (config 4: 128 -> 256 workgroups, 37.1 -> 35.6 us between events,
+  // bitwise the same output). PDA_LOCAL_HEAD_UNITS=0 keeps the GQA units
+  // (a measurement knob).
+  static const int head_units_env = [] {
+    const char* e = getenv("PDA_LOCAL_HEAD_UNITS");
+    return e && *e ? atoi(e) : -1;
+  }();
+  if (lp.lds_local > 0 && !pl.mf && pl.unit_heads > 1 && head_units_env != 0) {
+    const int64_t units = (int64_t)batch * kv_heads * pl.nhg * pl.unit_heads;
+    const KernelPair k1 = kernels_for(head_dim, 1, q8, bf16);
+    const size_t lds1 = (size_t)pda_decode::local_lds_offset(batch) * sizeof(int32_t) +
+                        (size_t)k1.split_waves * (lp.dim * sizeof(float) + sizeof(float2));
+    if (k1.split && units <= lp.groups && units <= kLocalMaxUnits && lds1 <= kLocalMaxLds) {
+      pl.pages_est *= pl.unit_heads;
+      pl.nhg *= pl.unit_heads;
+      pl.unit_heads = 1;
+      pl.G = 1;
+      lp.kp = k1;
+      lp.lds_local = lds1;
+    }
+  }
   const int heads = kv_heads * pl.nhg * pl.unit_heads;
   lp.ms = merge_shape(pl, lp.dim, grid_pairs, (int64_t)heads * batch);
   *out = lp;

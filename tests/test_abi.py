@@ -300,8 +300,8 @@ DESCRIBED = [
     ((32, 8, 128, 4, 131072, 8192, 0, 16, False),  # config 3, B=4 x 131K
      "paged_decode_kernel<128,4,false,false,false,false>",
      "paged_decode_merge_sliced_kernel<128,4,false,false>"),
-    ((8, 4, 256, 32, 32768, 2048, 1024, 16, False),  # config 4: local mode
-     "paged_decode_kernel<256,2,false,false,false,false>", None),
+    ((8, 4, 256, 32, 32768, 2048, 1024, 16, False),  # config 4: local mode, a unit per head
+     "paged_decode_kernel<256,1,false,false,false,false>", None),
     ((32, 8, 128, 256, 65536, 4096, 0, 16, False),  # config 5
      "paged_decode_kernel<128,4,false,false,false,false>",
      "paged_decode_merge_kernel<128,4,false,false>"),
@@ -341,6 +341,11 @@ def test_describe_validation():
     assert info["split_kernel"] == "paged_decode_kernel<128,8,true,false,true,false>"
     info = _lib.describe(2, 32, 1, 128, 16, 64, 1000, 0)
     assert (info["unit_heads"], info["units_per_kv_head"], info["head_slots"]) == (16, 2, 16)
+    # Local mode on the VALU kernels with CUs to spare: a unit per query head
+    # (config 4: 32 sequences x 4 kv heads x 2 heads = 256 workgroups).
+    info = _lib.describe(32, 8, 4, 256, 16, 2048, 32768, 1024)
+    assert info["local"]
+    assert (info["unit_heads"], info["units_per_kv_head"], info["head_slots"]) == (1, 2, 1)
     # Odd head dims (the reference's IN_HEAD guard takes any): the padded
     # generic width, element-wise loads, one query head per unit.
     for d, bits, bf16, dp in ((7, 16, False, 8), (129, 8, False, 256), (511, 16, True, 512),
