@@ -649,22 +649,25 @@ __device__ __forceinline__ void prefill_body(const PrefillParams p) {
           x[v] = usable_key & (causal | image) ? x[v] : -INFINITY;
         }
       }
-      float top = x[0];
-#pragma unroll
-      for (int v = 1; v < 16 * KB; ++v) top = fmaxf(top, x[v]);
-      top = fmaxf(top, __shfl_xor(top, 32)) * c;  // with the other half of this query's keys
       // Lazy running max: rescale only when a score passes it by 2^8.
-      if (top > m + kSlack) {
-        const float f = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - top);
-        m = top;
-        l *= f;
+      // Returns whether this lane's max moved.
+      auto lazy_max = [&]() -> bool {
+        float top = x[0];
 #pragma unroll
-        for (int b = 0; b < kDW / 32; ++b)
+        for (int v = 1; v < 16 * KB; ++v) top = fmaxf(top, x[v]);
+        top = fmaxf(top, __shfl_xor(top, 32)) * c;  // with the other half of this query's keys
+        if (top > m + kSlack) {
+          const float f = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - top);
+          m = top;
+          l *= f;
 #pragma unroll
-          for (int v = 0; v < 16; ++v) o[b][v] *= f;
-      }
-      // While every key so far is masked, m is -inf and so is every x.
-      const float mu = m == -INFINITY ? 0.0f : m;
+          for (int b = 0; b < kDW / 32; ++b)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) o[b][v] *= f;
+          return true;
+        }
+        return false;
+      };
       // P^T as the B operand: 16-key step ks holds values 8 ks .. 8 ks + 7,
       // i.e. keys 16 ks + 8 (t / 4) + 4 hh + t % 4. O^T += V^T P^T, A
       // operand of step ks for rows 32 b ..: keys 16 ks + 4 hh + 0..3 (first
@@ -684,28 +687,57 @@ __device__ __forceinline__ void prefill_body(const PrefillParams p) {
           o[b] = mfma16<BF>(a, pk, o[b]);
         }
       };
-      if constexpr (kInterleave) __builtin_amdgcn_s_setprio(1);
       f16x8 pb[2 * KB];
+      // The weights exp2(x c - mu) as 16-bit B operands, summed into `sum`
+      // (the 512-wide kernels: each step's products issued as it is done).
+      auto weights = [&](float mu, float& sum) {
 #pragma unroll
-      for (int ks = 0; ks < 2 * KB; ++ks) {
+        for (int ks = 0; ks < 2 * KB; ++ks) {
 #pragma unroll
-        for (int t2 = 0; t2 < 4; ++t2) {
-          if constexpr (BF) {
-            const bf16x2 pp = {(bf16)__builtin_amdgcn_exp2f(fmaf(x[8 * ks + 2 * t2], c, -mu)),
-                               (bf16)__builtin_amdgcn_exp2f(fmaf(x[8 * ks + 2 * t2 + 1], c, -mu))};
-            l = __builtin_amdgcn_fdot2_f32_bf16(pp, bf16x2{(bf16)1.0f, (bf16)1.0f}, l, false);
-            const f16x2 ph = __builtin_bit_cast(f16x2, pp);
-            pb[ks][2 * t2] = ph[0];
-            pb[ks][2 * t2 + 1] = ph[1];
-          } else {
-            const f16x2 ph = {(f16)__builtin_amdgcn_exp2f(fmaf(x[8 * ks + 2 * t2], c, -mu)),
-                              (f16)__builtin_amdgcn_exp2f(fmaf(x[8 * ks + 2 * t2 + 1], c, -mu))};
-            l = __builtin_amdgcn_fdot2(ph, f16x2{(f16)1.0f, (f16)1.0f}, l, false);
-            pb[ks][2 * t2] = ph[0];
-            pb[ks][2 * t2 + 1] = ph[1];
+          for (int t2 = 0; t2 < 4; ++t2) {
+            if constexpr (BF) {
+              const bf16x2 pp = {(bf16)__builtin_amdgcn_exp2f(fmaf(x[8 * ks + 2 * t2], c, -mu)),
+                                 (bf16)__builtin_amdgcn_exp2f(fmaf(x[8 * ks + 2 * t2 + 1], c, -mu))};
+              sum = __builtin_amdgcn_fdot2_f32_bf16(pp, bf16x2{(bf16)1.0f, (bf16)1.0f}, sum, false);
+              const f16x2 ph = __builtin_bit_cast(f16x2, pp);
+              pb[ks][2 * t2] = ph[0];
+              pb[ks][2 * t2 + 1] = ph[1];
+            } else {
+              const f16x2 ph = {(f16)__builtin_amdgcn_exp2f(fmaf(x[8 * ks + 2 * t2], c, -mu)),
+                                (f16)__builtin_amdgcn_exp2f(fmaf(x[8 * ks + 2 * t2 + 1], c, -mu))};
+              sum = __builtin_amdgcn_fdot2(ph, f16x2{(f16)1.0f, (f16)1.0f}, sum, false);
+              pb[ks][2 * t2] = ph[0];
+              pb[ks][2 * t2 + 1] = ph[1];
+            }
+          }
+          if constexpr (kInterleave) pv_step(ks, pb[ks]);
+        }
+      };
+      // Optimistic weights (D = 64, 96 and 256): the weights against the
+      // running max first. A weight past 2^8 (the lazy max's bound, which
+      // keeps 16-bit weights finite) makes the lane's weights sum past 2^8;
+      // only then, or while the lane's max is still -inf (every key so far
+      // masked, or none seen), does the wave take the max, and weigh again
+      // where it moved. The max's reduction chain leaves the common path:
+      // 3-7% faster at D = 64, 2-5% at D = 256, 2% at D = 96 (4096-token
+      // prompt and 512-token chunk at 32256); at D = 128 0-3% slower on
+      // causal prompts, so it keeps the max first.
+      constexpr bool kOptimistic = !kInterleave && D != 128;
+      if constexpr (!kOptimistic) {
+        lazy_max();
+        // While every key so far is masked, m is -inf and so is every x.
+        if constexpr (kInterleave) __builtin_amdgcn_s_setprio(1);
+        weights(m == -INFINITY ? 0.0f : m, l);
+      } else {
+        float lb = 0.0f;
+        weights(m == -INFINITY ? 0.0f : m, lb);
+        if (__ballot(m == -INFINITY || !(lb <= 256.0f)) != 0) {
+          if (__ballot(lazy_max()) != 0) {
+            lb = 0.0f;
+            weights(m == -INFINITY ? 0.0f : m, lb);
           }
         }
-        if constexpr (kInterleave) pv_step(ks, pb[ks]);
+        l += lb;
       }
       if constexpr (!kInterleave) {
         __builtin_amdgcn_s_setprio(1);
