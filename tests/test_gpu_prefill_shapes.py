@@ -138,6 +138,41 @@ def test_generic_bf16(gpu, d, splits):
     check(c, scale=d ** -0.5, splits=splits, bf16=True, what=f"bf16 D{d} splits {splits}")
 
 
+@pytest.mark.parametrize("d", [64, 96, 128, 256, 512])
+def test_running_max_moves_and_far_negative_scores(gpu, d):
+    """Scores that keep outgrowing the running max (key rows scaled up with
+    their position: the lazy max moves again and again mid-chunk, the
+    accumulators rescaled each time) and scores far below zero (every score
+    near -100 in log2 units, where weights taken against a max of zero would
+    all underflow), causal and with a window, against the float64 oracle.
+    Such peaked weights make an output nearly one value row, so the rows
+    are halved: the fp16 rounding of the output stays well inside the bar."""
+    def halve_values(c):
+        c["values"] = (c["values"].astype(np.float32) * 0.5).astype(np.float16)
+        v_dev = rows_to_pages(torch.as_tensor(c["values"], device=gpu), c["page"])
+        c["t"] = (c["t"][0], c["t"][1], v_dev, c["t"][3])
+
+    c = case(gpu, hq=8, hkv=2, d=d, start=300, count=700, seed=5)
+    halve_values(c)
+    rows = c["keys"].shape[0]
+    grow = (1.0 + np.arange(rows, dtype=np.float32) / 96.0)[:, None, None]
+    c["keys"] = (c["keys"].astype(np.float32) * grow).astype(np.float16)
+    q_dev, _, v_dev, table = c["t"]
+    k_dev = rows_to_pages(torch.as_tensor(c["keys"], device=gpu), c["page"])
+    c["t"] = (q_dev, k_dev, v_dev, table)
+    check(c, scale=d ** -0.5, what=f"D{d} growing keys")
+    check(c, scale=d ** -0.5, window=200, splits=3, what=f"D{d} growing keys, window, splits 3")
+    c = case(gpu, hq=8, hkv=2, d=d, start=100, count=500, seed=6)
+    halve_values(c)
+    q, k = c["q"].astype(np.float32), c["keys"].astype(np.float32)
+    q[..., 0], k[..., 0] = 24.0, -24.0
+    c["q"], c["keys"] = q.astype(np.float16), k.astype(np.float16)
+    q_dev = torch.as_tensor(c["q"], device=gpu)
+    k_dev = rows_to_pages(torch.as_tensor(c["keys"], device=gpu), c["page"])
+    c["t"] = (q_dev, k_dev, c["t"][2], c["t"][3])
+    check(c, scale=8.0 * d ** -0.5, what=f"D{d} far negative scores")
+
+
 def test_closed_form_from_cuda_tests(gpu):
     """tests/cuda_tests.cu:207-262 at its own shape: head_dim 4, page size 2,
     tokens 0, 1 in physical page 1 and token 2 in page 0. The prefill of the
