@@ -5,7 +5,9 @@ PDA_DECODE_LOCAL=1 forces it wherever the pieces fit and =0 turns it off;
 the library reads the variable once per process, so each setting runs in a
 child process. Every case is checked against the float64 oracle at the
 north star's bar (bf16: test_gpu_bf16.py's bar; 8-bit: attention over the
-dequantized rows), and the fixed-split mode for bitwise reproducibility."""
+dequantized rows), and the fixed-split mode for bitwise reproducibility.
+On the VALU kernels local mode gives each query head its own unit where the
+CUs have room; those outputs must equal the GQA units' bit for bit."""
 
 import os
 import subprocess
@@ -108,3 +110,53 @@ def test_local_mode_against_the_oracle(gpu, mode):
                        capture_output=True, text=True, timeout=300)
     print(r.stdout)
     assert r.returncode == 0, r.stdout + r.stderr[-3000:]
+
+
+HEADS_CHILD = r"""
+import hashlib
+import torch
+from instinct_amd import workloads
+from instinct_amd.hip_kernels import decode_kernel_names, paged_decode_attention
+
+gpu = torch.device("cuda:0")
+for hq, hkv, d, lengths, window, dtype, seed in (
+        (8, 4, 256, [4100, 5000, 9000], 1024, torch.float16, 3),   # config 4's shape
+        (16, 4, 128, [300, 700, 1000], 0, torch.float16, 4),       # 4 heads per kv head
+        (8, 2, 128, [50, 301], 0, torch.bfloat16, 5),
+        (12, 6, 96, [33, 257, 999], 200, torch.float16, 6),
+        (4, 2, 80, [9, 700], 0, torch.float16, 7)):                # generic head dim
+    w = workloads.reference_test_case(hq, hkv, d, lengths, window, 0.0, device=gpu, seed=seed)
+    w.q, w.keys, w.values = (x.to(dtype) for x in (w.q, w.keys, w.values))
+    w.to_layout("pages")
+    info = decode_kernel_names(hq, hkv, d, bf16=dtype == torch.bfloat16, batch=w.batch,
+                               longest=w.longest, page_size=16,
+                               table_width=int(w.tables.shape[1]), window=window)
+    assert info["local"], info
+    out = paged_decode_attention(w.q, w.keys, w.values, w.tables, w.lengths, page_size=16,
+                                 longest=w.longest, scale=w.scale, window=window)
+    torch.cuda.synchronize()
+    digest = hashlib.sha256(out.view(torch.int16).cpu().numpy().tobytes()).hexdigest()[:16]
+    print(f"{hq}/{hkv}/D{d} {dtype} heads/unit {info['heads_per_unit']} {digest}", flush=True)
+"""
+
+
+def test_local_head_units_match_gqa_units(gpu):
+    # Local mode on the VALU kernels takes a unit per query head where the
+    # CUs have room (PDA_LOCAL_HEAD_UNITS=0 keeps the GQA units). Each head's
+    # arithmetic does not depend on its unit, so both give the same bits.
+    runs = {}
+    for setting in ("", "0"):
+        env = dict(os.environ, PDA_DECODE_LOCAL="1",
+                   PYTHONPATH=os.pathsep.join([str(ROOT), str(ROOT / "llm-inference_amd"),
+                                               os.environ.get("PYTHONPATH", "")]))
+        env.pop("PDA_LOCAL_HEAD_UNITS", None)
+        if setting:
+            env["PDA_LOCAL_HEAD_UNITS"] = setting
+        r = subprocess.run([sys.executable, "-c", HEADS_CHILD], env=env, cwd=ROOT,
+                           capture_output=True, text=True, timeout=300)
+        print(r.stdout)
+        assert r.returncode == 0, r.stdout + r.stderr[-3000:]
+        runs[setting] = [line.split() for line in r.stdout.strip().splitlines()]
+    for heads, gqa in zip(runs[""], runs["0"]):
+        assert heads[-1] == gqa[-1], (heads, gqa)          # the same output bits
+        assert heads[-2] == "1" and gqa[-2] != "1", (heads, gqa)  # the policy took effect
