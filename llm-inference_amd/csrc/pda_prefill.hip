@@ -671,25 +671,9 @@ __device__ __forceinline__ void prefill_body(const PrefillParams p) {
       // P^T as the B operand: 16-key step ks holds values 8 ks .. 8 ks + 7,
       // i.e. keys 16 ks + 8 (t / 4) + 4 hh + t % 4. O^T += V^T P^T, A
       // operand of step ks for rows 32 b ..: keys 16 ks + 4 hh + 0..3 (first
-      // read) and + 8 (second read). The 512-wide kernels issue each step's
-      // products as soon as its probabilities exist, so that the matrix
-      // core works while the next step's exps run (1.6-2.5% faster there;
-      // at D <= 256, 1-2% slower than all exps first); the accumulation
-      // order per output block is the same either way.
-      constexpr bool kInterleave = kSlices > 1;
-      auto pv_step = [&](int ks, const f16x8& pk) {
-#pragma unroll
-        for (int b = 0; b < kDW / 32; ++b) {
-          const f16* vp = sv + v_lane + 16 * ks * kVRow + 32 * b;
-          const f16x4 lo4 = read_tr(vp);
-          const f16x4 hi4 = read_tr(vp + 8 * kVRow);
-          const f16x8 a = {lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
-          o[b] = mfma16<BF>(a, pk, o[b]);
-        }
-      };
+      // read) and + 8 (second read).
       f16x8 pb[2 * KB];
-      // The weights exp2(x c - mu) as 16-bit B operands, summed into `sum`
-      // (the 512-wide kernels: each step's products issued as it is done).
+      // The weights exp2(x c - mu) as 16-bit B operands, summed into `sum`.
       auto weights = [&](float mu, float& sum) {
 #pragma unroll
         for (int ks = 0; ks < 2 * KB; ++ks) {
@@ -710,23 +694,23 @@ __device__ __forceinline__ void prefill_body(const PrefillParams p) {
               pb[ks][2 * t2 + 1] = ph[1];
             }
           }
-          if constexpr (kInterleave) pv_step(ks, pb[ks]);
         }
       };
-      // Optimistic weights (D = 64, 96 and 256): the weights against the
+      // Optimistic weights (every width but 128): the weights against the
       // running max first. A weight past 2^8 (the lazy max's bound, which
       // keeps 16-bit weights finite) makes the lane's weights sum past 2^8;
       // only then, or while the lane's max is still -inf (every key so far
       // masked, or none seen), does the wave take the max, and weigh again
-      // where it moved. The max's reduction chain leaves the common path:
-      // 3-7% faster at D = 64, 2-5% at D = 256, 2% at D = 96 (4096-token
-      // prompt and 512-token chunk at 32256); at D = 128 0-3% slower on
-      // causal prompts, so it keeps the max first.
-      constexpr bool kOptimistic = !kInterleave && D != 128;
+      // where it moved. (At D = 512 the four slices of a query block hold
+      // the same scores, so they decide alike.) The max's reduction chain
+      // leaves the common path: 3-7% faster at D = 64, 2-5% at D = 256, 2%
+      // at D = 96, 1.3-2.4% at D = 512 (there against issuing each 16-key
+      // step's products as soon as its probabilities exist, max first); at
+      // D = 128 0-3% slower on causal prompts, so it keeps the max first.
+      constexpr bool kOptimistic = D != 128;
       if constexpr (!kOptimistic) {
         lazy_max();
         // While every key so far is masked, m is -inf and so is every x.
-        if constexpr (kInterleave) __builtin_amdgcn_s_setprio(1);
         weights(m == -INFINITY ? 0.0f : m, l);
       } else {
         float lb = 0.0f;
@@ -739,18 +723,16 @@ __device__ __forceinline__ void prefill_body(const PrefillParams p) {
         }
         l += lb;
       }
-      if constexpr (!kInterleave) {
-        __builtin_amdgcn_s_setprio(1);
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-        for (int b = 0; b < kDW / 32; ++b) {
+      for (int b = 0; b < kDW / 32; ++b) {
 #pragma unroll
-          for (int ks = 0; ks < 2 * KB; ++ks) {
-            const f16* vp = sv + v_lane + 16 * ks * kVRow + 32 * b;
-            const f16x4 lo4 = read_tr(vp);
-            const f16x4 hi4 = read_tr(vp + 8 * kVRow);
-            const f16x8 a = {lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
-            o[b] = mfma16<BF>(a, pb[ks], o[b]);
-          }
+        for (int ks = 0; ks < 2 * KB; ++ks) {
+          const f16* vp = sv + v_lane + 16 * ks * kVRow + 32 * b;
+          const f16x4 lo4 = read_tr(vp);
+          const f16x4 hi4 = read_tr(vp + 8 * kVRow);
+          const f16x8 a = {lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+          o[b] = mfma16<BF>(a, pb[ks], o[b]);
         }
       }
       __builtin_amdgcn_s_setprio(0);
